@@ -1,0 +1,81 @@
+/*
+ * ishizuki_hip.h — C ABI of libishizuki_hip.so, the MI355X (gfx950) quantized-weight matmul
+ * path of Ishizuki. Plain C: device pointers, sizes, a HIP stream, an int status.
+ *
+ * Each entry point replaces one operation of the reference's Swift kernel API (cited as
+ * path:line under struffl/ishizuki). The reference returns nil to mean "declined, fall back";
+ * here that is ISHZ_DECLINED, returned before anything is launched. Errors the reference would
+ * throw at validation are ISHZ_EINVAL; a failed HIP call is ISHZ_EHIP. ishz_last_error() gives
+ * the reason for the last non-OK status on the calling thread.
+ *
+ * All pointers are device pointers unless stated. Calls are asynchronous on `stream` (a
+ * hipStream_t; NULL = the default stream), never synchronise, and are reentrant: kernels keep no
+ * state between calls. Swift reaches this header through include/module.modulemap.
+ */
+#ifndef ISHIZUKI_HIP_H
+#define ISHIZUKI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *ishz_stream_t; /* hipStream_t */
+
+enum { ISHZ_OK = 0, ISHZ_DECLINED = 1, ISHZ_EINVAL = 2, ISHZ_EHIP = 3 };
+
+/* Element types of activations and outputs. */
+enum { ISHZ_DT_F32 = 0, ISHZ_DT_F16 = 1, ISHZ_DT_BF16 = 2 };
+
+/* GGML storage types, numbered as GGMLType's raw values (Config/GGUFFile.swift:13-43). */
+enum {
+  ISHZ_GGML_Q4_0 = 2,
+  ISHZ_GGML_Q4_K = 12,
+  ISHZ_GGML_Q6_K = 14,
+  ISHZ_GGML_IQ2_XS = 17
+};
+
+/* Reason for the calling thread's last non-OK status (static storage, never NULL). */
+const char *ishz_last_error(void);
+/* ABI version of this library (major * 100 + minor). */
+int ishz_version(void);
+
+/* GGMLType.blockSize / typeSize (Config/GGUFFile.swift:45-80) for the types this library
+   decodes; 0 for any other type. */
+int ishz_ggml_block_size(uint32_t type);
+int ishz_ggml_type_size(uint32_t type);
+
+/* GGMLKernels.matvec (Core/GGMLKernels.swift:177-213): y[M][N] = x[M][K] . W[N][K]^T with W
+   the GGML blocks of `type`, rows of W contiguous, never expanded. x and y are fp16; M in
+   1..16 (matvecBatch, :146). M = 1 runs the streaming GEMV, M >= 2 the MFMA verify kernel.
+   Declines (ISHZ_DECLINED) for an unsupported type or dtype, M outside 1..16, K not a whole
+   number of blocks, N < 1, or blocks_bytes < N * rowBytes (:181-189). */
+int ishz_ggml_matvec(uint32_t type, const void *x, int x_dtype, int M, int K, const void *blocks,
+                     size_t blocks_bytes, int N, void *y, ishz_stream_t stream);
+
+/* GGMLKernels.matmulFew (Core/GGMLKernels.swift:219-253): the same product for M in 2..8
+   (matmulFewRows, :217), 256-element block types only, as the reference. Each weight is decoded
+   once into MFMA operand registers and multiplied against every row. row_blocks is accepted for
+   signature parity and ignored (the tile shape is chosen per shape). */
+int ishz_ggml_matmul_few(uint32_t type, const void *x, int x_dtype, int M, int K,
+                         const void *blocks, size_t blocks_bytes, int N, int row_blocks, void *y,
+                         ishz_stream_t stream);
+
+/* GGMLKernels.dequantize (Core/GGMLKernels.swift:60-97): expand `count` elements of blocks to
+   out (fp32, fp16 or bf16), bit-exact with the CPU definition (Core/GGMLDequant.swift:25). */
+int ishz_ggml_dequant(uint32_t type, const void *blocks, size_t blocks_bytes, size_t count,
+                      void *out, int out_dtype, ishz_stream_t stream);
+
+/* GGMLKernels.gather (Core/GGMLKernels.swift:102-138): rows ids[0..n_ids) of W [n_rows][K]
+   decoded into out [n_ids][K]. An id outside [0, n_rows) yields a row of zeros instead of a
+   read out of bounds. */
+int ishz_ggml_gather(uint32_t type, const int32_t *ids, int n_ids, const void *blocks,
+                     size_t blocks_bytes, int n_rows, int K, void *out, int out_dtype,
+                     ishz_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ISHIZUKI_HIP_H */

@@ -1,0 +1,67 @@
+"""Loads libishizuki_hip.so and declares the C ABI of include/ishizuki_hip.h for ctypes.
+
+The product path has no fallback: if the library is missing, importing a kernel module raises.
+"""
+import ctypes
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libishizuki_hip.so")
+HEADER = os.path.join(HERE, "..", "include", "ishizuki_hip.h")
+
+OK, DECLINED, EINVAL, EHIP = 0, 1, 2, 3
+DT_F32, DT_F16, DT_BF16 = 0, 1, 2
+
+P, I, U32, SZ, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, ctypes.c_size_t, ctypes.c_float
+_SIGS = {
+    "ishz_last_error": (ctypes.c_char_p, []),
+    "ishz_version": (I, []),
+    "ishz_ggml_block_size": (I, [U32]),
+    "ishz_ggml_type_size": (I, [U32]),
+    "ishz_ggml_matvec": (I, [U32, P, I, I, I, P, SZ, I, P, P]),
+    "ishz_ggml_matmul_few": (I, [U32, P, I, I, I, P, SZ, I, I, P, P]),
+    "ishz_ggml_dequant": (I, [U32, P, SZ, SZ, P, I, P]),
+    "ishz_ggml_gather": (I, [U32, P, I, P, SZ, I, I, P, I, P]),
+}
+
+_lib = None
+
+
+class IshzError(RuntimeError):
+    pass
+
+
+def header_symbols():
+    """Function names declared by include/ishizuki_hip.h."""
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(ishz_\w+)\s*\(", text)))
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise IshzError(f"{LIB_PATH} is not built (run __graft_entry__.build())")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name, None)
+            if fn is None:
+                continue
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error():
+    return lib().ishz_last_error().decode()
+
+
+def check(rc, what):
+    """OK -> True, DECLINED -> False (the reference's nil), anything else raises."""
+    if rc == OK:
+        return True
+    if rc == DECLINED:
+        return False
+    raise IshzError(f"{what}: status {rc}: {last_error()}")

@@ -1,0 +1,98 @@
+// Shared device helpers for the gfx950 (CDNA4, wave64) kernels of libishizuki_hip.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/ishizuki_hip.h"
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+#define DEV __device__ __forceinline__
+
+// ---------------------------------------------------------------- loads
+// GGUF blocks are only 2-byte aligned (18, 74 and 210-byte blocks). On amdhsa targets the
+// hardware runs in unaligned mode, so a memcpy from a pointer known to be 2-aligned lowers to
+// one global_load_dwordx{1,2,4}.
+template <int A>
+DEV u4 ld16(const uint8_t *p) {
+  u4 v;
+  __builtin_memcpy(&v, __builtin_assume_aligned(p, A), 16);
+  return v;
+}
+template <int A>
+DEV u2 ld8(const uint8_t *p) {
+  u2 v;
+  __builtin_memcpy(&v, __builtin_assume_aligned(p, A), 8);
+  return v;
+}
+template <int A>
+DEV uint32_t ld4(const uint8_t *p) {
+  uint32_t v;
+  __builtin_memcpy(&v, __builtin_assume_aligned(p, A), 4);
+  return v;
+}
+DEV uint32_t ld2(const uint8_t *p) { return *(const uint16_t *)__builtin_assume_aligned(p, 2); }
+
+// ---------------------------------------------------------------- fp16 bits
+DEV float h2f(uint32_t bits16) { return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16); }
+DEV uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+DEV h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
+DEV uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// Two small unsigned integers held in the low bits of each 16-bit half become exact fp16
+// values by setting the exponent of 1024 above them and subtracting 1024 + bias.
+DEV uint32_t magic(uint32_t halves) { return halves | 0x64006400u; }
+DEV uint32_t unmagic(uint32_t halves, _Float16 off) {
+  return as_u32(as_h2(halves | 0x64006400u) - h2{off, off});
+}
+
+// fp32 += a.lo*b.lo + a.hi*b.hi (v_dot2_f32_f16).
+DEV float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
+}
+
+// ---------------------------------------------------------------- cross-lane sums
+#define ISHZ_DPP(v, ctrl)                                                                  \
+  __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, \
+                                                        0xf, 0xf, true))
+// Sum over aligned groups of W lanes (W = 8, 16, 32, 64); every lane of a group gets the sum.
+template <int W>
+DEV float group_sum(float v) {
+  v += ISHZ_DPP(v, 0xB1);   // quad_perm [1,0,3,2]
+  v += ISHZ_DPP(v, 0x4E);   // quad_perm [2,3,0,1]
+  v += ISHZ_DPP(v, 0x141);  // row_half_mirror: lane j <- 7-j within 8
+  if (W >= 16) v += ISHZ_DPP(v, 0x140);  // row_mirror: lane j <- 15-j within 16
+  if (W >= 32) v += __shfl_xor(v, 16, 64);
+  if (W >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+// ---------------------------------------------------------------- MFMA
+// C[i][j] += sum_k A[i][k] B[k][j], 16x16 fp32 tile. Lane l holds A row l%16 and B column l%16
+// (k slots chosen by l/16; any consistent k order works) and C rows 4*(l/16)+r, column l%16.
+DEV f4 mfma32(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+DEV f4 mfma16(h4 a, h4 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
+DEV h8 as_h8(u4 v) { return __builtin_bit_cast(h8, v); }
+DEV h4 as_h4(u2 v) { return __builtin_bit_cast(h4, v); }
+
+// ---------------------------------------------------------------- host side
+namespace ishz {
+void set_error(const std::string &msg);
+int fail(const char *what, hipError_t e);
+int decline(const std::string &why);
+int einval(const std::string &why);
+inline hipStream_t S(ishz_stream_t s) { return (hipStream_t)s; }
+}  // namespace ishz
+
+#define ISHZ_LAUNCH_CHECK(what)                     \
+  do {                                              \
+    hipError_t _e = hipGetLastError();              \
+    if (_e != hipSuccess) return ishz::fail(what, _e); \
+  } while (0)

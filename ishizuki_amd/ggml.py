@@ -1,0 +1,83 @@
+"""GGMLKernels for MI355X: the reference's quantized GGUF matmul API over libishizuki_hip.
+
+Mirrors Sources/IshizukiKit/Core/GGMLKernels.swift: each call returns a fresh tensor, or None
+when the kernel declines (the reference's nil: unsupported type, rows out of range, K not a whole
+number of blocks, short buffer), so the caller can fall back.
+"""
+import torch
+
+from . import _lib
+from ._torch import DTYPES, TORCH, ptr, require_cuda, stream
+
+Q4_0, Q4_K, Q6_K, IQ2_XS = 2, 12, 14, 17
+SUPPORTED = (Q4_0, Q4_K, Q6_K, IQ2_XS)
+NAMES = {Q4_0: "Q4_0", Q4_K: "Q4_K", Q6_K: "Q6_K", IQ2_XS: "IQ2_XS"}
+
+matvec_batch = range(1, 17)     # GGMLKernels.matvecBatch (:146)
+matmul_few_rows = range(2, 9)   # GGMLKernels.matmulFewRows (:217)
+
+
+def block_size(t):
+    return _lib.lib().ishz_ggml_block_size(t)
+
+
+def type_size(t):
+    return _lib.lib().ishz_ggml_type_size(t)
+
+
+def row_bytes(t, K):
+    return K // block_size(t) * type_size(t)
+
+
+def matvec(x, blocks, type_, output_dim):
+    """GGMLKernels.matvec (Core/GGMLKernels.swift:177): x [M, K] -> [M, N] in x.dtype."""
+    require_cuda(x, blocks)
+    if x.dim() != 2:
+        return None
+    x = x.contiguous()
+    M, K = x.shape
+    y = torch.empty((M, output_dim), dtype=x.dtype, device=x.device)
+    rc = _lib.lib().ishz_ggml_matvec(type_, ptr(x), DTYPES.get(x.dtype, -1), M, K, ptr(blocks),
+                                     blocks.numel() * blocks.element_size(), output_dim, ptr(y),
+                                     stream())
+    return y if _lib.check(rc, "ggml_matvec") else None
+
+
+def matmul_few(x, blocks, type_, output_dim, row_blocks=2):
+    """GGMLKernels.matmulFew (:219): M in 2..8, 256-element blocks."""
+    require_cuda(x, blocks)
+    if x.dim() != 2:
+        return None
+    x = x.contiguous()
+    M, K = x.shape
+    y = torch.empty((M, output_dim), dtype=x.dtype, device=x.device)
+    rc = _lib.lib().ishz_ggml_matmul_few(type_, ptr(x), DTYPES.get(x.dtype, -1), M, K, ptr(blocks),
+                                         blocks.numel() * blocks.element_size(), output_dim,
+                                         row_blocks, ptr(y), stream())
+    return y if _lib.check(rc, "ggml_matmul_few") else None
+
+
+def dequantize(blocks, type_, shape, dtype=torch.bfloat16):
+    """GGMLKernels.dequantize (:60): blocks -> dense array of `shape`."""
+    require_cuda(blocks)
+    count = 1
+    for s in shape:
+        count *= s
+    out = torch.empty(count, dtype=dtype, device=blocks.device)
+    rc = _lib.lib().ishz_ggml_dequant(type_, ptr(blocks), blocks.numel() * blocks.element_size(),
+                                      count, ptr(out), DTYPES.get(dtype, -1), stream())
+    return out.view(*shape) if _lib.check(rc, "ggml_dequant") else None
+
+
+def gather(ids, blocks, type_, input_dim, dtype=torch.bfloat16, rows=None):
+    """GGMLKernels.gather (:102): rows `ids` of W [rows, input_dim] -> [len(ids), input_dim]."""
+    require_cuda(ids, blocks)
+    ids = ids.reshape(-1).to(torch.int32).contiguous()
+    nbytes = blocks.numel() * blocks.element_size()
+    if rows is None:
+        rb = row_bytes(type_, input_dim) if block_size(type_) else 0
+        rows = nbytes // rb if rb else 0
+    out = torch.empty((ids.numel(), input_dim), dtype=dtype, device=blocks.device)
+    rc = _lib.lib().ishz_ggml_gather(type_, ptr(ids), ids.numel(), ptr(blocks), nbytes, rows,
+                                     input_dim, ptr(out), DTYPES.get(dtype, -1), stream())
+    return out if _lib.check(rc, "ggml_gather") else None

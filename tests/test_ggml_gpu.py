@@ -1,0 +1,122 @@
+"""GGML kernels on the GPU vs the CPU oracle, through the C ABI.
+
+Dequant/gather: bit-exact (fp32 bits; fp16/bf16 = the oracle's fp32 rounded once).
+Matmul (GEMV M=1 and MFMA verify M=2..16): max |y - ref| <= 1e-3 * max |ref| on fp16 outputs,
+ref = the oracle's dequantize-then-fp32-dot.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import assert_close, bits_equal
+from ishizuki_amd import ggml, synth
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+TYPES = [ggml.Q4_0, ggml.Q4_K, ggml.Q6_K, ggml.IQ2_XS]
+
+
+def to_bf16_bits(a):
+    u = np.asarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(a)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+@pytest.mark.parametrize("t", [12, 14, 17])
+def test_dequant_golden_bit_exact(golden_ggml, t):
+    b, e = golden_ggml[t]
+    out = ggml.dequantize(torch.from_numpy(b).to(DEV), t, (e.size,), dtype=torch.float32)
+    assert bits_equal(out.cpu().numpy(), e)
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16])
+def test_dequant_synthetic(t, dt):
+    N, K = 37, 1024
+    blk = synth.ggml_blocks(t, N, K, seed=7 + t)
+    ref = oracle.dequant(t, blk, N * K)
+    out = ggml.dequantize(torch.from_numpy(blk).to(DEV), t, (N, K), dtype=dt).cpu()
+    if dt == torch.float32:
+        assert bits_equal(out.numpy().reshape(-1), ref)
+    elif dt == torch.float16:
+        assert np.array_equal(out.numpy().reshape(-1).view(np.uint16), ref.astype(np.float16).view(np.uint16))
+    else:
+        assert np.array_equal(out.view(torch.int16).numpy().reshape(-1).view(np.uint16), to_bf16_bits(ref))
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_gather_exact_and_out_of_range_is_zero(t):
+    N, K = 50, 512
+    blk = synth.ggml_blocks(t, N, K, seed=3)
+    ref = oracle.dequant(t, blk, N * K).reshape(N, K)
+    ids = np.array([3, 49, 0, 3, 17, -1, 50], np.int32)
+    out = ggml.gather(torch.from_numpy(ids).to(DEV), torch.from_numpy(blk).to(DEV), t, K,
+                      dtype=torch.float32).cpu().numpy()
+    assert bits_equal(out[:5], ref[ids[:5]])
+    assert np.all(out[5:] == 0)
+
+
+def run_matvec(t, M, N, K, seed=0, few=False):
+    blk = synth.ggml_blocks(t, N, K, seed=seed)
+    x = synth.fp16_normal((M, K), seed=seed + 1)
+    ref = oracle.ggml_matmul(t, x.astype(np.float32), blk, N)
+    xb = torch.from_numpy(x).to(DEV)
+    wb = torch.from_numpy(blk).to(DEV)
+    y = (ggml.matmul_few if few else ggml.matvec)(xb, wb, t, N)
+    assert y is not None, "kernel declined"
+    return y.float().cpu().numpy(), ref
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("N,K", [(64, 4096), (17, 5120), (1000, 768 * 4), (40, 256 * 3)])
+def test_gemv_m1(t, N, K):
+    if K % synth.BLOCK[t][0]:
+        pytest.skip("K not whole blocks")
+    print(f"gemv type={t} N={N} K={K}", flush=True)
+    y, ref = run_matvec(t, 1, N, K, seed=N + t)
+    assert_close(y, ref, what=f"gemv t={t} N={N} K={K}")
+
+
+def test_gemv_wide_lanes():
+    # units >= 1024 per row: the 32-lanes-per-row variant
+    y, ref = run_matvec(ggml.Q4_0, 1, 48, 32768, seed=5)
+    assert_close(y, ref)
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("M", [2, 3, 5, 8, 16])
+def test_verify_rows(t, M):
+    N, K = 4100, 1024   # N >= 4096: two tiles per workgroup, ragged last tile
+    print(f"verify type={t} M={M}", flush=True)
+    y, ref = run_matvec(t, M, N, K, seed=M + 10 * t)
+    assert_close(y, ref, what=f"verify t={t} M={M}")
+
+
+@pytest.mark.parametrize("t", [ggml.Q4_K, ggml.Q6_K, ggml.IQ2_XS])
+def test_matmul_few_ragged(t):
+    # GGMLKernelTests.matmulFew (:145-175): N = 17, a ragged tile
+    for M in range(2, 9):
+        y, ref = run_matvec(t, M, 17, 512, seed=M, few=True)
+        assert_close(y, ref, what=f"few t={t} M={M}")
+
+
+def test_matvec_rows_agree_with_single_row():
+    # a row's result does not depend on how many rows ride along
+    t, N, K = ggml.Q4_K, 300, 2048
+    blk = torch.from_numpy(synth.ggml_blocks(t, N, K, seed=9)).to(DEV)
+    x = torch.from_numpy(synth.fp16_normal((8, K), seed=10)).to(DEV)
+    y8 = ggml.matvec(x, blk, t, N).float()
+    for m in range(8):
+        y1 = ggml.matvec(x[m:m + 1], blk, t, N).float()
+        assert torch.allclose(y1[0], y8[m], rtol=2e-3, atol=2e-3 * y8[m].abs().max().item())
+
+
+def test_declines_return_none():
+    blk = torch.zeros(144 * 4, dtype=torch.uint8, device=DEV)
+    x = torch.zeros((17, 256), dtype=torch.float16, device=DEV)
+    assert ggml.matvec(x, blk, ggml.Q4_K, 4) is None
+    assert ggml.matvec(x[:1].float(), blk, ggml.Q4_K, 4) is None
+    assert ggml.matvec(x[:1], blk, ggml.Q4_K, 5) is None   # short buffer

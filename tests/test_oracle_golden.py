@@ -1,0 +1,156 @@
+"""The CPU oracle against the reference's own known-answer vectors and closed forms.
+
+ggml_reference.bin is llama.cpp's to_float output for 8 pseudo-random blocks per type
+(the fixture of Tests/IshizukiKitTests/GGMLDequantTests.swift:60-85), NaN == NaN.
+exl3_reference.npz holds exllamav3's reconstructions (EXL3Tests.swift:44-55).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import bits_equal
+
+ALL_TYPES = [0, 1, 30, 10, 12, 14, 19, 29, 16, 17, 22, 18, 21, 23]
+
+
+@pytest.mark.parametrize("t", ALL_TYPES)
+def test_dequant_matches_llama_cpp(golden_ggml, t):
+    b, e = golden_ggml[t]
+    assert bits_equal(oracle.dequant(t, b, e.size), e)
+
+
+def test_golden_covers_every_type(golden_ggml):
+    assert sorted(golden_ggml) == sorted(ALL_TYPES)
+
+
+def test_refusals():
+    # GGMLDequantTests.refusesUnsupported / refusesShortBuffer (:87-105)
+    with pytest.raises(ValueError):
+        oracle.dequant(11, np.zeros(1024, np.uint8), 256)      # Q3_K: no dequantizer
+    with pytest.raises(ValueError):
+        oracle.dequant(17, np.zeros(73, np.uint8), 256)        # short buffer
+    with pytest.raises(ValueError):
+        oracle.dequant(17, np.zeros(1024, np.uint8), 100)      # not whole blocks
+
+
+def test_q4_0_closed_form():
+    # Q4_0 has no reference decoder: pinned by ggml's block definition, element j of a block is
+    # (lo(qs[j]) - 8) * d and element j + 16 is (hi(qs[j]) - 8) * d.
+    blk = np.zeros(18, np.uint8)
+    blk[0:2] = np.array([0.5], np.float16).view(np.uint8)
+    blk[2:] = np.arange(16, dtype=np.uint8) | (np.arange(16, dtype=np.uint8)[::-1] << 4)
+    y = oracle.dequant(2, blk, 32)
+    assert np.array_equal(y[:16], (np.arange(16) - 8) * 0.5)
+    assert np.array_equal(y[16:], (np.arange(16)[::-1] - 8) * 0.5)
+    # every code once, with a subnormal and a negative scale
+    for d in (np.float16(-3.25), np.float16(6e-8)):
+        blk[0:2] = np.array([d], np.float16).view(np.uint8)
+        y = oracle.dequant(2, blk, 32)
+        assert np.array_equal(y[:16], ((np.arange(16) - 8) * np.float32(d)).astype(np.float32))
+
+
+def test_q4_k_matches_brute_force_layout():
+    # One Q4_K block built by hand: scale j = j+1, min j = 2j, nibble pattern known.
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.array([0.25], np.float16).view(np.uint8)
+    blk[2:4] = np.array([0.125], np.float16).view(np.uint8)
+    sc = [1, 2, 3, 4, 5, 6, 7, 8]
+    mn = [0, 2, 4, 6, 8, 10, 12, 14]
+    q = blk[4:16]
+    for j in range(4):
+        q[j] = sc[j] | ((sc[j + 4] >> 4) << 6)
+        q[j + 4] = mn[j] | ((mn[j + 4] >> 4) << 6)
+        q[j + 8] = (sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4)
+    codes = np.random.default_rng(1).integers(0, 16, 256)
+    for jj in range(4):
+        for l in range(32):
+            blk[16 + 32 * jj + l] = codes[64 * jj + l] | (codes[64 * jj + 32 + l] << 4)
+    y = oracle.dequant(12, blk, 256)
+    want = np.array([0.25 * sc[k // 32] * codes[k] - 0.125 * mn[k // 32] for k in range(256)], np.float32)
+    assert np.array_equal(y, want)
+
+
+def test_half_conversions():
+    vals = np.array([0, -0.0, 1, -2.5, 65504, 6e-8, 1e-5, 3.14159, 70000, -1e9], np.float32)
+    for v in vals:
+        assert oracle.lib().ishzo_float_to_half(float(v)) == int(np.float32(v).astype(np.float16).view(np.uint16))
+    for h in range(0, 65536, 7):
+        f = oracle.lib().ishzo_half_to_float(h)
+        ref = float(np.uint16(h).view(np.float16))
+        assert (np.isnan(f) and np.isnan(ref)) or f == ref
+
+
+EXL3_CASES = [("r1c0", 0), ("r2c1", 1), ("r3c2", 2), ("r4c0", 0), ("r5c2", 2), ("r6c1", 1),
+              ("r7c2", 2), ("r8c0", 0), ("r1h5c2", 2), ("r2h5c2", 2), ("r3h5c2", 2)]
+
+
+@pytest.mark.parametrize("name,cb", EXL3_CASES)
+def test_exl3_decode_matches_exllamav3(golden_exl3, name, cb):
+    t = golden_exl3[name + ".trellis"]
+    w = oracle.exl3_dequant(t, t.shape[2] // 8, cb)
+    assert bits_equal(w, golden_exl3[name + ".expected"])
+
+
+@pytest.mark.parametrize("name,cb", [("qwen3", 0), ("qwen38", 2)])
+def test_exl3_projection_reproduces_checkpoint(golden_exl3, name, cb):
+    # EXL3Tests.projectionMatchesCheckpoint (:74-98): rel-L2 < 0.12 vs the original fp16 weight.
+    t = golden_exl3[name + ".trellis"]
+    suh = golden_exl3[name + ".suh"].astype(np.float32)
+    svh = golden_exl3[name + ".svh"].astype(np.float32)
+    ref = golden_exl3[name + ".weight"].astype(np.float32)
+    x = np.random.default_rng(3).standard_normal((12, 128)).astype(np.float16).astype(np.float32)
+    y = oracle.exl3_apply(x, t, suh, svh, t.shape[2] // 8, cb)
+    want = x @ ref
+    err = np.sqrt(((y - want) ** 2).sum() / (want ** 2).sum())
+    assert err < 0.12
+
+
+@pytest.mark.parametrize("block", [2, 8, 128, 512])
+def test_hadamard_closed_form(block):
+    # Sylvester order: H[i][j] = (-1)^popcount(i & j) / sqrt(b); orthonormal and symmetric.
+    eye = np.eye(block, dtype=np.float32)
+    H = oracle.hadamard(eye, block)
+    i = np.arange(block)
+    pc = np.vectorize(lambda v: bin(v).count("1"))(i[:, None] & i[None, :])
+    want = np.where(pc % 2 == 0, 1.0, -1.0) / np.sqrt(block)
+    assert np.allclose(H, want, atol=1e-6)
+    x = np.random.default_rng(0).standard_normal((3, 4 * block)).astype(np.float32)
+    s = np.where(np.random.default_rng(1).integers(0, 2, 4 * block) == 1, 1.0, -1.0).astype(np.float32)
+    y = oracle.hadamard(x, block, s)
+    back = oracle.hadamard(y, block, s, inverse=True)
+    assert np.allclose(back, x, atol=1e-5)
+
+
+def test_affine_closed_form():
+    from ishizuki_amd import synth
+    codes, s, b = synth.affine_pack(8, 256, group=64, seed=2)
+    w = oracle.affine_dequant(codes, s.view(np.uint16), b.view(np.uint16), 8, 256, 2, 64)
+    q = np.stack([(codes[:, k // 16] >> np.uint32(2 * (k % 16))) & 3 for k in range(256)], 1)
+    sf = np.repeat(s.astype(np.float32), 64, 1)
+    assert np.array_equal(w, (sf * q + np.repeat(b.astype(np.float32), 64, 1)).astype(np.float32))
+    assert set(np.unique(q)) <= {0, 1, 2}
+    # {0, 1, 2} -> {-s, 0, +s} exactly
+    assert np.array_equal(np.abs(w[q != 1]), sf[q != 1]) and np.all(w[q == 1] == 0)
+
+
+def test_matmul_fused_agrees_with_expanded():
+    from ishizuki_amd import synth
+    for t, K in ((2, 512), (12, 512), (14, 512), (17, 512)):
+        blk = synth.ggml_blocks(t, 33, K, seed=t)
+        x = np.random.default_rng(0).standard_normal((3, K)).astype(np.float32)
+        a = oracle.ggml_matmul(t, x, blk, 33)
+        f = oracle.ggml_matmul(t, x, blk, 33, fused=True)
+        w = oracle.dequant(t, blk, 33 * K).reshape(33, K)
+        assert np.allclose(a, x @ w.T, rtol=1e-4, atol=1e-4 * np.abs(a).max())
+        assert np.allclose(a, f, rtol=1e-5, atol=1e-5 * np.abs(a).max())
+
+
+def test_moe_route_matches_numpy():
+    logits = np.random.default_rng(5).standard_normal((6, 128)).astype(np.float32)
+    ids, w = oracle.moe_route(logits, 8)
+    p = np.exp(logits - logits.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    order = np.argsort(-p, 1, kind="stable")[:, :8]
+    assert np.array_equal(ids, order)
+    sel = np.take_along_axis(p, order, 1)
+    assert np.allclose(w, sel / sel.sum(1, keepdims=True), rtol=1e-6)
