@@ -53,6 +53,21 @@ DEV uint32_t unmagic(uint32_t halves, _Float16 off) {
   return as_u32(as_h2(halves | 0x64006400u) - h2{off, off});
 }
 
+// (a & mask) | orv in one v_and_or_b32. gfx9 VOP3 encodings take no literal and read one SGPR,
+// so with two constants the compiler splits this into v_and + v_or; keeping orv in a VGPR
+// (see vconst) and the mask in an SGPR makes it one instruction.
+DEV uint32_t and_or(uint32_t a, uint32_t mask, uint32_t orv) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(orv));
+  return r;
+}
+// A constant materialised once into a VGPR the compiler cannot rematerialise per use.
+DEV uint32_t vconst(uint32_t c) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(c));
+  return r;
+}
+
 // fp32 += a.lo*b.lo + a.hi*b.hi (v_dot2_f32_f16).
 DEV float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
@@ -72,6 +87,12 @@ DEV float group_sum(float v) {
   if (W >= 32) v += __shfl_xor(v, 16, 64);
   if (W >= 64) v += __shfl_xor(v, 32, 64);
   return v;
+}
+
+// Value of lane K of each quad (DPP quad_perm [K,K,K,K]).
+template <int K>
+DEV uint32_t quad_bcast(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, K * 0x55, 0xf, 0xf, false);
 }
 
 // ---------------------------------------------------------------- MFMA

@@ -20,13 +20,25 @@
 
 namespace ishz {
 
-// LDS working set of the GEMV kernel.
+// LDS working set of the GEMV kernel. x is stored in the order lanes consume it: a unit reads R
+// 16-byte slots (8 fp16 x each, pair-permuted) and Q sums of 16 x. Slot r of unit u lives at
+// (u / 16) * 16R + r * 16 + u % 16, so the 16 lanes that read slot r of 16 consecutive units in
+// one instruction touch 256 contiguous bytes: every LDS bank once, no conflicts.
 struct GemvShared {
-  const uint32_t *x;     // permuted fp16 x, K/2 dwords
-  const float *xsum;     // sum of x over each aligned 16 (min formats only)
+  uint32_t mg;           // 0x64006400 held in a VGPR (magic exponent for code -> fp16)
+  const u4 *x;
+  const float *xsum;
   const u4 *grid;        // i-quant grid as fp16, permuted like x (IQ2_XS only)
   const u4 *sgn;         // i-quant sign masks for the same order (IQ2_XS only)
+  template <int R>
+  DEV u4 slot(int u, int r) const { return x[(u >> 4) * 16 * R + r * 16 + (u & 15)]; }
+  template <int Q>
+  DEV float sum(int u, int q) const { return xsum[(u >> 4) * 16 * Q + q * 16 + (u & 15)]; }
 };
+
+DEV void unpack(u4 a, u4 b, uint32_t *d) {
+  d[0] = a.x, d[1] = a.y, d[2] = a.z, d[3] = a.w, d[4] = b.x, d[5] = b.y, d[6] = b.z, d[7] = b.w;
+}
 
 // x0..x7 (natural) -> (x0,x2,x1,x3, x4,x6,x5,x7): the order of the nibble/byte pairs below.
 DEV u4 perm0213(u4 a) {
@@ -70,7 +82,12 @@ DEV void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, int &sc, in
 struct FQ4_0 {
   static constexpr uint32_t TYPE = ISHZ_GGML_Q4_0;
   static constexpr int BS = 32, TS = 18, UPB = 1;  // unit: the whole block, 32 weights
-  static constexpr bool XSUM = false, GRID = false;
+  static constexpr int BATCH = 4;  // units per lane per batch (two batches in flight)
+  static constexpr bool XSUM = true, GRID = false;
+  static constexpr int R = 4, Q = 2;  // x slots: lo run k0, k0+8, hi run k0+16, k0+24
+  static DEV int slot_k(int u, int r) { return 32 * u + 8 * r; }
+  static DEV int sum_k(int u, int q) { return 32 * u + 16 * q; }
+  static constexpr int SUM_LEN = 16;
   struct Raw {
     u4 q;
     uint32_t d;
@@ -79,18 +96,23 @@ struct FQ4_0 {
     const uint8_t *p = row + (size_t)u * TS;
     return {ld16<2>(p + 2), ld2(p)};
   }
+  // Low nibbles become 1024 + q and high nibbles 1024 + 16q (masked in place, no shift); the
+  // offsets come back out through the per-16 sums of x.
   static DEV float dot(const Raw &r, int u, const GemvShared &s) {
-    const uint32_t *xl = s.x + u * 16, *xh = xl + 8;
-    uint32_t lo[8], hi[8];
+    uint32_t xl[8], xh[8], lo[8], hi[8];
+    unpack(s.slot<R>(u, 0), s.slot<R>(u, 1), xl);
+    unpack(s.slot<R>(u, 2), s.slot<R>(u, 3), xh);
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-      const uint32_t q = r.q[t];
-      lo[2 * t] = unmagic(q & 0x000F000Fu, 1032);
-      lo[2 * t + 1] = unmagic((q >> 8) & 0x000F000Fu, 1032);
-      hi[2 * t] = unmagic((q >> 4) & 0x000F000Fu, 1032);
-      hi[2 * t + 1] = unmagic((q >> 12) & 0x000F000Fu, 1032);
+      const uint32_t q = r.q[t], q8 = q >> 8;
+      lo[2 * t] = and_or(q, 0x000F000Fu, s.mg);
+      lo[2 * t + 1] = and_or(q8, 0x000F000Fu, s.mg);
+      hi[2 * t] = and_or(q, 0x00F000F0u, s.mg);
+      hi[2 * t + 1] = and_or(q8, 0x00F000F0u, s.mg);
     }
-    return h2f(r.d) * dot8(hi, xh, dot8(lo, xl, 0.0f));
+    const float sl = dot8(lo, xl, 0.0f), sh = dot8(hi, xh, 0.0f);
+    const float xs_l = s.sum<Q>(u, 0), xs_h = s.sum<Q>(u, 1);
+    return h2f(r.d) * ((sl - 1032.0f * xs_l) + (0.0625f * sh - 72.0f * xs_h));
   }
 
   // Verify: one MFMA 16x16x32 per block. Lane group g takes k = 8g..8g+7: lo nibbles of bytes
@@ -124,36 +146,62 @@ struct FQ4_0 {
 // 64jj+l (sub-block 2jj), high nibbles 64jj+32+l (sub-block 2jj+1); w = d*sc*q - dmin*m.
 struct FQ4_K {
   static constexpr uint32_t TYPE = ISHZ_GGML_Q4_K;
-  static constexpr int BS = 256, TS = 144, UPB = 8;  // unit: 16 B of qs, 32 weights
+  static constexpr int BS = 256, TS = 144, UPB = 4;  // unit: 32 B of qs (chunk jj), 64 weights
+  static constexpr int BATCH = 2;
   static constexpr bool XSUM = true, GRID = false;
+  static constexpr int R = 8, Q = 2;  // slots: lo run k0 + 8i (i < 4), hi run k0 + 32 + 8i
+  static DEV int k0_of(int u) { return (u >> 2) * 256 + (u & 3) * 64; }
+  static DEV int slot_k(int u, int r) { return k0_of(u) + 8 * r; }
+  static DEV int sum_k(int u, int q) { return k0_of(u) + 32 * q; }
+  static constexpr int SUM_LEN = 32;
+  // The four lanes of a block (a quad: units are consecutive per lane) each load one dword of
+  // its 16-byte header and share them by quad broadcast, so the header is read once.
   struct Raw {
-    u4 q, h;
+    u4 q0, q1;
+    uint32_t h;
   };
   static DEV Raw load(const uint8_t *row, int u) {
-    const uint8_t *p = row + (size_t)(u >> 3) * TS;
-    return {ld16<16>(p + 16 + 16 * (u & 7)), ld16<16>(p)};
+    const uint8_t *p = row + (size_t)(u >> 2) * TS;
+    const uint8_t *qs = p + 16 + 32 * (u & 3);
+    return {ld16<16>(qs), ld16<16>(qs + 16), ld4<4>(p + 4 * (u & 3))};
   }
+  // Chunk jj: low nibbles of its 32 bytes are sub-block 2jj (weights k0..k0+31), high nibbles
+  // sub-block 2jj+1 (k0+32..k0+63). Low nibbles become 1024 + q, high ones 1024 + 16q, and
+  // with S = sum code * x and X = sum x over the sub-block: sum q x = S - 1024 X, or S/16 - 64 X.
   static DEV float dot(const Raw &r, int u, const GemvShared &s) {
-    const int b = u >> 3, c = u & 7, jj = c >> 1;
-    const int k0 = b * 256 + jj * 64 + (c & 1) * 16;
-    const uint32_t *xl = s.x + k0 / 2, *xh = xl + 16;
-    uint32_t lo[8], hi[8];
+    const int jj = u & 3;
+    uint32_t qw[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    float sl = 0.0f, sh = 0.0f;
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      const uint32_t q = r.q[t];
-      lo[2 * t] = unmagic(q & 0x000F000Fu, 1024);
-      lo[2 * t + 1] = unmagic((q >> 8) & 0x000F000Fu, 1024);
-      hi[2 * t] = unmagic((q >> 4) & 0x000F000Fu, 1024);
-      hi[2 * t + 1] = unmagic((q >> 12) & 0x000F000Fu, 1024);
+    for (int hb = 0; hb < 2; hb++) {
+      uint32_t xl[8], xh[8];
+      unpack(s.slot<R>(u, 2 * hb), s.slot<R>(u, 2 * hb + 1), xl);
+      unpack(s.slot<R>(u, 4 + 2 * hb), s.slot<R>(u, 5 + 2 * hb), xh);
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const uint32_t q = qw[4 * hb + t], q8 = q >> 8;
+        sl = dot2(and_or(q, 0x000F000Fu, s.mg), xl[2 * t], sl);
+        sl = dot2(and_or(q8, 0x000F000Fu, s.mg), xl[2 * t + 1], sl);
+        sh = dot2(and_or(q, 0x00F000F0u, s.mg), xh[2 * t], sh);
+        sh = dot2(and_or(q8, 0x00F000F0u, s.mg), xh[2 * t + 1], sh);
+      }
     }
-    int sc0, m0, sc1, m1;
-    q4k_scale_min(r.h.y, r.h.z, r.h.w, 2 * jj, sc0, m0);
-    q4k_scale_min(r.h.y, r.h.z, r.h.w, 2 * jj + 1, sc1, m1);
-    const float d = h2f(r.h.x & 0xffff), dmin = h2f(r.h.x >> 16);
-    const float sl = dot8(lo, xl, 0.0f), sh = dot8(hi, xh, 0.0f);
-    const float xl16 = s.xsum[k0 / 16], xh16 = s.xsum[k0 / 16 + 2];
-    return (d * (float)sc0) * sl - (dmin * (float)m0) * xl16 + (d * (float)sc1) * sh -
-           (dmin * (float)m1) * xh16;
+    // scales/mins of sub-blocks 2jj, 2jj+1 (GGMLDequant.q4K.scaleMin), branch-free
+    const uint32_t h0 = quad_bcast<0>(r.h), s0 = quad_bcast<1>(r.h), s1 = quad_bcast<2>(r.h),
+                   s2 = quad_bcast<3>(r.h);
+    const bool lo4 = jj < 2;
+    const uint32_t sh0 = 16 * (jj & 1);  // byte 2jj & 3 of the scale words
+    const uint32_t a0 = s0 >> sh0, b0 = s1 >> sh0, c0 = s2 >> sh0;
+    const uint32_t a1 = a0 >> 8, b1 = b0 >> 8, c1 = c0 >> 8;
+    const uint32_t sc0 = lo4 ? (a0 & 63) : ((c0 & 15) | ((a0 >> 2) & 48));
+    const uint32_t m0 = lo4 ? (b0 & 63) : (((c0 >> 4) & 15) | ((b0 >> 2) & 48));
+    const uint32_t sc1 = lo4 ? (a1 & 63) : ((c1 & 15) | ((a1 >> 2) & 48));
+    const uint32_t m1 = lo4 ? (b1 & 63) : (((c1 >> 4) & 15) | ((b1 >> 2) & 48));
+    const float d = h2f(h0 & 0xffff), dmin = h2f(h0 >> 16);
+    const float xs_l = s.sum<Q>(u, 0), xs_h = s.sum<Q>(u, 1);
+    const float dl0 = d * (float)sc0, dl1 = d * (float)sc1;
+    return dl0 * (sl - 1024.0f * xs_l) - (dmin * (float)m0) * xs_l +
+           dl1 * (0.0625f * sh - 64.0f * xs_h) - (dmin * (float)m1) * xs_h;
   }
 
   // Verify: one MFMA 16x16x32 per sub-block; lane group g takes l = 8g..8g+7 of it, i.e. the
@@ -212,7 +260,13 @@ struct FQ4_K {
 struct FQ6_K {
   static constexpr uint32_t TYPE = ISHZ_GGML_Q6_K;
   static constexpr int BS = 256, TS = 210, UPB = 4;  // unit: (n, l-half), 64 weights
-  static constexpr bool XSUM = false, GRID = false;
+  static constexpr int BATCH = 2;
+  static constexpr bool XSUM = true, GRID = false;
+  static constexpr int R = 8, Q = 4;  // slot 2qq + i: k0 + 32qq + 8i; sum qq: k0 + 32qq
+  static DEV int k0_of(int u) { return (u >> 2) * 256 + ((u >> 1) & 1) * 128 + (u & 1) * 16; }
+  static DEV int slot_k(int u, int r) { return k0_of(u) + 32 * (r >> 1) + 8 * (r & 1); }
+  static DEV int sum_k(int u, int q) { return k0_of(u) + 32 * q; }
+  static constexpr int SUM_LEN = 16;
   struct Raw {
     u4 qa, qb, qh;
     u2 sc;
@@ -229,10 +283,13 @@ struct FQ6_K {
     r.d = ld2(p + 208);
     return r;
   }
+  // Each 6-bit code becomes 1024 + q; sum (q - 32) x = S - 1056 X over a 16-weight group.
   static DEV float dot(const Raw &r, int u, const GemvShared &s) {
-    const int b = u >> 2, n = (u >> 1) & 1, lh = u & 1;
-    const int k0 = b * 256 + 128 * n + 16 * lh;
+    const int lh = u & 1;
     float S[4] = {0, 0, 0, 0};
+    uint32_t xv[4][8];
+#pragma unroll
+    for (int qq = 0; qq < 4; qq++) unpack(s.slot<R>(u, 2 * qq), s.slot<R>(u, 2 * qq + 1), xv[qq]);
 #pragma unroll
     for (int t = 0; t < 4; t++) {
       const uint32_t a = r.qa[t], bq = r.qb[t], h = r.qh[t];
@@ -242,9 +299,8 @@ struct FQ6_K {
                              ((bq >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u)};
 #pragma unroll
       for (int qq = 0; qq < 4; qq++) {
-        const uint32_t *x = s.x + (k0 + 32 * qq + 4 * t) / 2;
-        S[qq] = dot2(unmagic(v[qq] & 0x003F003Fu, 1056), x[0], S[qq]);
-        S[qq] = dot2(unmagic((v[qq] >> 8) & 0x003F003Fu, 1056), x[1], S[qq]);
+        S[qq] = dot2(and_or(v[qq], 0x003F003Fu, s.mg), xv[qq][2 * t], S[qq]);
+        S[qq] = dot2(and_or(v[qq] >> 8, 0x003F003Fu, s.mg), xv[qq][2 * t + 1], S[qq]);
       }
     }
     // sc[8n + lh + 2qq]: bytes lh, lh+2 of the low word, lh, lh+2 of the high word.
@@ -252,7 +308,8 @@ struct FQ6_K {
     const int sh = 8 * lh;
     const float s0 = (float)(int8_t)(r.sc.x >> sh), s1 = (float)(int8_t)(r.sc.x >> (sh + 16));
     const float s2 = (float)(int8_t)(r.sc.y >> sh), s3 = (float)(int8_t)(r.sc.y >> (sh + 16));
-    return (d * s0) * S[0] + (d * s1) * S[1] + (d * s2) * S[2] + (d * s3) * S[3];
+    return (d * s0) * (S[0] - 1056.0f * s.sum<Q>(u, 0)) + (d * s1) * (S[1] - 1056.0f * s.sum<Q>(u, 1)) +
+           (d * s2) * (S[2] - 1056.0f * s.sum<Q>(u, 2)) + (d * s3) * (S[3] - 1056.0f * s.sum<Q>(u, 3));
   }
 
   // Verify: MFMA 16x16x16, one per 16-weight scale group (n, qq, lh); lane group g takes
@@ -311,7 +368,12 @@ struct FQ6_K {
 struct FIQ2_XS {
   static constexpr uint32_t TYPE = ISHZ_GGML_IQ2_XS;
   static constexpr int BS = 256, TS = 74, UPB = 4;  // unit: two groups, 16 B of qs, 64 weights
+  static constexpr int BATCH = 2;
   static constexpr bool XSUM = false, GRID = true;
+  static constexpr int R = 8, Q = 1;  // slot l: k0 + 8l
+  static DEV int slot_k(int u, int r) { return (u >> 2) * 256 + (u & 3) * 64 + 8 * r; }
+  static DEV int sum_k(int u, int q) { return 0; }
+  static constexpr int SUM_LEN = 16;
   struct Raw {
     u4 q;
     uint32_t sc, d;
@@ -322,15 +384,13 @@ struct FIQ2_XS {
     return {ld16<2>(p + 2 + 16 * pp), ld2(p + 66 + 2 * pp), ld2(p)};
   }
   static DEV float dot(const Raw &r, int u, const GemvShared &s) {
-    const int b = u >> 2, pp = u & 3;
-    const int k0 = b * 256 + 64 * pp;
     const float d = h2f(r.d);
     float acc = 0.0f;
 #pragma unroll
     for (int l = 0; l < 8; l++) {
       const uint32_t q = (r.q[l >> 1] >> (16 * (l & 1))) & 0xffffu;
       const u4 G = s.grid[q & 511], M = s.sgn[q >> 9];
-      const u4 X = *(const u4 *)(s.x + (k0 + 8 * l) / 2);
+      const u4 X = s.slot<R>(u, l);
       float e = dot2(G.x ^ M.x, X.x, 0.0f);
       e = dot2(G.y ^ M.y, X.y, e);
       e = dot2(G.z ^ M.z, X.z, e);
