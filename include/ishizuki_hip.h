@@ -75,6 +75,33 @@ int ishz_ggml_gather(uint32_t type, const int32_t *ids, int n_ids, const void *b
                      size_t blocks_bytes, int n_rows, int K, void *out, int out_dtype,
                      ishz_stream_t stream);
 
+/* hadamardRotate (Core/Hadamard.swift:8-23): per contiguous `block` of each row,
+   y = WHT_block(x * signs) / sqrt(block) in fp32 (signs applied after the transform when
+   inverse), Sylvester (natural) order, output in the input dtype. signs: fp32 [width] or NULL
+   (all +1). block a power of two <= 4096; width * 4 bytes <= 64 KiB. */
+int ishz_hadamard(const void *x, int dtype, int rows, int width, int block, const float *signs,
+                  int inverse, void *y, ishz_stream_t stream);
+
+/* MLX affine quantized matmul: y[M][N] = x[M][K] . W^T, W[n][k] = s[n][k/group] * q + b[...].
+   codes u32 [N][K/16] (2-bit, code k at bits 2*(k%16) of word k/16: MLX's pack,
+   Quantize/WeightedAffineQuantizer.swift:142-153), scales/biases [N][K/group] in scale_dtype
+   (fp16 or bf16). x and y fp16. M = 1 is the streaming GEMV (MLX quantizedMM's qmv, called at
+   Core/Hadamard.swift:228-230); M = 2..16 the MFMA verify kernel (VerifyMatmul.applyAny,
+   Core/VerifyMatmul.swift:73-120). Declines: bits != 2, group not 64/128, K % 128, other dtypes. */
+int ishz_affine_matmul(const void *x, int x_dtype, int M, int K, const uint32_t *codes,
+                       const void *scales, const void *biases, int scale_dtype, int N, int bits,
+                       int group, void *y, ishz_stream_t stream);
+
+/* The rotated PackedLinear forward (Core/Hadamard.swift:180-231): hadamardRotate(x, block,
+   signs) rounded to fp16, then ishz_affine_matmul. block = 0 means no rotation. For M = 1 the
+   rotation runs inside the GEMV (x is rotated while it is staged into LDS); for M >= 2 it is a
+   separate kernel into `workspace` (ishz_affine_workspace_size bytes). */
+size_t ishz_affine_workspace_size(int M, int K);
+int ishz_affine_linear(const void *x, int x_dtype, int M, int K, const float *signs, int block,
+                       const uint32_t *codes, const void *scales, const void *biases,
+                       int scale_dtype, int N, int bits, int group, void *y, void *workspace,
+                       size_t workspace_bytes, ishz_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,6 +23,10 @@ _SIGS = {
     "ishz_ggml_matmul_few": (I, [U32, P, I, I, I, P, SZ, I, I, P, P]),
     "ishz_ggml_dequant": (I, [U32, P, SZ, SZ, P, I, P]),
     "ishz_ggml_gather": (I, [U32, P, I, P, SZ, I, I, P, I, P]),
+    "ishz_hadamard": (I, [P, I, I, I, I, P, I, P, P]),
+    "ishz_affine_matmul": (I, [P, I, I, I, P, P, P, I, I, I, I, P, P]),
+    "ishz_affine_workspace_size": (SZ, [I, I]),
+    "ishz_affine_linear": (I, [P, I, I, I, P, I, P, P, P, I, I, I, I, P, P, SZ, P]),
 }
 
 _lib = None

@@ -1,0 +1,100 @@
+"""Affine 2-bit matmul and Hadamard rotation on the GPU vs the CPU oracle (through the C ABI).
+
+Rotation: fp32 output within 1e-5 of the oracle's fp32 WHT (summation order differs); fp16 output
+equal to the oracle rounded to fp16 except for rare one-ulp rounding-boundary cases.
+Matmul: max |y - ref| <= 1e-3 * max |ref| with ref = the oracle's dequantize-then-fp32-dot of the
+fp16-rounded rotated x (the reference casts the rotation back to x.dtype).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import assert_close
+from ishizuki_amd import affine, synth
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+@pytest.mark.parametrize("block", [2, 32, 128, 512, 4096])
+@pytest.mark.parametrize("inverse", [False, True])
+def test_hadamard_fp32(block, inverse):
+    x = np.random.default_rng(block).standard_normal((3, 8192)).astype(np.float32)
+    s = synth.hadamard_signs(8192, seed=4)
+    ref = oracle.hadamard(x, block, s, inverse=inverse)
+    y = affine.hadamard_rotate(torch.from_numpy(x).to(DEV), block, torch.from_numpy(s), inverse).cpu().numpy()
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+def test_hadamard_fp16_roundtrip():
+    x = synth.fp16_normal((4, 5120), seed=1)
+    xt = torch.from_numpy(x).to(DEV)
+    y = affine.hadamard_rotate(xt, 128)
+    ref = oracle.hadamard(x.astype(np.float32), 128).astype(np.float16)
+    diff = np.abs(y.cpu().numpy().astype(np.float32) - ref.astype(np.float32))
+    ulp = np.abs(ref.astype(np.float32)) * 2.0 ** -10 + 1e-7
+    assert np.all(diff <= ulp)
+    back = affine.hadamard_rotate(y, 128).cpu().numpy().astype(np.float32)  # H.H = I
+    assert np.abs(back - x.astype(np.float32)).max() < 4e-3 * np.abs(x).max()
+
+
+def affine_case(N, K, M, group, seed, block=0, signs_seed=None):
+    codes, s, b = synth.affine_pack(N, K, group=group, seed=seed)
+    x = synth.fp16_normal((M, K), seed=seed + 1)
+    xf = x.astype(np.float32)
+    signs = synth.hadamard_signs(K, seed=signs_seed) if block else None
+    if block:
+        xf = oracle.hadamard(xf, block, signs).astype(np.float16).astype(np.float32)
+    ref = oracle.affine_matmul(xf, codes, s.view(np.uint16), b.view(np.uint16), N, 2, group)
+    dev = lambda a: torch.from_numpy(a).to(DEV)
+    args = (dev(x), dev(codes.view(np.int32)), dev(s), dev(b))
+    return args, signs, ref
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 8, 16])
+@pytest.mark.parametrize("group", [64, 128])
+def test_affine_matmul(M, group):
+    N, K = 1000, 2048
+    (x, w, s, b), _, ref = affine_case(N, K, M, group, seed=M)
+    y = affine.quantized_matmul(x, w, s, b, group_size=group)
+    assert y is not None
+    assert_close(y.float().cpu().numpy(), ref, what=f"affine M={M} g={group}")
+
+
+@pytest.mark.parametrize("M", [1, 2, 8])
+@pytest.mark.parametrize("signs_seed", [None, 7])
+def test_affine_rotated_linear(M, signs_seed):
+    N, K = 1088, 5120
+    (x, w, s, b), signs, ref = affine_case(N, K, M, 64, seed=20 + M, block=128, signs_seed=signs_seed)
+    y = affine.linear(x, w, s, b, signs=torch.from_numpy(signs), block=128, group_size=64)
+    assert y is not None
+    assert_close(y.float().cpu().numpy(), ref, what=f"rotated M={M}")
+
+
+def test_affine_bf16_scales():
+    N, K = 300, 1024
+    codes, s, b = synth.affine_pack(N, K, group=64, seed=3)
+    sb = torch.from_numpy(s.astype(np.float32)).to(torch.bfloat16)
+    bb = torch.from_numpy(b.astype(np.float32)).to(torch.bfloat16)
+    sf = sb.float().numpy().astype(np.float16)  # bf16 values are exact in fp32; oracle takes fp16
+    x = synth.fp16_normal((1, K), seed=4)
+    w = oracle.affine_dequant(codes, np.zeros_like(s).view(np.uint16), np.zeros_like(b).view(np.uint16), N, K, 2, 64)
+    q = w  # all-zero scales/biases give zeros: rebuild from codes directly
+    qv = np.stack([(codes[:, k // 16] >> np.uint32(2 * (k % 16))) & 3 for k in range(K)], 1).astype(np.float32)
+    wf = np.repeat(sb.float().numpy(), 64, 1) * qv + np.repeat(bb.float().numpy(), 64, 1)
+    ref = x.astype(np.float32) @ wf.T
+    for M in (1, 4):
+        xx = np.repeat(x, M, 0)
+        y = affine.quantized_matmul(torch.from_numpy(xx).to(DEV), torch.from_numpy(codes.view(np.int32)).to(DEV),
+                                    sb.to(DEV), bb.to(DEV), group_size=64)
+        assert_close(y.float().cpu().numpy(), np.repeat(ref, M, 0), what=f"bf16 scales M={M}")
+
+
+def test_affine_declines():
+    x = torch.zeros((1, 256), dtype=torch.float16, device=DEV)
+    w = torch.zeros((4, 16), dtype=torch.int32, device=DEV)
+    s = torch.zeros((4, 8), dtype=torch.float16, device=DEV)
+    assert affine.quantized_matmul(x, w, s, s, group_size=32) is None        # group 32
+    assert affine.quantized_matmul(x.float(), w, s, s, group_size=64) is None  # fp32 x
+    assert affine.verify_apply(torch.zeros((1, 256), dtype=torch.float16, device=DEV), w, s, s) is None
