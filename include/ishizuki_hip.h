@@ -102,6 +102,33 @@ int ishz_affine_linear(const void *x, int x_dtype, int M, int K, const float *si
                        int scale_dtype, int N, int bits, int group, void *y, void *workspace,
                        size_t workspace_bytes, ishz_stream_t stream);
 
+/* EXL3 codebooks (EXL3Tensor.Codebook, Core/EXL3.swift:10-14); rates are bits2 = 2 * bits in
+   {2,3,4,5,6,7,8,10,12,14,16} (supportedBits, :27), half-integer rates only with MUL1. */
+enum { ISHZ_EXL3_3INST = 0, ISHZ_EXL3_MCG = 1, ISHZ_EXL3_MUL1 = 2 };
+
+/* EXL3Kernels.dequantize (Core/EXL3.swift:133-147): trellis int16 [K/16][N/16][8*bits2] to a
+   dense W [K][N] (fp32 / fp16 / bf16), bit-exact with the trellis decoder. */
+int ishz_exl3_dequant(const int16_t *trellis, int K, int N, int bits2, int codebook, void *out,
+                      int out_dtype, ishz_stream_t stream);
+
+/* EXL3Kernels.rotate (Core/EXL3.swift:102-124, kernel :219-265): per 128-block of each row,
+   (x * scales if before) -> WHT / sqrt(128) -> (* scales if not before), fp32 math, output in
+   out_dtype (fp32 or fp16). scales fp16 [width] (the suh / svh vectors). */
+int ishz_exl3_rotate(const void *x, int in_dtype, int rows, int width, const uint16_t *scales,
+                     int before, void *y, int out_dtype, ishz_stream_t stream);
+
+/* EXL3Kernels.matvec (Core/EXL3.swift:149-164, kernel :286-330): yh[M][N] (fp32) = xh[M][K]
+   (fp16) . W, W decoded in-kernel. M in 1..16 (the reference: 1..8, 9..16 as two launches). */
+int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const int16_t *trellis, int N,
+                     int bits2, int codebook, float *yh, ishz_stream_t stream);
+
+/* EXL3Kernels.apply (Core/EXL3.swift:82-100): y = fp16(rotate_out(xh . W)) with
+   xh = fp16(rotate_in(x)). Needs ishz_exl3_workspace_size(M, K, N) bytes of device workspace. */
+size_t ishz_exl3_workspace_size(int M, int K, int N);
+int ishz_exl3_apply(const void *x, int x_dtype, int M, int K, const int16_t *trellis,
+                    const uint16_t *suh, const uint16_t *svh, int N, int bits2, int codebook,
+                    void *y, void *workspace, size_t workspace_bytes, ishz_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,318 @@
+// EXL3 trellis-coded projections on gfx950, decoded inside the matmul.
+//
+// Replaces EXL3Kernels (Sources/IshizukiKit/Core/EXL3.swift:79-332): apply (:82-100) = rotate in,
+// matvec (1..16 rows), rotate out; dequantize (:133-147); rotate (:102-124).
+//
+// Format (EXL3Tensor, :9-77): trellis int16 [K/16][N/16][16*bits], one 16x16 tile per
+// (tk, tn). A tile's int16s pair little-endian into u32 words read as one MSB-first ring of
+// RING bits; weight p (0..255) is the codebook image of the 16 bits ending at end(p) (wrapping);
+// p = 8*lane + i sits at row (lane%4)*2 + {0,1,8,9}[i%4], column lane/4 + 8*(i/4).
+//
+// Work split: lane (j = l%16, g = l/16) decodes positions 8*(4*(j%8) + g) + 4*(j/8) + {0..3},
+// which are rows 2g + {0,1,8,9} of column j: every weight of a tile is decoded exactly once per
+// wave, already in MFMA B-operand order (k rows by lane group, column j by lane).
+#include <algorithm>
+
+#include "common.h"
+
+namespace ishz {
+
+// exl3_decode (EXL3.swift:136-147): 3INST / MCG / MUL1 codebooks, fp16 single rounding.
+DEV _Float16 exl3_decode(uint32_t s, int cb) {
+  if (cb == 2) {
+    const uint32_t x = s * 0x83DCD12Du;
+    const uint32_t p = (x & 0x00ff00ffu) + ((x >> 8) & 0x00ff00ffu);
+    const _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)((p & 0xffffu) + (p >> 16) + 0x6400u));
+    return __builtin_fmaf16(h, __builtin_bit_cast(_Float16, (uint16_t)0x1eee),
+                            __builtin_bit_cast(_Float16, (uint16_t)0xc931));
+  }
+  uint32_t x = cb == 1 ? s * 0xCBAC1FEDu : s * 89226354u + 64248484u;
+  x = (x & 0x8fff8fffu) ^ 0x3b603b60u;
+  return __builtin_bit_cast(_Float16, (uint16_t)x) + __builtin_bit_cast(_Float16, (uint16_t)(x >> 16));
+}
+
+template <int KA, bool HALF>
+struct Trellis {
+  static constexpr int RING = HALF ? 128 * (2 * KA + 1) : 256 * KA;
+  static constexpr int WORDS = RING / 32;
+  static DEV int end(int p) {
+    return HALF ? (p >> 1) * (2 * KA + 1) + KA + (p & 1) * (KA + 1) : (p + 1) * KA;
+  }
+  // Bit offsets (after the window start) where the states of p0..p0+3 end; p0 is even.
+  static constexpr int rel(int i) {
+    return HALF ? 16 + (i >> 1) * (2 * KA + 1) + (i & 1) * (KA + 1) : 16 + i * KA;
+  }
+  // Per-lane constants for positions p0..p0+3: first word and shift of the 64-bit window.
+  struct Win {
+    int j0, j1, j2, sh;
+  };
+  static DEV Win window(int p0) {
+    const int lo = (end(p0) + RING - 16) % RING;
+    const int i0 = lo >> 5;
+    return {i0, (i0 + 1) % WORDS, (i0 + 2) % WORDS, lo & 31};
+  }
+  // Decode four weights from a tile's words; returns them as two packed fp16 pairs.
+  static DEV u2 decode4(const uint32_t *tile, const Win &wn, int cb) {
+    const uint64_t w0 = tile[wn.j0], w1 = tile[wn.j1], w2 = tile[wn.j2];
+    uint64_t a = ((w0 << 32) | w1) << wn.sh;
+    if (wn.sh) a |= w2 >> (32 - wn.sh);
+    uint16_t h[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t s = (uint32_t)(a >> (64 - rel(i))) & 0xffffu;
+      h[i] = __builtin_bit_cast(uint16_t, exl3_decode(s, cb));
+    }
+    return u2{(uint32_t)h[0] | (uint32_t)h[1] << 16, (uint32_t)h[2] | (uint32_t)h[3] << 16};
+  }
+};
+
+// ------------------------------------------------------------------- matvec / verify
+// A workgroup owns one column tile tn (16 outputs); its KS waves take tiles tk = wave, wave+KS,
+// ... and partial results are summed through LDS. MF: one MFMA 16x16x16 per tile (tokens in A,
+// up to 16). Otherwise (M = 1) each lane dots its four weights with x in fp32 (v_dot2) and the
+// four k-groups of a column are summed by cross-lane shuffles.
+template <int KA, bool HALF, bool MF>
+__global__ __launch_bounds__(1024) void exl3_mm(const uint16_t *__restrict__ xh, int M, int K,
+                                                const uint32_t *__restrict__ trellis, int N, int cb,
+                                                float *__restrict__ yh) {
+  using TR = Trellis<KA, HALF>;
+  extern __shared__ __align__(16) float red[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, KS = blockDim.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int tn = blockIdx.x, tiles_n = N / 16, tiles_k = K / 16;
+  const typename TR::Win wn = TR::window(8 * (4 * (j & 7) + g) + 4 * (j >> 3));
+  const uint32_t *col = trellis + (size_t)tn * TR::WORDS;
+  const size_t tstride = (size_t)tiles_n * TR::WORDS;
+
+  if constexpr (MF) {
+    const bool tok = j < M;
+    const uint16_t *xr = xh + (size_t)(tok ? j : 0) * K + 2 * g;
+    f4 acc = {0, 0, 0, 0};
+    for (int tk = wave; tk < tiles_k; tk += KS) {
+      const u2 B = TR::decode4(col + tk * tstride, wn, cb);
+      const u2 A = tok ? u2{*(const uint32_t *)(xr + 16 * tk), *(const uint32_t *)(xr + 16 * tk + 8)}
+                       : u2{0, 0};
+      acc = mfma16(as_h4(A), as_h4(B), acc);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) red[(wave * 4 + r) * 64 + lane] = acc[r];
+    __syncthreads();
+    for (int o = threadIdx.x; o < 256; o += blockDim.x) {
+      const int r = o >> 6, l = o & 63;
+      float s = 0.0f;
+      for (int v = 0; v < KS; v++) s += red[(v * 4 + r) * 64 + l];
+      const int t = 4 * (l >> 4) + r;
+      if (t < M) yh[(size_t)t * N + tn * 16 + (l & 15)] = s;
+    }
+  } else {
+    const uint16_t *xr = xh + 2 * g;
+    float acc = 0.0f;
+    for (int tk = wave; tk < tiles_k; tk += KS) {
+      const u2 B = TR::decode4(col + tk * tstride, wn, cb);
+      acc = dot2(B.x, *(const uint32_t *)(xr + 16 * tk), acc);
+      acc = dot2(B.y, *(const uint32_t *)(xr + 16 * tk + 8), acc);
+    }
+    acc += __shfl_xor(acc, 16, 64);
+    acc += __shfl_xor(acc, 32, 64);
+    if (g == 0) red[wave * 16 + j] = acc;
+    __syncthreads();
+    if (threadIdx.x < 16) {
+      float s = 0.0f;
+      for (int v = 0; v < KS; v++) s += red[v * 16 + threadIdx.x];
+      yh[tn * 16 + threadIdx.x] = s;
+    }
+  }
+}
+
+// ------------------------------------------------------------------- dequantize
+template <int KA, bool HALF>
+__global__ __launch_bounds__(256) void exl3_dequant_kernel(const uint32_t *__restrict__ trellis,
+                                                           int K, int N, int cb, void *out,
+                                                           int dt) {
+  using TR = Trellis<KA, HALF>;
+  const size_t tile = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int tiles_n = N / 16;
+  if (tile >= (size_t)(K / 16) * tiles_n) return;
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const u2 v = TR::decode4(trellis + tile * TR::WORDS, TR::window(8 * (4 * (j & 7) + g) + 4 * (j >> 3)), cb);
+  const size_t tk = tile / tiles_n, tn = tile % tiles_n;
+  const uint16_t h[4] = {(uint16_t)v.x, (uint16_t)(v.x >> 16), (uint16_t)v.y, (uint16_t)(v.y >> 16)};
+  const int rows[4] = {2 * g, 2 * g + 1, 2 * g + 8, 2 * g + 9};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const size_t o = (tk * 16 + rows[i]) * (size_t)N + tn * 16 + j;
+    const float f = h2f(h[i]);
+    if (dt == ISHZ_DT_F32) ((float *)out)[o] = f;
+    else if (dt == ISHZ_DT_F16) ((uint16_t *)out)[o] = h[i];
+    else ((uint16_t *)out)[o] = (uint16_t)((__builtin_bit_cast(uint32_t, f) + 0x7fffu +
+                                            ((__builtin_bit_cast(uint32_t, f) >> 16) & 1u)) >> 16);
+  }
+}
+
+// ------------------------------------------------------------------- 128-point rotation
+// EXL3Kernels.rotate (EXL3.swift:102-124): per 128 block, (x * s if before) -> WHT / sqrt(128)
+// -> (* s if after), fp32, cast to the output dtype. One wave per block, two values per lane.
+__global__ __launch_bounds__(256) void exl3_rotate_kernel(const void *__restrict__ x, int in_dt,
+                                                          size_t blocks, int width,
+                                                          const uint16_t *__restrict__ scales,
+                                                          int before, void *__restrict__ y,
+                                                          int out_dt) {
+  const size_t blk = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (blk >= blocks) return;
+  const int lane = threadIdx.x & 63;
+  const size_t base = blk * 128 + 2 * lane;
+  const int col = (int)((blk * 128) % width) + 2 * lane;
+  float v0, v1;
+  if (in_dt == ISHZ_DT_F32) {
+    v0 = ((const float *)x)[base];
+    v1 = ((const float *)x)[base + 1];
+  } else {
+    v0 = h2f(((const uint16_t *)x)[base]);
+    v1 = h2f(((const uint16_t *)x)[base + 1]);
+  }
+  if (before) {
+    v0 *= h2f(scales[col]);
+    v1 *= h2f(scales[col + 1]);
+  }
+  float a = v0 + v1, b = v0 - v1;
+  v0 = a;
+  v1 = b;
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const float p0 = __shfl_xor(v0, m, 64), p1 = __shfl_xor(v1, m, 64);
+    const bool hi = (lane & m) != 0;
+    v0 = hi ? p0 - v0 : v0 + p0;
+    v1 = hi ? p1 - v1 : v1 + p1;
+  }
+  const float r = 0.08838834764831845f;  // 1 / sqrt(128)
+  v0 *= r;
+  v1 *= r;
+  if (!before) {
+    v0 *= h2f(scales[col]);
+    v1 *= h2f(scales[col + 1]);
+  }
+  if (out_dt == ISHZ_DT_F32) {
+    ((float *)y)[base] = v0;
+    ((float *)y)[base + 1] = v1;
+  } else {
+    ((uint16_t *)y)[base] = f2h(v0);
+    ((uint16_t *)y)[base + 1] = f2h(v1);
+  }
+}
+
+// ------------------------------------------------------------------- host
+static int num_cu_e() {
+  static int n = [] {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      return v;
+    return 256;
+  }();
+  return n;
+}
+
+// Calls F.template operator()<KA, HALF>() for a rate given as bits2 = 2 * bits.
+template <class F>
+static int by_rate(int bits2, F &&f) {
+  switch (bits2) {
+  case 2: return f.template operator()<1, false>();
+  case 3: return f.template operator()<1, true>();
+  case 4: return f.template operator()<2, false>();
+  case 5: return f.template operator()<2, true>();
+  case 6: return f.template operator()<3, false>();
+  case 7: return f.template operator()<3, true>();
+  case 8: return f.template operator()<4, false>();
+  case 10: return f.template operator()<5, false>();
+  case 12: return f.template operator()<6, false>();
+  case 14: return f.template operator()<7, false>();
+  case 16: return f.template operator()<8, false>();
+  }
+  return decline("EXL3 rate is not one of 1, 1.5, 2, 2.5, 3, 3.5, 4..8 bits");
+}
+
+// EXL3Tensor.init validation (EXL3.swift:29-55).
+static int check_exl3(int K, int N, int bits2, int cb) {
+  if (cb < 0 || cb > 2) return decline("unknown EXL3 codebook");
+  if ((bits2 & 1) && cb != 2) return decline("half-integer EXL3 rates need the mul1 codebook");
+  if (K <= 0 || N <= 0 || K % 128 || N % 128) return decline("EXL3 K and N must be multiples of 128");
+  return ISHZ_OK;
+}
+
+}  // namespace ishz
+
+using namespace ishz;
+
+extern "C" int ishz_exl3_dequant(const int16_t *trellis, int K, int N, int bits2, int codebook,
+                                 void *out, int out_dtype, ishz_stream_t stream) {
+  if (codebook < 0 || codebook > 2 || ((bits2 & 1) && codebook != 2)) return decline("bad codebook/rate");
+  if (K <= 0 || N <= 0 || K % 16 || N % 16) return decline("EXL3 K and N must be multiples of 16");
+  if (out_dtype < ISHZ_DT_F32 || out_dtype > ISHZ_DT_BF16) return decline("unsupported output dtype");
+  if (!trellis || !out) return einval("null pointer");
+  const size_t tiles = (size_t)(K / 16) * (N / 16);
+  return by_rate(bits2, [&]<int KA, bool HALF>() -> int {
+    hipLaunchKernelGGL((exl3_dequant_kernel<KA, HALF>), dim3((unsigned)((tiles + 3) / 4)), dim3(256), 0,
+                       S(stream), (const uint32_t *)trellis, K, N, codebook, out, out_dtype);
+    ISHZ_LAUNCH_CHECK("exl3 dequant launch");
+    return ISHZ_OK;
+  });
+}
+
+extern "C" int ishz_exl3_rotate(const void *x, int in_dtype, int rows, int width,
+                                const uint16_t *scales, int before, void *y, int out_dtype,
+                                ishz_stream_t stream) {
+  if ((in_dtype != ISHZ_DT_F32 && in_dtype != ISHZ_DT_F16) ||
+      (out_dtype != ISHZ_DT_F32 && out_dtype != ISHZ_DT_F16))
+    return decline("rotation takes fp32 or fp16");
+  if (rows <= 0 || width <= 0 || width % 128) return einval("width must be a multiple of 128");
+  if (!x || !y || !scales) return einval("null pointer");
+  const size_t blocks = (size_t)rows * (width / 128);
+  hipLaunchKernelGGL(exl3_rotate_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, S(stream), x,
+                     in_dtype, blocks, width, scales, before, y, out_dtype);
+  ISHZ_LAUNCH_CHECK("exl3 rotate launch");
+  return ISHZ_OK;
+}
+
+extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const int16_t *trellis,
+                                int N, int bits2, int codebook, float *yh, ishz_stream_t stream) {
+  int rc = check_exl3(K, N, bits2, codebook);
+  if (rc) return rc;
+  if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
+  if (M < 1 || M > 16) return decline("row count outside 1..16");
+  if (!xh || !trellis || !yh) return einval("null pointer");
+  const int wgs = N / 16, tiles_k = K / 16;
+  int ks = 1;
+  while (ks < 16 && ks < tiles_k && wgs * ks < num_cu_e() * 16) ks *= 2;
+  return by_rate(bits2, [&]<int KA, bool HALF>() -> int {
+    if (M == 1)
+      hipLaunchKernelGGL((exl3_mm<KA, HALF, false>), dim3(wgs), dim3(64 * ks), (size_t)ks * 16 * 4,
+                         S(stream), (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, codebook, yh);
+    else
+      hipLaunchKernelGGL((exl3_mm<KA, HALF, true>), dim3(wgs), dim3(64 * ks), (size_t)ks * 256 * 4,
+                         S(stream), (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, codebook, yh);
+    ISHZ_LAUNCH_CHECK("exl3 matvec launch");
+    return ISHZ_OK;
+  });
+}
+
+extern "C" size_t ishz_exl3_workspace_size(int M, int K, int N) {
+  return ((size_t)M * K * 2 + 255) / 256 * 256 + (size_t)M * N * 4;
+}
+
+extern "C" int ishz_exl3_apply(const void *x, int x_dtype, int M, int K, const int16_t *trellis,
+                               const uint16_t *suh, const uint16_t *svh, int N, int bits2,
+                               int codebook, void *y, void *workspace, size_t workspace_bytes,
+                               ishz_stream_t stream) {
+  int rc = check_exl3(K, N, bits2, codebook);
+  if (rc) return rc;
+  if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
+  if (M < 1 || M > 16) return decline("row count outside 1..16");
+  if (!x || !trellis || !suh || !svh || !y) return einval("null pointer");
+  if (!workspace || workspace_bytes < ishz_exl3_workspace_size(M, K, N))
+    return einval("workspace too small (ishz_exl3_workspace_size)");
+  uint16_t *xh = (uint16_t *)workspace;
+  float *yh = (float *)((uint8_t *)workspace + ((size_t)M * K * 2 + 255) / 256 * 256);
+  if ((rc = ishz_exl3_rotate(x, ISHZ_DT_F16, M, K, suh, 1, xh, ISHZ_DT_F16, stream))) return rc;
+  if ((rc = ishz_exl3_matvec(xh, ISHZ_DT_F16, M, K, trellis, N, bits2, codebook, yh, stream))) return rc;
+  return ishz_exl3_rotate(yh, ISHZ_DT_F32, M, N, svh, 0, y, ISHZ_DT_F16, stream);
+}

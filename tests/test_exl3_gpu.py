@@ -1,0 +1,98 @@
+"""EXL3 on the GPU vs the oracle and exllamav3's golden reconstructions (through the C ABI).
+
+Dequant: bit-exact against exl3_reference.npz (11 rate/codebook cases, EXL3Tests.swift:44-55).
+Matvec: max |y - ref| <= 1e-3 * max|ref| against the oracle's fp32 product with the decoded W
+(the reference's own check is 1e-5 of the |x||W| bound in fp32, EXL3Tests.swift:57-72; ours are
+fp16 activations with fp32 accumulation in a different order).
+Apply: the full rotate -> matvec -> rotate path vs the oracle restatement, 1e-3 of max|ref|.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import assert_close, bits_equal
+from ishizuki_amd import exl3, synth
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+CASES = [("r1c0", 0), ("r2c1", 1), ("r3c2", 2), ("r4c0", 0), ("r5c2", 2), ("r6c1", 1),
+         ("r7c2", 2), ("r8c0", 0), ("r1h5c2", 2), ("r2h5c2", 2), ("r3h5c2", 2)]
+
+
+@pytest.mark.parametrize("name,cb", CASES)
+def test_dequant_matches_exllamav3(golden_exl3, name, cb):
+    t = golden_exl3[name + ".trellis"]
+    K, N = t.shape[0] * 16, t.shape[1] * 16
+    out = torch.empty((K, N), dtype=torch.float32, device=DEV)
+    from ishizuki_amd import _lib
+    from ishizuki_amd._torch import ptr
+    rc = _lib.lib().ishz_exl3_dequant(ptr(torch.from_numpy(t).to(DEV)), K, N, t.shape[2] // 8, cb, ptr(out),
+                                      _lib.DT_F32, None)
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    assert bits_equal(out.cpu().numpy(), golden_exl3[name + ".expected"])
+
+
+def make(K, N, bits2, cb, seed):
+    t, suh, svh = synth.exl3_pack(K, N, bits2=bits2, seed=seed)
+    ten = exl3.EXL3Tensor(torch.from_numpy(t).to(DEV), torch.from_numpy(suh).to(DEV),
+                          torch.from_numpy(svh).to(DEV), codebook=cb)
+    return t, suh, svh, ten
+
+
+@pytest.mark.parametrize("bits2,cb", [(4, 0), (4, 1), (4, 2), (2, 0), (3, 2), (8, 0), (16, 1), (7, 2)])
+def test_dequant_random_rates(bits2, cb):
+    t, _, _, ten = make(256, 384, bits2, cb, seed=bits2 * 3 + cb)
+    w = exl3.dequantize(ten, torch.float32).cpu().numpy()
+    assert bits_equal(w, oracle.exl3_dequant(t, bits2, cb))
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 8, 16])
+@pytest.mark.parametrize("bits2,cb", [(4, 0), (4, 2), (3, 2), (6, 1)])
+def test_matvec(M, bits2, cb):
+    K, N = 1024, 512
+    t, _, _, ten = make(K, N, bits2, cb, seed=M + bits2)
+    w = oracle.exl3_dequant(t, bits2, cb)
+    xh = synth.fp16_normal((M, K), seed=M)
+    ref = xh.astype(np.float32) @ w
+    y = exl3.matvec(torch.from_numpy(xh).to(DEV), ten)
+    assert y is not None
+    assert_close(y.cpu().numpy(), ref, what=f"exl3 matvec M={M} bits2={bits2} cb={cb}")
+
+
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_apply_matches_oracle(M):
+    K, N = 5120, 1024
+    t, suh, svh, ten = make(K, N, 4, 0, seed=40 + M)
+    x = synth.fp16_normal((M, K), seed=M + 100)
+    ref = oracle.exl3_apply(x.astype(np.float32), t, suh.astype(np.float32), svh.astype(np.float32), 4, 0)
+    y = exl3.apply(torch.from_numpy(x).to(DEV), ten)
+    assert_close(y.float().cpu().numpy(), ref, what=f"exl3 apply M={M}")
+
+
+@pytest.mark.parametrize("name,cb", [("qwen3", 0), ("qwen38", 2)])
+def test_projection_reproduces_checkpoint(golden_exl3, name, cb):
+    # EXL3Tests.projectionMatchesCheckpoint (:74-98): rel-L2 < 0.12 against the fp16 checkpoint.
+    t = torch.from_numpy(golden_exl3[name + ".trellis"]).to(DEV)
+    ten = exl3.EXL3Tensor(t, torch.from_numpy(golden_exl3[name + ".suh"]).to(DEV),
+                          torch.from_numpy(golden_exl3[name + ".svh"]).to(DEV), codebook=cb)
+    ref_w = golden_exl3[name + ".weight"].astype(np.float32)
+    x = np.random.default_rng(3).standard_normal((16, 128)).astype(np.float16)
+    prev = None
+    for rows in (1, 5, 12, 16):
+        y = exl3.apply(torch.from_numpy(x[:rows]).to(DEV), ten).float().cpu().numpy()
+        want = x[:rows].astype(np.float32) @ ref_w
+        err = np.sqrt(((y - want) ** 2).sum() / (want ** 2).sum())
+        assert err < 0.12, (rows, err)
+        if prev is not None:
+            assert np.abs(y[0] - prev[0]).max() < 2e-2
+        prev = y
+
+
+def test_tensor_validation():
+    z = torch.zeros((8, 8, 24), dtype=torch.int16)
+    with pytest.raises(ValueError):
+        exl3.EXL3Tensor(z, torch.ones(128), torch.ones(128), codebook=0)   # 1.5 bits needs mul1
+    with pytest.raises(ValueError):
+        exl3.EXL3Tensor(torch.zeros((8, 8, 20), dtype=torch.int16), torch.ones(128), torch.ones(128))
