@@ -129,6 +129,28 @@ int ishz_exl3_apply(const void *x, int x_dtype, int M, int K, const int16_t *tre
                     const uint16_t *suh, const uint16_t *svh, int N, int bits2, int codebook,
                     void *y, void *workspace, size_t workspace_bytes, ishz_stream_t stream);
 
+/* MoEBlock routing (Text/MoEBlock.swift:124-134): softmax over E logits (fp32) per token, the
+   topk largest (ties to the lower index), renormalised to sum 1 when `normalize`. ids [T][topk]
+   in descending order, weights [T][topk]. */
+int ishz_moe_route(const float *logits, int T, int E, int topk, int normalize, int32_t *ids,
+                   float *weights, ishz_stream_t stream);
+
+/* The MoE FFN (MoEBlock.callAsFunction + ResidentExperts.swiglu, Text/MoEBlock.swift:124-171)
+   over GGML-block experts: route (as ishz_moe_route), then for each routed (token, expert)
+   down(silu(gate(x)) * up(x)) with fp16 intermediates, weighted and summed in fp32 into
+   y [T][H] (fp16). gate/up hold E experts of [I][H] blocks back to back, down E experts of
+   [H][I]; expert_bytes is the size of one expert's matrix. Only routed experts' blocks are
+   read. type: Q4_K (also Q4_0, Q6_K). ids_out / weights_out (optional, [T][topk]) receive the
+   routing. workspace: ishz_moe_workspace_size bytes. (The reference runs this through MLX's
+   gatherQuantizedMM over affine experts; GGUF experts are a composition of its routing with the
+   GGML kernels.) */
+size_t ishz_moe_workspace_size(int T, int H, int E, int I, int topk);
+int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T, int H, const float *logits,
+                    int E, int topk, int normalize, const void *gate, const void *up,
+                    const void *down, size_t expert_bytes, int I, void *y, int32_t *ids_out,
+                    float *weights_out, void *workspace, size_t workspace_bytes,
+                    ishz_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

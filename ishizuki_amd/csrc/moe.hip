@@ -1,0 +1,301 @@
+// MoE expert-gathered quantized SwiGLU FFN on gfx950.
+//
+// Restates MoEBlock.callAsFunction + ResidentExperts.swiglu (Sources/IshizukiKit/Text/
+// MoEBlock.swift:124-171) over GGML-block experts: softmax over all E experts in fp32, top-k
+// (ties to the lower index), optional renormalisation, then per (token, expert)
+// down(silu(gate(x)) * up(x)), the k outputs weighted and summed in fp32, narrowed once.
+// Activations between stages are fp16 as the reference's gatherQuantizedMM outputs x.dtype.
+//
+// Kernels: route (one workgroup: routing, per-expert pair lists, active-expert list); gate+up
+// (grid over active experts x 16-row tiles of I; the expert's gate and up rows are two MFMA
+// tiles of the same workgroup, tokens gathered through the pair list; SwiGLU in the epilogue);
+// down (active experts x tiles of H); combine (weighted sum per token). Only routed experts'
+// blocks are ever read.
+#include <algorithm>
+
+#include "ggml_formats.h"
+
+namespace ishz {
+
+struct MoeRoute {
+  int32_t *ids;       // [T*k] expert of (t, s)
+  float *w;           // [T*k] routing weight of (t, s)
+  int32_t *count;     // [1] number of active experts
+  int32_t *active;    // [E] active experts, ascending
+  int32_t *offs;      // [E+1] pair range of expert e in the sorted list
+  int32_t *pair_tok;  // [T*k] token of sorted pair
+  int32_t *inv;       // [T*k] sorted position of (t, s)
+};
+
+// One workgroup of 1024 threads.
+__global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict__ logits, int T,
+                                                         int E, int k, int normalize, MoeRoute R) {
+  extern __shared__ int32_t cnt[];  // E counts
+  for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
+  __syncthreads();
+  for (int t = threadIdx.x; t < T; t += blockDim.x) {
+    const float *l = logits + (size_t)t * E;
+    float mx = l[0];
+    for (int e = 1; e < E; e++) mx = fmaxf(mx, l[e]);
+    float sum = 0.0f;
+    for (int e = 0; e < E; e++) sum += expf(l[e] - mx);
+    float tot = 0.0f;
+    int prev_best = -1;
+    float prev_val = INFINITY;
+    for (int s = 0; s < k; s++) {
+      // next largest logit strictly after (prev_val, prev_best) in (value desc, index asc) order
+      int best = -1;
+      float bv = -INFINITY;
+      for (int e = 0; e < E; e++) {
+        const float v = l[e];
+        const bool after = v < prev_val || (v == prev_val && e > prev_best);
+        if (after && (best < 0 || v > bv)) {
+          best = e;
+          bv = v;
+        }
+      }
+      const float p = expf(bv - mx) / sum;
+      R.ids[t * k + s] = best;
+      R.w[t * k + s] = p;
+      tot += p;
+      prev_best = best;
+      prev_val = bv;
+      if (R.offs) atomicAdd(&cnt[best], 1);
+    }
+    if (normalize)
+      for (int s = 0; s < k; s++) R.w[t * k + s] /= tot;
+  }
+  if (!R.offs) return;  // routing only
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int off = 0, na = 0;
+    for (int e = 0; e < E; e++) {
+      R.offs[e] = off;
+      if (cnt[e]) R.active[na++] = e;
+      off += cnt[e];
+    }
+    R.offs[E] = off;
+    R.count[0] = na;
+  }
+  __syncthreads();
+  // stable placement: expert e's pairs in (t, s) order
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int pos = R.offs[e];
+    if (!cnt[e]) continue;
+    for (int q = 0; q < T * k; q++)
+      if (R.ids[q] == e) {
+        R.pair_tok[pos] = q / k;
+        R.inv[q] = pos;
+        pos++;
+      }
+  }
+}
+
+DEV float r16(float v) { return (float)(_Float16)v; }
+
+// gate + up for one 16-row tile of I of one active expert, 16 routed tokens at a time.
+template <class F>
+__global__ __launch_bounds__(1024) void moe_gate_up_kernel(const uint16_t *__restrict__ x, int H,
+                                                           const uint8_t *__restrict__ gate,
+                                                           const uint8_t *__restrict__ up, int I,
+                                                           MoeRoute R, uint16_t *__restrict__ h) {
+  extern __shared__ __align__(16) float red[];
+  const int a = blockIdx.y;
+  if (a >= R.count[0]) return;
+  const int e = R.active[a], p0 = R.offs[e], p1 = R.offs[e + 1];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, KS = blockDim.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int nblk = H / F::BS;
+  const size_t rb = (size_t)nblk * F::TS;
+  const int i0 = blockIdx.x * 16;
+  const size_t erow = (size_t)e * I + min(i0 + j, I - 1);
+  const uint8_t *rows[2] = {gate + erow * rb, up + erow * rb};
+  for (int c0 = p0; c0 < p1; c0 += 16) {
+    const bool tok = c0 + j < p1;
+    const uint16_t *xr = x + (size_t)(tok ? R.pair_tok[c0 + j] : 0) * H;
+    f4 acc[2] = {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}};
+    for (int b = wave; b < nblk; b += KS) F::template vblock<2>(rows, b, g, xr, tok, acc);
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) red[((wave * 2 + t) * 4 + r) * 64 + lane] = acc[t][r];
+    __syncthreads();
+    for (int o = threadIdx.x; o < 256; o += blockDim.x) {
+      const int r = o >> 6, l = o & 63;
+      float gs = 0.0f, us = 0.0f;
+      for (int v = 0; v < KS; v++) {
+        gs += red[((v * 2 + 0) * 4 + r) * 64 + l];
+        us += red[((v * 2 + 1) * 4 + r) * 64 + l];
+      }
+      const int t = 4 * (l >> 4) + r, i = i0 + (l & 15);
+      if (c0 + t < p1 && i < I) {
+        const float g16 = r16(gs), u16 = r16(us);
+        const float sg = r16(1.0f / (1.0f + __expf(-g16)));
+        h[(size_t)(c0 + t) * I + i] = f2h(r16(g16 * sg) * u16);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// down projection: o[pair][H] = h[pair] . down_e^T, fp16.
+template <class F>
+__global__ __launch_bounds__(1024) void moe_down_kernel(const uint16_t *__restrict__ h, int I,
+                                                        const uint8_t *__restrict__ down, int H,
+                                                        MoeRoute R, uint16_t *__restrict__ o) {
+  extern __shared__ __align__(16) float red[];
+  const int a = blockIdx.y;
+  if (a >= R.count[0]) return;
+  const int e = R.active[a], p0 = R.offs[e], p1 = R.offs[e + 1];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, KS = blockDim.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int nblk = I / F::BS;
+  const size_t rb = (size_t)nblk * F::TS;
+  const int n0 = blockIdx.x * 32;
+  const uint8_t *rows[2] = {down + ((size_t)e * H + min(n0 + j, H - 1)) * rb,
+                            down + ((size_t)e * H + min(n0 + 16 + j, H - 1)) * rb};
+  for (int c0 = p0; c0 < p1; c0 += 16) {
+    const bool tok = c0 + j < p1;
+    const uint16_t *xr = h + (size_t)(tok ? c0 + j : 0) * I;
+    f4 acc[2] = {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}};
+    for (int b = wave; b < nblk; b += KS) F::template vblock<2>(rows, b, g, xr, tok, acc);
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) red[((wave * 2 + t) * 4 + r) * 64 + lane] = acc[t][r];
+    __syncthreads();
+    for (int q = threadIdx.x; q < 512; q += blockDim.x) {
+      const int t2 = q >> 8, r = (q >> 6) & 3, l = q & 63;
+      float s = 0.0f;
+      for (int v = 0; v < KS; v++) s += red[((v * 2 + t2) * 4 + r) * 64 + l];
+      const int t = 4 * (l >> 4) + r, n = n0 + 16 * t2 + (l & 15);
+      if (c0 + t < p1 && n < H) o[(size_t)(c0 + t) * H + n] = f2h(s);
+    }
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__restrict__ o, int H,
+                                                          int T, int k, MoeRoute R,
+                                                          uint16_t *__restrict__ y) {
+  const size_t total = (size_t)T * H;
+  for (size_t q = blockIdx.x * (size_t)blockDim.x + threadIdx.x; q < total;
+       q += (size_t)gridDim.x * blockDim.x) {
+    const int t = (int)(q / H), n = (int)(q % H);
+    float acc = 0.0f;
+    for (int s = 0; s < k; s++) acc += h2f(o[(size_t)R.inv[t * k + s] * H + n]) * R.w[t * k + s];
+    y[q] = f2h(acc);
+  }
+}
+
+// ------------------------------------------------------------------- host
+struct MoeLayout {
+  size_t ids, w, count, active, offs, pair_tok, inv, h, o, total;
+};
+static MoeLayout moe_layout(int T, int H, int E, int I, int k) {
+  auto al = [](size_t v) { return (v + 255) / 256 * 256; };
+  MoeLayout L;
+  const size_t P = (size_t)T * k;
+  size_t off = 0;
+  L.ids = off; off += al(P * 4);
+  L.w = off; off += al(P * 4);
+  L.count = off; off += al(4);
+  L.active = off; off += al((size_t)E * 4);
+  L.offs = off; off += al((size_t)(E + 1) * 4);
+  L.pair_tok = off; off += al(P * 4);
+  L.inv = off; off += al(P * 4);
+  L.h = off; off += al(P * I * 2);
+  L.o = off; off += al(P * H * 2);
+  L.total = off;
+  return L;
+}
+
+static MoeRoute moe_route_ptrs(void *ws, const MoeLayout &L) {
+  uint8_t *b = (uint8_t *)ws;
+  return MoeRoute{(int32_t *)(b + L.ids), (float *)(b + L.w), (int32_t *)(b + L.count),
+                  (int32_t *)(b + L.active), (int32_t *)(b + L.offs), (int32_t *)(b + L.pair_tok),
+                  (int32_t *)(b + L.inv)};
+}
+
+static int ks_for(int tiles, int nblk) {
+  int ks = 1;
+  while (ks < 16 && ks < nblk && tiles * ks < 256 * 16) ks *= 2;
+  return ks;
+}
+
+template <class F>
+static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void *gate,
+                   const void *up, const void *down, MoeRoute R, uint16_t *h, uint16_t *o, void *y,
+                   hipStream_t st) {
+  const int amax = std::min(E, T * k);
+  int ks = ks_for((I / 16) * amax, H / F::BS);
+  hipLaunchKernelGGL((moe_gate_up_kernel<F>), dim3(I / 16, amax), dim3(64 * ks), (size_t)ks * 2 * 256 * 4, st,
+                     (const uint16_t *)x, H, (const uint8_t *)gate, (const uint8_t *)up, I, R, h);
+  ISHZ_LAUNCH_CHECK("moe gate/up launch");
+  ks = ks_for((H / 32) * amax, I / F::BS);
+  hipLaunchKernelGGL((moe_down_kernel<F>), dim3((H + 31) / 32, amax), dim3(64 * ks), (size_t)ks * 2 * 256 * 4,
+                     st, h, I, (const uint8_t *)down, H, R, o);
+  ISHZ_LAUNCH_CHECK("moe down launch");
+  const size_t total = (size_t)T * H;
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)std::min<size_t>((total + 255) / 256, 4096)), dim3(256), 0,
+                     st, o, H, T, k, R, (uint16_t *)y);
+  ISHZ_LAUNCH_CHECK("moe combine launch");
+  return ISHZ_OK;
+}
+
+}  // namespace ishz
+
+using namespace ishz;
+
+extern "C" size_t ishz_moe_workspace_size(int T, int H, int E, int I, int topk) {
+  return moe_layout(T, H, E, I, topk).total;
+}
+
+extern "C" int ishz_moe_route(const float *logits, int T, int E, int topk, int normalize,
+                              int32_t *ids, float *weights, ishz_stream_t stream) {
+  if (T <= 0 || E <= 0 || topk <= 0 || topk > E || E > 4096) return decline("bad routing shape");
+  if (!logits || !ids || !weights) return einval("null pointer");
+  MoeRoute R{ids, weights, nullptr, nullptr, nullptr, nullptr, nullptr};
+  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(1024), (size_t)E * 4, S(stream), logits, T, E,
+                     topk, normalize, R);
+  ISHZ_LAUNCH_CHECK("moe route launch");
+  return ISHZ_OK;
+}
+
+extern "C" int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T, int H,
+                               const float *logits, int E, int topk, int normalize,
+                               const void *gate, const void *up, const void *down,
+                               size_t expert_bytes, int I, void *y, int32_t *ids_out,
+                               float *weights_out, void *workspace, size_t workspace_bytes,
+                               ishz_stream_t stream) {
+  const int bs = ishz_ggml_block_size(type);
+  if (type != ISHZ_GGML_Q4_K && type != ISHZ_GGML_Q6_K && type != ISHZ_GGML_Q4_0)
+    return decline("MoE experts must be Q4_0, Q4_K or Q6_K");
+  if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
+  if (T <= 0 || E <= 0 || topk <= 0 || topk > E || E > 4096) return decline("bad routing shape");
+  if (H <= 0 || I <= 0 || H % bs || I % bs) return decline("H and I must be whole blocks");
+  const size_t need = (size_t)I * (H / bs) * ishz_ggml_type_size(type);
+  if (expert_bytes < need || (size_t)H * (I / bs) * ishz_ggml_type_size(type) > expert_bytes)
+    return decline("expert buffers too short");
+  if (!x || !logits || !gate || !up || !down || !y) return einval("null pointer");
+  const MoeLayout L = moe_layout(T, H, E, I, topk);
+  if (!workspace || workspace_bytes < L.total) return einval("workspace too small (ishz_moe_workspace_size)");
+  MoeRoute R = moe_route_ptrs(workspace, L);
+  hipStream_t st = S(stream);
+  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(1024), (size_t)E * 4, st, logits, T, E, topk,
+                     normalize, R);
+  ISHZ_LAUNCH_CHECK("moe route launch");
+  uint16_t *h = (uint16_t *)((uint8_t *)workspace + L.h), *o = (uint16_t *)((uint8_t *)workspace + L.o);
+  int rc;
+  switch (type) {
+  case ISHZ_GGML_Q4_K: rc = moe_ffn<FQ4_K>(x, T, H, E, I, topk, gate, up, down, R, h, o, y, st); break;
+  case ISHZ_GGML_Q6_K: rc = moe_ffn<FQ6_K>(x, T, H, E, I, topk, gate, up, down, R, h, o, y, st); break;
+  default: rc = moe_ffn<FQ4_0>(x, T, H, E, I, topk, gate, up, down, R, h, o, y, st); break;
+  }
+  if (rc) return rc;
+  if (ids_out && hipMemcpyAsync(ids_out, R.ids, (size_t)T * topk * 4, hipMemcpyDeviceToDevice, st) != hipSuccess)
+    return fail("moe ids copy", hipGetLastError());
+  if (weights_out && hipMemcpyAsync(weights_out, R.w, (size_t)T * topk * 4, hipMemcpyDeviceToDevice, st) != hipSuccess)
+    return fail("moe weights copy", hipGetLastError());
+  return ISHZ_OK;
+}

@@ -617,7 +617,9 @@ void ishzo_moe_route(const float *logits, int T, int E, int topk, int normalize,
       for (int e = 0; e < E; e++) {
         int used = 0;
         for (int q = 0; q < s; q++) used |= ids[(size_t)t * topk + q] == e;
-        if (!used && (best < 0 || g[e] > g[best])) best = e;
+        /* softmax is strictly increasing in the logit, so ranking logits picks the same top-k
+           as argPartition over the probabilities, without rounding ties */
+        if (!used && (best < 0 || l[e] > l[best])) best = e;
       }
       ids[(size_t)t * topk + s] = best;
       weights[(size_t)t * topk + s] = g[best];
