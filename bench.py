@@ -1,0 +1,276 @@
+"""Benchmark of the quantized-weight matmul path on one MI355X.
+
+Headline (BASELINE.json metric "weight-stream GB/s (% HBM peak) + us per quant matmul at M=1 and
+M=8", configs[1]): one step = one rotated MLX-affine 2-bit projection (Ternary Bonsai 27B style,
+17408 x 5120, group 64, 128-point Walsh-Hadamard on the input fused into the GEMV) at M=1, over
+synthetic seeded weights already resident in HBM. value = algorithmic weight-stream bytes / time
+per call (GB/s, 1e9). The weights rotate through >= 512 MB of copies so the 256 MB Infinity Cache
+cannot serve them. Calls are captured once into a HIP graph and replayed, so the timed region
+holds kernel time, not Python launch overhead.
+
+Also printed (same JSON line, "families"): us/call and GB/s at M = 1 and 8 for every family at
+17408 x 5120 (Q4_0, Q4_K, Q6_K, IQ2_XS, affine g64 + WHT, EXL3 2 bpw), the MoE FFN, and, with
+--all, every BASELINE config. cpu_baseline: the CPU oracle (dequantize-then-fp32-dot, OpenMP on
+all host cores) on a bounded row sample of the headline workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12
+CACHE_DEFEAT = 600e6
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--all", action="store_true", help="every BASELINE config, not just 17408x5120")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="comma list of family names to run (debug)")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the kernels shard by "
+              "output rows; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from ishizuki_amd import affine, exl3, ggml, moe, synth
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    def copies_of(nbytes):
+        return max(2, int(np.ceil(CACHE_DEFEAT / max(nbytes, 1))))
+
+    def timed(calls, steps, warmup):
+        """Capture one pass over `calls` (one per weight copy) in a HIP graph; replay until
+        `steps` calls ran. Returns seconds per call (events on the capture stream)."""
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for c in calls:  # first call outside capture (lazy init), checks the result exists
+                c()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for c in calls:
+                c()
+        reps = max(1, (steps + len(calls) - 1) // len(calls))
+        wreps = max(1, (warmup + len(calls) - 1) // len(calls))
+        for _ in range(wreps):
+            g.replay()
+        torch.cuda.synchronize()
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st.record()
+        for _ in range(reps):
+            g.replay()
+        en.record()
+        torch.cuda.synchronize()
+        return st.elapsed_time(en) * 1e-3 / (reps * len(calls)), reps * len(calls)
+
+    # ------------------------------------------------------------------ workloads
+    def ggml_case(t, N, K, M, seed=1):
+        blk = torch.from_numpy(synth.ggml_blocks(t, N, K, seed=seed)).to(dev)
+        nb = blk.numel()
+        ws = [blk] + [blk.clone() for _ in range(copies_of(nb) - 1)]
+        x = torch.from_numpy(synth.fp16_normal((M, K), seed=seed + 1)).to(dev)
+        y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        L = ggml._lib.lib()
+        from ishizuki_amd._torch import ptr
+        calls = [lambda w=w: L.ishz_ggml_matvec(t, ptr(x), 1, M, K, ptr(w), nb, N, ptr(y),
+                                                torch.cuda.current_stream().cuda_stream) for w in ws]
+        return calls, nb, nb + 2 * M * (K + N)
+
+    def affine_case(N, K, M, seed=2):
+        codes, s, b = synth.affine_pack(N, K, group=64, seed=seed)
+        c0 = torch.from_numpy(codes.view(np.int32)).to(dev)
+        s0, b0 = torch.from_numpy(s).to(dev), torch.from_numpy(b).to(dev)
+        nb = c0.numel() * 4 + s0.numel() * 2 + b0.numel() * 2
+        sets = [(c0, s0, b0)] + [(c0.clone(), s0.clone(), b0.clone()) for _ in range(copies_of(nb) - 1)]
+        x = torch.from_numpy(synth.fp16_normal((M, K), seed=seed + 1)).to(dev)
+        signs = torch.from_numpy(synth.hadamard_signs(K, seed=seed + 2)).to(dev)
+        y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        L = affine._lib.lib()
+        from ishizuki_amd._torch import ptr
+        wsb = L.ishz_affine_workspace_size(M, K)
+        wsp = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+        calls = [lambda c=c, sc=sc, bi=bi: L.ishz_affine_linear(
+            ptr(x), 1, M, K, ptr(signs), 128, ptr(c), ptr(sc), ptr(bi), 1, N, 2, 64, ptr(y), ptr(wsp), wsb,
+            torch.cuda.current_stream().cuda_stream) for c, sc, bi in sets]
+        return calls, nb, nb + 2 * M * (K + N)
+
+    def exl3_case(K, N, M, bits2=4, seed=3):
+        t, suh, svh = synth.exl3_pack(K, N, bits2=bits2, seed=seed)
+        t0 = torch.from_numpy(t).to(dev)
+        su, sv = torch.from_numpy(suh).to(dev), torch.from_numpy(svh).to(dev)
+        nb = t0.numel() * 2
+        ts = [t0] + [t0.clone() for _ in range(copies_of(nb) - 1)]
+        x = torch.from_numpy(synth.fp16_normal((M, K), seed=seed + 1)).to(dev)
+        y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        L = exl3._lib.lib()
+        from ishizuki_amd._torch import ptr
+        wsb = L.ishz_exl3_workspace_size(M, K, N)
+        wsp = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        calls = [lambda tt=tt: L.ishz_exl3_apply(ptr(x), 1, M, K, ptr(tt), ptr(su), ptr(sv), N, bits2, 0, ptr(y),
+                                                 ptr(wsp), wsb, torch.cuda.current_stream().cuda_stream) for tt in ts]
+        return calls, nb + 2 * (K + N), nb + 2 * (K + N) + 2 * M * (K + N)
+
+    def moe_case(T, E=128, H=2048, I=768, k=8, seed=4):
+        gate = synth.ggml_blocks(ggml.Q4_K, E * I, H, seed=seed)
+        up = synth.ggml_blocks(ggml.Q4_K, E * I, H, seed=seed + 1)
+        down = synth.ggml_blocks(ggml.Q4_K, E * H, I, seed=seed + 2)
+        ex = moe.GGMLExperts(*(torch.from_numpy(a).to(dev) for a in (gate, up, down)), ggml.Q4_K, E, H, I)
+        pool = 3 * ex.expert_bytes * E
+        exs = [ex] + [moe.GGMLExperts(ex.gate.clone(), ex.up.clone(), ex.down.clone(), ggml.Q4_K, E, H, I)
+                      for _ in range(copies_of(pool) - 1)]
+        x = torch.from_numpy(synth.fp16_normal((T, H), seed=seed + 3)).to(dev)
+        logits_np = np.random.default_rng(seed + 5).standard_normal((T, E)).astype(np.float32)
+        logits = torch.from_numpy(logits_np).to(dev)
+        # distinct experts this seed routes to (top-k of the logits = top-k of the softmax)
+        distinct = len(np.unique(np.argsort(-logits_np, axis=1, kind="stable")[:, :k]))
+        y = torch.empty((T, H), dtype=torch.float16, device=dev)
+        L = moe._lib.lib()
+        from ishizuki_amd._torch import ptr
+        wsb = L.ishz_moe_workspace_size(T, H, E, I, k)
+        wsp = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        calls = [lambda e=e: L.ishz_moe_swiglu(ggml.Q4_K, ptr(x), 1, T, H, ptr(logits), E, k, 1, ptr(e.gate),
+                                               ptr(e.up), ptr(e.down), e.expert_bytes, I, ptr(y), None, None,
+                                               ptr(wsp), wsb, torch.cuda.current_stream().cuda_stream) for e in exs]
+        nb = distinct * 3 * ex.expert_bytes
+        return calls, nb, nb, distinct
+
+    def measure(name, builder, M, steps, warmup, extra=None):
+        out = builder()
+        calls, wbytes, allbytes = out[0], out[1], out[2]
+        sec, n = timed(calls, steps, warmup)
+        r = {"name": name, "M": M, "us": round(sec * 1e6, 3), "weight_bytes": int(wbytes),
+             "GBps": round(wbytes / sec / 1e9, 1), "hbm_frac": round(wbytes / sec / HBM_PEAK, 4)}
+        if extra:
+            r.update(extra(out))
+        del out, calls
+        torch.cuda.empty_cache()
+        return r, sec, n
+
+    only = set(filter(None, args.only.split(",")))
+    NS, KS = 17408, 5120
+    families = []
+
+    # headline: rotated affine 2-bit, M=1
+    head, head_sec, head_n = measure("affine2_g64_wht128", lambda: affine_case(NS, KS, 1), 1, args.steps, args.warmup)
+
+    plan = [
+        ("q4_0", lambda M: ggml_case(ggml.Q4_0, NS, KS, M)),
+        ("q4_k", lambda M: ggml_case(ggml.Q4_K, NS, KS, M)),
+        ("q6_k", lambda M: ggml_case(ggml.Q6_K, NS, KS, M)),
+        ("iq2_xs", lambda M: ggml_case(ggml.IQ2_XS, NS, KS, M)),
+        ("affine2_g64_wht128", lambda M: affine_case(NS, KS, M)),
+        ("exl3_2bpw", lambda M: exl3_case(KS, NS, M)),
+    ]
+    fam_steps = max(50, args.steps // 2)
+    for name, b in plan:
+        if only and name not in only:
+            continue
+        for M in (1, 8):
+            r, _, _ = measure(f"{name}", lambda b=b, M=M: b(M), M, fam_steps, args.warmup)
+            r["shape"] = f"{NS}x{KS}"
+            families.append(r)
+    if not only or "moe" in only:
+        for T in (1, 8, 64):
+            r, _, _ = measure("moe_q4k_e128_h2048_i768_top8", lambda T=T: moe_case(T), T, fam_steps, args.warmup,
+                              extra=lambda o: {"distinct_experts": int(o[3])})
+            families.append(r)
+    if args.all:
+        for M in (1,):
+            r, _, _ = measure("q4_0_cfg0", lambda: ggml_case(ggml.Q4_0, 4096, 4096, 1), 1, fam_steps, args.warmup)
+            r["shape"] = "4096x4096"
+            families.append(r)
+        for t, nm in ((ggml.Q4_K, "q4_k"), (ggml.Q6_K, "q6_k"), (ggml.IQ2_XS, "iq2_xs")):
+            for (N, K) in ((25600, 5120), (5120, 25600)):
+                for M in (1, 8):
+                    r, _, _ = measure(f"{nm}_mlp", lambda t=t, N=N, K=K, M=M: ggml_case(t, N, K, M), M, fam_steps,
+                                      args.warmup)
+                    r["shape"] = f"{N}x{K}"
+                    families.append(r)
+        for M in (2, 4):
+            r, _, _ = measure("affine2_g64_wht128", lambda M=M: affine_case(NS, KS, M), M, fam_steps, args.warmup)
+            families.append(r)
+            r, _, _ = measure("exl3_2bpw", lambda M=M: exl3_case(KS, NS, M), M, fam_steps, args.warmup)
+            families.append(r)
+
+    # ------------------------------------------------------------------ CPU baseline
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        threads = os.cpu_count() or 1
+        rows = 2048
+        codes, s, b = synth.affine_pack(rows, KS, group=64, seed=2)
+        x = synth.fp16_normal((1, KS), seed=3).astype(np.float32)
+        xr = oracle.hadamard(x, 128, synth.hadamard_signs(KS, seed=4)).astype(np.float16).astype(np.float32)
+        oracle.affine_matmul(xr, codes, s.view(np.uint16), b.view(np.uint16), rows, 2, 64, threads=threads)
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < 10.0 and reps < 200:
+            xr = oracle.hadamard(x, 128, synth.hadamard_signs(KS, seed=4)).astype(np.float16).astype(np.float32)
+            oracle.affine_matmul(xr, codes, s.view(np.uint16), b.view(np.uint16), rows, 2, 64, threads=threads)
+            reps += 1
+        dt = (time.perf_counter() - t0) / reps
+        row_bytes = KS // 4 + 2 * 2 * (KS // 64)
+        cpu = {"value": round(rows * row_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"oracle rotate + dequantize-then-fp32-dot of {rows} of {NS} rows (K={KS}, M=1), "
+                         f"{reps} reps over {dt * reps:.1f} s, OpenMP {threads} threads"}
+
+    us = head_sec * 1e6
+    line = {
+        "metric": "weight-stream GB/s (% HBM peak) + us per quant matmul at M=1 and M=8",
+        "value": head["GBps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": head_n,
+        "warmup": args.warmup,
+        "ms_per_step": round(us / 1000, 6),
+        "us_per_call": round(us, 3),
+        "hbm_frac": head["hbm_frac"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 activations, 2-bit affine codes (fp32 accumulate)",
+        "data": "synthetic (seeded): BASELINE configs[1] distributions",
+        "config": {"workload": "MLX affine 2-bit g64 + 128-pt WHT GEMV, 17408x5120, M=1 (BASELINE configs[1])",
+                   "N": NS, "K": KS, "M": 1, "group": 64, "hadamard_block": 128,
+                   "weight_bytes": head["weight_bytes"], "cache_defeat_bytes": int(CACHE_DEFEAT)},
+        "roofline": {"bound": "hbm", "achieved": round(head["weight_bytes"] / head_sec / 1e9, 1),
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": head["hbm_frac"],
+                     "traffic": _traffic()},
+        "cpu_baseline": cpu,
+        "families": families,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def _traffic():
+    """HBM bytes per launch of the headline kernel, from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel of known size), or None if absent."""
+    p = os.path.join(ROOT, "profiles", "traffic_affine2_gemv_17408x5120.json")
+    if not os.path.exists(p):
+        return None
+    try:
+        return json.load(open(p)).get("bytes_per_launch")
+    except Exception:
+        return None
+
+
+if __name__ == "__main__":
+    main()
