@@ -36,7 +36,7 @@ DEV void lds_wht(float *v, int width, int block, const float *signs, bool invers
   __syncthreads();
   for (int h = 1; h < block; h <<= 1) {
     for (int p = threadIdx.x; p < width / 2; p += blockDim.x) {
-      const int i = (p / h) * 2 * h + (p % h);  // butterfly (i, i + h) inside one block
+      const int i = ((p & ~(h - 1)) << 1) | (p & (h - 1));  // butterfly (i, i + h), h a power of 2
       const float a = v[i], c = v[i + h];
       v[i] = a + c;
       v[i + h] = a - c;
@@ -66,17 +66,57 @@ DEV void store_act(void *y, size_t i, int dt, float v) {
   }
 }
 
-// hadamardRotate as a kernel: one workgroup per row, fp32 in LDS, output in `out_dt`.
+// hadamardRotate as a kernel. Blocks up to 128: one wave per 128 contiguous values, two per
+// lane, butterflies across lanes by shuffles (stages above the block size skipped). Larger
+// blocks: one workgroup per block, in LDS. fp32 math, output in `out_dt`.
+__global__ __launch_bounds__(256) void hadamard_wave_kernel(const void *__restrict__ x, int in_dt,
+                                                            size_t chunks, int width, int block,
+                                                            const float *__restrict__ signs,
+                                                            int inverse, void *__restrict__ y,
+                                                            int out_dt) {
+  const size_t c = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (c >= chunks) return;
+  const int lane = threadIdx.x & 63;
+  const size_t base = c * 128 + 2 * lane;
+  const int col = (int)(base % width);
+  float v0 = load_act(x, base, in_dt), v1 = load_act(x, base + 1, in_dt);
+  if (signs && !inverse) {
+    v0 *= signs[col];
+    v1 *= signs[col + 1];
+  }
+  if (block >= 2) {
+    const float a = v0 + v1, b = v0 - v1;
+    v0 = a;
+    v1 = b;
+  }
+  for (int m = 1; 2 * m < block; m <<= 1) {
+    const float p0 = __shfl_xor(v0, m, 64), p1 = __shfl_xor(v1, m, 64);
+    const bool hi = (lane & m) != 0;
+    v0 = hi ? p0 - v0 : v0 + p0;
+    v1 = hi ? p1 - v1 : v1 + p1;
+  }
+  const float scale = 1.0f / __builtin_sqrtf((float)block);
+  v0 *= scale;
+  v1 *= scale;
+  if (signs && inverse) {
+    v0 *= signs[col];
+    v1 *= signs[col + 1];
+  }
+  store_act(y, base, out_dt, v0);
+  store_act(y, base + 1, out_dt, v1);
+}
+
 __global__ __launch_bounds__(256) void hadamard_kernel(const void *__restrict__ x, int in_dt,
                                                        int width, int block,
                                                        const float *__restrict__ signs,
                                                        int inverse, void *__restrict__ y,
                                                        int out_dt) {
   extern __shared__ float hv[];
-  const size_t base = (size_t)blockIdx.x * width;
-  for (int i = threadIdx.x; i < width; i += blockDim.x) hv[i] = load_act(x, base + i, in_dt);
-  lds_wht(hv, width, block, signs, inverse != 0);
-  for (int i = threadIdx.x; i < width; i += blockDim.x) store_act(y, base + i, out_dt, hv[i]);
+  const size_t base = (size_t)blockIdx.x * block;
+  const int col = (int)(base % width);
+  for (int i = threadIdx.x; i < block; i += blockDim.x) hv[i] = load_act(x, base + i, in_dt);
+  lds_wht(hv, block, block, signs ? signs + col : nullptr, inverse != 0);
+  for (int i = threadIdx.x; i < block; i += blockDim.x) store_act(y, base + i, out_dt, hv[i]);
 }
 
 // ------------------------------------------------------------------- GEMV (M = 1)
@@ -145,28 +185,36 @@ __global__ __launch_bounds__(256) void affine_gemv(const uint16_t *__restrict__ 
       uint32_t d[4];
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const int p = p0 + j;
-        const float inv = 1.0f / pair_div(p);
-        d[j] = (uint32_t)f2h(xv(kw + p) * inv) | (uint32_t)f2h(xv(kw + p + 8) * inv) << 16;
+        const int e = -2 * ((p0 + j) < 5 ? (p0 + j) : (p0 + j) - 5);  // x / 4^i, exact
+        d[j] = (uint32_t)f2h(__builtin_ldexpf(xv(kw + p0 + j), e)) |
+               (uint32_t)f2h(__builtin_ldexpf(xv(kw + p0 + j + 8), e)) << 16;
       }
       slots[i] = u4{d[0], d[1], d[2], d[3]};
     }
   }
-  for (int i = threadIdx.x; i < ug * 16 * 2; i += blockDim.x) {
-    const int u = (i / 32) * 16 + (i & 15), q = (i >> 4) & 1;
+  __syncthreads();
+  // Per unit: C = 1024 * sum of its 64 staged x' (the code offset) and X = sum of x (for the
+  // bias), read back from the slots in a fixed order.
+  for (int i = threadIdx.x; i < ug * 16; i += blockDim.x) {
+    const int u = (i / 16) * 16 + (i & 15);
     if (u < units) {
-      float s = 0.0f;
-      for (int k = 0; k < 64; k++) {
-        const float v = xv(64 * u + k);
-        if (q == 0) {
-          const int p = k & 15;  // position in word; pair index of x[k]
-          const int pi = p < 8 ? p : p - 8;
-          s += (float)(_Float16)(v / pair_div(pi));
-        } else {
-          s += v;
+      const u4 *sl = slots + (u >> 4) * 128 + (u & 15);
+      float c = 0.0f, xs = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 8; r++) {
+        const u4 v = sl[r * 16];
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+          const int p = (r & 1) * 4 + d;
+          const h2 hv = as_h2(v[d]);
+          const float pr = (float)hv.x + (float)hv.y;
+          c += pr;
+          xs += __builtin_ldexpf(pr, 2 * (p < 5 ? p : p - 5));
         }
       }
-      sums[i] = q == 0 ? 1024.0f * s : s;
+      float *sm = sums + (u >> 4) * 32 + (u & 15);
+      sm[0] = 1024.0f * c;
+      sm[16] = xs;
     }
   }
   __syncthreads();
@@ -403,10 +451,16 @@ extern "C" int ishz_hadamard(const void *x, int dtype, int rows, int width, int 
   if (dtype < ISHZ_DT_F32 || dtype > ISHZ_DT_BF16) return decline("unsupported dtype");
   if (!pow2(block) || block > 4096) return decline("block must be a power of two <= 4096");
   if (rows <= 0 || width <= 0 || width % block) return einval("block does not divide the width");
-  if ((size_t)width * 4 > 64 * 1024) return decline("width too large for one workgroup");
   if (!x || !y) return einval("null pointer");
-  hipLaunchKernelGGL(hadamard_kernel, dim3(rows), dim3(256), (size_t)width * 4, S(stream), x, dtype,
-                     width, block, signs, inverse, y, dtype);
+  if (block <= 128) {
+    if (width % 128) return decline("width must be a multiple of 128 for blocks up to 128");
+    const size_t chunks = (size_t)rows * width / 128;
+    hipLaunchKernelGGL(hadamard_wave_kernel, dim3((unsigned)((chunks + 3) / 4)), dim3(256), 0, S(stream), x,
+                       dtype, chunks, width, block, signs, inverse, y, dtype);
+  } else {
+    hipLaunchKernelGGL(hadamard_kernel, dim3((unsigned)((size_t)rows * width / block)), dim3(256),
+                       (size_t)block * 4, S(stream), x, dtype, width, block, signs, inverse, y, dtype);
+  }
   ISHZ_LAUNCH_CHECK("hadamard launch");
   return ISHZ_OK;
 }

@@ -27,67 +27,96 @@ struct MoeRoute {
   int32_t *inv;       // [T*k] sorted position of (t, s)
 };
 
-// One workgroup of 1024 threads.
+// One workgroup of 1024 threads. Routing: one wave per token (lanes over experts), the top-k by
+// k rounds of a wave-wide arg-max in (logit desc, index asc) order. Pair lists: per-expert counts
+// in LDS, a prefix over experts, then each pair placed at offs[e] + (its rank among earlier pairs
+// of e), so the order inside an expert is (token, slot) and deterministic.
+DEV void argmax_merge(float &v, int &e, float ov, int oe) {
+  if (oe >= 0 && (e < 0 || ov > v || (ov == v && oe < e))) {
+    v = ov;
+    e = oe;
+  }
+}
+
 __global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict__ logits, int T,
                                                          int E, int k, int normalize, MoeRoute R) {
   extern __shared__ int32_t cnt[];  // E counts
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
   for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
   __syncthreads();
-  for (int t = threadIdx.x; t < T; t += blockDim.x) {
+  for (int t = wave; t < T; t += waves) {
     const float *l = logits + (size_t)t * E;
-    float mx = l[0];
-    for (int e = 1; e < E; e++) mx = fmaxf(mx, l[e]);
+    float mx = -INFINITY;
+    for (int e = lane; e < E; e += 64) mx = fmaxf(mx, l[e]);
+    for (int m = 32; m; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
     float sum = 0.0f;
-    for (int e = 0; e < E; e++) sum += expf(l[e] - mx);
-    float tot = 0.0f;
-    int prev_best = -1;
-    float prev_val = INFINITY;
+    for (int e = lane; e < E; e += 64) sum += expf(l[e] - mx);
+    for (int m = 32; m; m >>= 1) sum += __shfl_xor(sum, m, 64);
+    float prev_v = INFINITY, tot = 0.0f, wsel = 0.0f;
+    int prev_e = -1;
     for (int s = 0; s < k; s++) {
-      // next largest logit strictly after (prev_val, prev_best) in (value desc, index asc) order
-      int best = -1;
       float bv = -INFINITY;
-      for (int e = 0; e < E; e++) {
+      int be = -1;
+      for (int e = lane; e < E; e += 64) {
         const float v = l[e];
-        const bool after = v < prev_val || (v == prev_val && e > prev_best);
-        if (after && (best < 0 || v > bv)) {
-          best = e;
-          bv = v;
-        }
+        if (v < prev_v || (v == prev_v && e > prev_e)) argmax_merge(bv, be, v, e);
+      }
+      for (int m = 32; m; m >>= 1) {
+        const float ov = __shfl_xor(bv, m, 64);
+        const int oe = __shfl_xor(be, m, 64);
+        argmax_merge(bv, be, ov, oe);
       }
       const float p = expf(bv - mx) / sum;
-      R.ids[t * k + s] = best;
-      R.w[t * k + s] = p;
+      if (lane == s) wsel = p;
       tot += p;
-      prev_best = best;
-      prev_val = bv;
-      if (R.offs) atomicAdd(&cnt[best], 1);
+      prev_v = bv;
+      prev_e = be;
+      if (lane == 0) {
+        R.ids[t * k + s] = be;
+        if (R.offs) atomicAdd(&cnt[be], 1);
+      }
     }
-    if (normalize)
-      for (int s = 0; s < k; s++) R.w[t * k + s] /= tot;
+    if (lane < k) R.w[t * k + lane] = normalize ? wsel / tot : wsel;
   }
   if (!R.offs) return;  // routing only
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int off = 0, na = 0;
-    for (int e = 0; e < E; e++) {
-      R.offs[e] = off;
-      if (cnt[e]) R.active[na++] = e;
-      off += cnt[e];
-    }
-    R.offs[E] = off;
-    R.count[0] = na;
-  }
-  __syncthreads();
-  // stable placement: expert e's pairs in (t, s) order
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    int pos = R.offs[e];
-    if (!cnt[e]) continue;
-    for (int q = 0; q < T * k; q++)
-      if (R.ids[q] == e) {
-        R.pair_tok[pos] = q / k;
-        R.inv[q] = pos;
-        pos++;
+  // exclusive prefix of the counts by wave 0 (64 experts per round), active list by rank
+  int32_t *ids_l = cnt + E;  // T*k ids copied to LDS for the placement below
+  if (wave == 0) {
+    int carry = 0, nact = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + lane;
+      const int c = e < E ? cnt[e] : 0;
+      int incl = c, act = c > 0;
+      for (int m = 1; m < 64; m <<= 1) {
+        const int v = __shfl_up(incl, m, 64), a2 = __shfl_up(act, m, 64);
+        if (lane >= m) {
+          incl += v;
+          act += a2;
+        }
       }
+      if (e < E) {
+        R.offs[e] = carry + incl - c;
+        if (c) R.active[nact + act - 1] = e;
+      }
+      carry += __shfl(incl, 63, 64);
+      nact += __shfl(act, 63, 64);
+    }
+    if (lane == 0) {
+      R.offs[E] = carry;
+      R.count[0] = nact;
+    }
+  }
+  const int P = T * k;
+  for (int q = threadIdx.x; q < P; q += blockDim.x) ids_l[q] = R.ids[q];
+  __syncthreads();
+  for (int q = threadIdx.x; q < P; q += blockDim.x) {
+    const int e = ids_l[q];
+    int rank = 0;
+    for (int q2 = 0; q2 < q; q2++) rank += ids_l[q2] == e;
+    const int pos = R.offs[e] + rank;
+    R.pair_tok[pos] = q / k;
+    R.inv[q] = pos;
   }
 }
 
@@ -273,6 +302,7 @@ extern "C" int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T,
     return decline("MoE experts must be Q4_0, Q4_K or Q6_K");
   if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
   if (T <= 0 || E <= 0 || topk <= 0 || topk > E || E > 4096) return decline("bad routing shape");
+  if ((size_t)(E + T * topk) * 4 > 64 * 1024) return decline("too many tokens for one routing workgroup");
   if (H <= 0 || I <= 0 || H % bs || I % bs) return decline("H and I must be whole blocks");
   const size_t need = (size_t)I * (H / bs) * ishz_ggml_type_size(type);
   if (expert_bytes < need || (size_t)H * (I / bs) * ishz_ggml_type_size(type) > expert_bytes)
@@ -282,8 +312,8 @@ extern "C" int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T,
   if (!workspace || workspace_bytes < L.total) return einval("workspace too small (ishz_moe_workspace_size)");
   MoeRoute R = moe_route_ptrs(workspace, L);
   hipStream_t st = S(stream);
-  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(1024), (size_t)E * 4, st, logits, T, E, topk,
-                     normalize, R);
+  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(1024), (size_t)(E + T * topk) * 4, st, logits, T,
+                     E, topk, normalize, R);
   ISHZ_LAUNCH_CHECK("moe route launch");
   uint16_t *h = (uint16_t *)((uint8_t *)workspace + L.h), *o = (uint16_t *)((uint8_t *)workspace + L.o);
   int rc;
