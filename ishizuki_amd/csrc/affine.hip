@@ -15,6 +15,7 @@
 #include <cstdlib>
 
 #include "common.h"
+#include "gemv.h"
 
 namespace ishz {
 
@@ -120,158 +121,221 @@ __global__ __launch_bounds__(256) void hadamard_kernel(const void *__restrict__ 
 }
 
 // ------------------------------------------------------------------- GEMV (M = 1)
-// Unit = 64 weights = 16 bytes of codes (4 words) of one row; LPR lanes per row, 64/LPR rows per
-// wave, waves take equal shares of row groups and ping-pong two register batches of units (the
-// same streaming scheme as the GGML GEMV). With ROT, x is rotated in LDS before staging.
-constexpr int AFF_B = 4;  // units per batch
-
-struct AffRaw {
-  u4 q;
-  uint32_t s, b;
-};
-
-template <int GS, int LPR, bool ROT>
-__global__ __launch_bounds__(256) void affine_gemv(const uint16_t *__restrict__ x,
-                                                   const float *__restrict__ signs, int block,
-                                                   const uint32_t *__restrict__ codes,
-                                                   const uint16_t *__restrict__ scales,
-                                                   const uint16_t *__restrict__ biases, int bf16s,
-                                                   int K, int N, uint16_t *__restrict__ y,
-                                                   int groups_per_wave) {
-  extern __shared__ __align__(16) uint32_t smem[];
-  const int units = K / 64;
-  const int ug = (units + 15) / 16;
-  u4 *slots = (u4 *)smem;                      // ug*16*8 slots (R = 8)
-  float *sums = (float *)(slots + ug * 16 * 8);  // ug*16*2 (C offset, X plain)
-  float *xr = sums + ug * 16 * 2;              // K floats (rotated x), ROT only
-
-  constexpr int RPW = 64 / LPR, B = AFF_B;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int sub = lane % LPR, rg = lane / LPR;
-  const int nb = (units + B * LPR - 1) / (B * LPR);
-  const int gpr = K / GS;
-  const int gw = blockIdx.x * (blockDim.x >> 6) + wave;
-  const int g_end = min((gw + 1) * groups_per_wave, (N + RPW - 1) / RPW);
-  const int g_last = max(g_end - 1, 0);
-
-  auto load_batch = [&](int g, int bi, AffRaw *r) {
-    const int row = min(min(g, g_last) * RPW + rg, N - 1);
-    const uint32_t *cr = codes + (size_t)row * (K / 16);
-    const uint16_t *sr = scales + (size_t)row * gpr, *br = biases + (size_t)row * gpr;
-#pragma unroll
-    for (int i = 0; i < B; i++) {
-      const int u = min(sub + (bi * B + i) * LPR, units - 1);
-      r[i].q = *(const u4 *)(cr + 4 * u);
-      r[i].s = sr[(64 * u) / GS];
-      r[i].b = br[(64 * u) / GS];
-    }
+// Format for the shared streaming GEMV skeleton. Unit = 64 weights = 16 bytes of codes (4 words)
+// of one row, with its group's scale and bias. Slot r of a unit is word t = r / 2, pairs
+// p = 4 (r % 2) .. +3: the x at offsets p and p + 8 of the word's 16, divided by 4^i of the pair.
+// Sums: 0 = 1024 * the unit's staged x' (the code offset), 1 = the unit's plain x (the bias).
+template <int GS, bool BF16S>
+struct FAffine {
+  struct Args {
+    const uint32_t *codes;
+    const uint16_t *scales, *biases;
+    const float *signs;
+    int block;  // Hadamard block (0: x is not rotated)
+    int K, N;
   };
-  int g = gw * groups_per_wave, bi = 0;
-  AffRaw cur[B], alt[B];
-  load_batch(g, 0, cur);
-
-  // ---- stage x (rotated first when ROT): slots of x / 4^i, per-unit offset and plain sums
-  if constexpr (ROT) {
-    for (int i = threadIdx.x; i < K; i += blockDim.x) xr[i] = h2f(x[i]);
-    lds_wht(xr, K, block, signs, false);
-    for (int i = threadIdx.x; i < K; i += blockDim.x) xr[i] = (float)(_Float16)xr[i];  // x.dtype
-    __syncthreads();
+  struct Raw {
+    u4 q;
+    uint32_t s, b;
+  };
+  struct LaneC {};
+  static constexpr int R = 8, Q = 2, MAXB = 5, PREFB = 5, GRID_ENTRIES = 0;
+  static __host__ __device__ int units(int K) { return K / 64; }
+  // Blocks above 128 are rotated in an LDS copy of x (one fp32 per element).
+  static size_t extra_lds_bytes(const Args &a) { return a.block > 128 ? (size_t)a.K * 4 : 0; }
+  static DEV LaneC lane(int) { return {}; }
+  static DEV Raw load(const Args &a, int row, int u) {
+    const size_t g = (size_t)row * (a.K / GS) + (64 * u) / GS;
+    return {*(const u4 *)(a.codes + (size_t)row * (a.K / 16) + 4 * u), a.scales[g], a.biases[g]};
   }
-  auto xv = [&](int k) -> float { return ROT ? xr[k] : h2f(x[k]); };
-  for (int i = threadIdx.x; i < ug * 16 * 8; i += blockDim.x) {
-    const int u = (i / 128) * 16 + (i & 15), r = (i >> 4) & 7;  // slot r = word t = r/2, half
-    if (u < units) {
-      const int t = r >> 1, p0 = (r & 1) * 4, kw = 64 * u + 16 * t;
-      uint32_t d[4];
+
+  // Writes x[k], x[k + 1] (k even, already rotated and rounded to fp16) to their slots and
+  // returns their contributions to the unit's sums.
+  static DEV void put2(uint16_t *xh, int k, float v0, float v1, float &c, float &xsum) {
+    c = 0.0f;
+    xsum = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int e = -2 * ((p0 + j) < 5 ? (p0 + j) : (p0 + j) - 5);  // x / 4^i, exact
-        d[j] = (uint32_t)f2h(__builtin_ldexpf(xv(kw + p0 + j), e)) |
-               (uint32_t)f2h(__builtin_ldexpf(xv(kw + p0 + j + 8), e)) << 16;
-      }
-      slots[i] = u4{d[0], d[1], d[2], d[3]};
+    for (int e = 0; e < 2; e++) {
+      const float v = e ? v1 : v0;
+      const int kk = k + e, u = kk >> 6, w = kk & 63, q = w & 15, p = q & 7;
+      const int r = 2 * (w >> 4) + (p >> 2);
+      const uint16_t h = f2h(__builtin_ldexpf(v, -2 * (p < 5 ? p : p - 5)));  // x / 4^i, exact
+      xh[((u >> 4) * 16 * R + r * 16 + (u & 15)) * 8 + (p & 3) * 2 + (q >> 3)] = h;
+      c += h2f(h);
+      xsum += v;
     }
   }
-  __syncthreads();
-  // Per unit: C = 1024 * sum of its 64 staged x' (the code offset) and X = sum of x (for the
-  // bias), read back from the slots in a fixed order.
-  for (int i = threadIdx.x; i < ug * 16; i += blockDim.x) {
-    const int u = (i / 16) * 16 + (i & 15);
-    if (u < units) {
-      const u4 *sl = slots + (u >> 4) * 128 + (u & 15);
-      float c = 0.0f, xs = 0.0f;
-#pragma unroll
-      for (int r = 0; r < 8; r++) {
-        const u4 v = sl[r * 16];
-#pragma unroll
-        for (int d = 0; d < 4; d++) {
-          const int p = (r & 1) * 4 + d;
-          const h2 hv = as_h2(v[d]);
-          const float pr = (float)hv.x + (float)hv.y;
-          c += pr;
-          xs += __builtin_ldexpf(pr, 2 * (p < 5 ? p : p - 5));
-        }
-      }
-      float *sm = sums + (u >> 4) * 32 + (u & 15);
+  static DEV void put_sums(float *xsum, int k, float c, float xs) {
+    c = group_sum<32>(c);
+    xs = group_sum<32>(xs);
+    if ((threadIdx.x & 31) == 0) {
+      const int u = k >> 6;
+      float *sm = xsum + (u >> 4) * 16 * Q + (u & 15);
       sm[0] = 1024.0f * c;
       sm[16] = xs;
     }
   }
-  __syncthreads();
-  const uint32_t mg = vconst(0x64006400u);
 
-  float acc = 0.0f;
-  auto advance = [&](int &gg, int &bb) {
-    if (++bb == nb) {
-      bb = 0;
-      gg++;
-    }
-  };
-  auto consume = [&](int gg, int bb, const AffRaw *r) {
+  // x[k .. k + 7] (k % 8 == 0, rotated and rounded to fp16) of lane l and x[k ^ 8 ...] of lane
+  // l ^ 1 fill two slots of one code word: the lanes swap the halves the other writes (one DPP
+  // per dword pair), so each writes one whole 16-byte slot. Unit sums over 8 lanes by DPP.
+  static DEV void put8(u4 *xs, float *xsum, int k, const float *v, bool valid) {
+    const int t = (k >> 4) & 3, hf = (k >> 3) & 1, u = k >> 6;
+    uint32_t h[8];
+    float c = 0.0f, xsm = 0.0f;
 #pragma unroll
-    for (int i = 0; i < B; i++) {
-      const int u0 = sub + (bb * B + i) * LPR, u = min(u0, units - 1);
-      const u4 *sl = slots + (u >> 4) * 128 + (u & 15);
-      float S = 0.0f;
+    for (int p = 0; p < 8; p++) {
+      h[p] = f2h(__builtin_ldexpf(v[p], -2 * (p < 5 ? p : p - 5)));  // x / 4^i, exact
+      c += h2f(h[p]);
+      xsm += v[p];
+    }
+    // Selects by mask (a select between two elements of h would become a dynamic index, i.e.
+    // scratch memory).
+    const uint32_t hm = 0u - (uint32_t)hf;
+    uint32_t keep[4], send[2];
 #pragma unroll
-      for (int t = 0; t < 4; t++) {
-        const uint32_t w = r[i].q[t], w10 = w >> 10;
-        const u4 a = sl[(2 * t) * 16], c = sl[(2 * t + 1) * 16];
-        S = dot2(and_or(w, 0x00030003u, mg), a.x, S);
-        S = dot2(and_or(w, 0x000C000Cu, mg), a.y, S);
-        S = dot2(and_or(w, 0x00300030u, mg), a.z, S);
-        S = dot2(and_or(w, 0x00C000C0u, mg), a.w, S);
-        S = dot2(and_or(w, 0x03000300u, mg), c.x, S);
-        S = dot2(and_or(w10, 0x00030003u, mg), c.y, S);
-        S = dot2(and_or(w10, 0x000C000Cu, mg), c.z, S);
-        S = dot2(and_or(w10, 0x00300030u, mg), c.w, S);
-      }
-      const float *sm = sums + (u >> 4) * 32 + (u & 15);
-      const float v = ld_scale((const uint16_t *)&r[i].s, bf16s) * (S - sm[0]) +
-                      ld_scale((const uint16_t *)&r[i].b, bf16s) * sm[16];
-      acc += u0 < units ? v : 0.0f;
+    for (int j = 0; j < 4; j++) keep[j] = (h[4 + j] & hm) | (h[j] & ~hm);
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+      send[j] = ((h[2 * j] | h[2 * j + 1] << 16) & hm) | ((h[4 + 2 * j] | h[5 + 2 * j] << 16) & ~hm);
+    uint32_t rv[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+      rv[j] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)send[j], 0xB1, 0xf, 0xf, true);  // lane ^ 1
+    u4 o;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t r = (rv[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+      o[j] = hf ? (r | keep[j] << 16) : (keep[j] | r << 16);
     }
-    if (bb == nb - 1) {
-      acc = group_sum<LPR>(acc);
-      const int row = gg * RPW + rg;
-      if (sub == 0 && row < N) y[row] = f2h(acc);
-      acc = 0.0f;
+    if (valid) xs[(u >> 4) * 16 * R + (2 * t + hf) * 16 + (u & 15)] = o;
+    c = group_sum<8>(c);
+    xsm = group_sum<8>(xsm);
+    if (valid && (threadIdx.x & 7) == 0) {
+      float *sm = xsum + (u >> 4) * 16 * Q + (u & 15);
+      sm[0] = 1024.0f * c;
+      sm[16] = xsm;
     }
-  };
-  while (g < g_end) {
-    int g1 = g, b1 = bi;
-    advance(g1, b1);
-    load_batch(g1, b1, alt);
-    consume(g, bi, cur);
-    if (g1 >= g_end) break;
-    int g2 = g1, b2 = b1;
-    advance(g2, b2);
-    load_batch(g2, b2, cur);
-    consume(g1, b1, alt);
-    g = g2;
-    bi = b2;
   }
-}
+
+  // Butterfly inside a lane: pairs (i, i + H) of its eight values.
+  template <int H>
+  static DEV void lbfly(float *v) {
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      if (!(i & H)) {
+        const float p = v[i], q = v[i + H];
+        v[i] = p + q;
+        v[i + H] = p - q;
+      }
+  }
+
+  // Butterfly across lanes: partner = lane ^ m (m = 1, 2, 4, 8 within a 16-lane row, from DPP
+  // quad permutes and row mirrors); the lower lane keeps a + b, the upper b's partner - b.
+  template <int M>
+  static DEV float xbfly(float v, int lane) {
+    float t;
+    if constexpr (M == 1) t = ISHZ_DPP(v, 0xB1);
+    else if constexpr (M == 2) t = ISHZ_DPP(v, 0x4E);
+    else if constexpr (M == 4) t = ISHZ_DPP(ISHZ_DPP(v, 0x141), 0x1B);  // half mirror, quad reverse
+    else t = ISHZ_DPP(ISHZ_DPP(v, 0x141), 0x140);                      // half mirror, mirror
+    return (lane & M) ? t - v : v + t;
+  }
+
+  // Eight consecutive x per lane, 512 per wave pass: hadamardRotate's sign flip, butterflies
+  // (h = 1, 2, 4 in-lane, 8 .. 64 across lanes) and 1/sqrt(block), rounded to fp16 as the
+  // reference's rotated activation is, then written to the slots. Loads for PF passes are issued
+  // before any is used. One barrier.
+  static DEV void stage(const Args &a, const uint16_t *x, u4 *xs, float *xsum, u4 *extra, int) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if (a.block > 128) {
+      uint16_t *xh = (uint16_t *)xs;
+      float *xr = (float *)extra;
+      for (int i = threadIdx.x; i < a.K; i += blockDim.x) xr[i] = h2f(x[i]);
+      lds_wht(xr, a.K, a.block, a.signs, false);  // ends with a barrier
+      for (int c0 = wave * 128; c0 < a.K; c0 += nw * 128) {
+        const int k = c0 + 2 * lane;
+        float c, s;
+        put2(xh, k, (float)(_Float16)xr[k], (float)(_Float16)xr[k + 1], c, s);
+        put_sums(xsum, k, c, s);
+      }
+      __syncthreads();
+      return;
+    }
+    constexpr int PF = 4;
+    const int bl = a.block;
+    const float scale = bl > 1 ? 1.0f / __builtin_sqrtf((float)bl) : 1.0f;
+    const int npass = (a.K + 511) / 512;
+    for (int c0 = wave; c0 < npass; c0 += PF * nw) {
+      u4 xv[PF];
+      f4 sg[PF][2];
+#pragma unroll
+      for (int j = 0; j < PF; j++) {
+        const int k = min(min(c0 + j * nw, npass - 1) * 512 + 8 * lane, a.K - 8);
+        xv[j] = *(const u4 *)(x + k);
+        if (a.signs) {
+          sg[j][0] = *(const f4 *)(a.signs + k);
+          sg[j][1] = *(const f4 *)(a.signs + k + 4);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < PF; j++) {
+        if (c0 + j * nw >= npass) break;
+        const int k = (c0 + j * nw) * 512 + 8 * lane;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const h2 hv = as_h2(xv[j][e]);
+          v[2 * e] = (float)hv.x;
+          v[2 * e + 1] = (float)hv.y;
+        }
+        if (bl > 0) {
+          if (a.signs)
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] *= sg[j][e >> 2][e & 3];
+          if (bl > 1) lbfly<1>(v);
+          if (bl > 2) lbfly<2>(v);
+          if (bl > 4) lbfly<4>(v);
+          if (bl > 8)
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = xbfly<1>(v[e], lane);
+          if (bl > 16)
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = xbfly<2>(v[e], lane);
+          if (bl > 32)
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = xbfly<4>(v[e], lane);
+          if (bl > 64)
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = xbfly<8>(v[e], lane);
+#pragma unroll
+          for (int e = 0; e < 8; e++) v[e] = (float)(_Float16)(v[e] * scale);
+        }
+        put8(xs, xsum, k, v, k < a.K);
+      }
+    }
+    __syncthreads();
+  }
+
+  static DEV float ld_s(uint32_t v) { return BF16S ? __builtin_bit_cast(float, v << 16) : h2f(v); }
+  static DEV float dot(const Raw &r, const UnitX &s, const LaneC &) {
+    float S = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const uint32_t w = r.q[t], w10 = w >> 10;
+      const u4 a = s.slot(2 * t), c = s.slot(2 * t + 1);
+      S = dot2(and_or(w, 0x00030003u, s.mg), a.x, S);
+      S = dot2(and_or(w, 0x000C000Cu, s.mg), a.y, S);
+      S = dot2(and_or(w, 0x00300030u, s.mg), a.z, S);
+      S = dot2(and_or(w, 0x00C000C0u, s.mg), a.w, S);
+      S = dot2(and_or(w, 0x03000300u, s.mg), c.x, S);
+      S = dot2(and_or(w10, 0x00030003u, s.mg), c.y, S);
+      S = dot2(and_or(w10, 0x000C000Cu, s.mg), c.z, S);
+      S = dot2(and_or(w10, 0x00300030u, s.mg), c.w, S);
+    }
+    return ld_s(r.s) * (S - s.sum(0)) + ld_s(r.b) * s.sum(1);
+  }
+};
 
 // ------------------------------------------------------------------- verify (MFMA, M <= 16)
 // Tokens are the A operand, decoded codes the B operand (see the GGML verify kernel). One group
@@ -367,35 +431,16 @@ static int num_cu_aff() {
 
 static bool pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
-template <int GS, int LPR, bool ROT>
-static int launch_affine_gemv(const void *x, const float *signs, int block, const uint32_t *codes,
-                              const void *scales, const void *biases, int bf16s, int K, int N,
-                              void *y, hipStream_t st) {
-  constexpr int RPW = 64 / LPR;
-  const int groups = (N + RPW - 1) / RPW;
-  const int capacity = num_cu_aff() * 4 * 4;
-  const int per_wave = (groups + capacity - 1) / capacity;
-  const int waves = (groups + per_wave - 1) / per_wave;
-  const size_t ug = (size_t)(K / 64 + 15) / 16;
-  const size_t lds = ug * 16 * 8 * 16 + ug * 16 * 2 * 4 + (ROT ? (size_t)K * 4 : 0);
-  if (lds > 160 * 1024) return decline("K too large for the affine GEMV's LDS");
-  hipLaunchKernelGGL((affine_gemv<GS, LPR, ROT>), dim3((waves + 3) / 4), dim3(256), lds, st,
-                     (const uint16_t *)x, signs, block, codes, (const uint16_t *)scales,
-                     (const uint16_t *)biases, bf16s, K, N, (uint16_t *)y, per_wave);
-  ISHZ_LAUNCH_CHECK("affine gemv launch");
-  return ISHZ_OK;
-}
-
-template <int GS, bool ROT>
-static int affine_gemv_lpr(const void *x, const float *signs, int block, const uint32_t *codes,
-                           const void *scales, const void *biases, int bf16s, int K, int N,
-                           void *y, hipStream_t st) {
-  const int units = K / 64;
-  if (units <= 32)
-    return launch_affine_gemv<GS, 8, ROT>(x, signs, block, codes, scales, biases, bf16s, K, N, y, st);
-  if (units <= 128)
-    return launch_affine_gemv<GS, 16, ROT>(x, signs, block, codes, scales, biases, bf16s, K, N, y, st);
-  return launch_affine_gemv<GS, 32, ROT>(x, signs, block, codes, scales, biases, bf16s, K, N, y, st);
+template <int GS>
+static int affine_gemv(const void *x, const float *signs, int block, const uint32_t *codes,
+                       const void *scales, const void *biases, int bf16s, int K, int N, void *y,
+                       hipStream_t st) {
+  if (bf16s) {
+    const typename FAffine<GS, true>::Args a{codes, (const uint16_t *)scales, (const uint16_t *)biases, signs, block, K, N};
+    return launch_gemv<FAffine<GS, true>>(a, x, y, st);
+  }
+  const typename FAffine<GS, false>::Args a{codes, (const uint16_t *)scales, (const uint16_t *)biases, signs, block, K, N};
+  return launch_gemv<FAffine<GS, false>>(a, x, y, st);
 }
 
 template <int GS>
@@ -430,13 +475,9 @@ static int check_affine(const void *x, int x_dtype, int M, int K, const void *co
 static int affine_dispatch(const void *x, int M, int K, const float *signs, int block,
                            const uint32_t *codes, const void *scales, const void *biases,
                            int bf16s, int N, int group, void *y, hipStream_t st) {
-  const bool rot = block > 0;
   if (M == 1) {
-    if (group == 64)
-      return rot ? affine_gemv_lpr<64, true>(x, signs, block, codes, scales, biases, bf16s, K, N, y, st)
-                 : affine_gemv_lpr<64, false>(x, signs, block, codes, scales, biases, bf16s, K, N, y, st);
-    return rot ? affine_gemv_lpr<128, true>(x, signs, block, codes, scales, biases, bf16s, K, N, y, st)
-               : affine_gemv_lpr<128, false>(x, signs, block, codes, scales, biases, bf16s, K, N, y, st);
+    return group == 64 ? affine_gemv<64>(x, signs, block, codes, scales, biases, bf16s, K, N, y, st)
+                       : affine_gemv<128>(x, signs, block, codes, scales, biases, bf16s, K, N, y, st);
   }
   return group == 64 ? affine_verify_launch<64>(x, M, K, codes, scales, biases, bf16s, N, y, st)
                      : affine_verify_launch<128>(x, M, K, codes, scales, biases, bf16s, N, y, st);

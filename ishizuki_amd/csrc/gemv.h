@@ -1,0 +1,221 @@
+// The streaming M = 1 GEMV skeleton shared by every weight format (GGML blocks, MLX affine).
+//
+// A wave owns a contiguous, equal share of row groups (64/LPR rows each, LPR lanes per row) and
+// streams their units as one sequence: lane `sub` takes units sub, sub + LPR, ... of each row, in
+// batches of B units; two register batches ping-pong, so the next batch's loads are in flight
+// while one is decoded. Loads are never predicated: a batch slot is valid for all lanes or none
+// (unless RAGGED), and an invalid slot reloads the lane's first unit, so the waitcnt pass only
+// waits for the batch being decoded. The first batch is issued before x is staged into LDS.
+//
+// A format F provides: Args (pointers and sizes), Raw (one unit's registers), LaneC (per-lane
+// constants), units(K), load(args, row, u), dot(raw, UnitX, LaneC), stage(...) (fills the LDS
+// slots and sums of x, see UnitX), extra_lds_bytes(args), and R / Q (slots and sums per unit).
+#pragma once
+#include <algorithm>
+#include <cstdlib>
+
+#include "common.h"
+
+namespace ishz {
+
+// x as a GEMV lane sees it for one unit. The kernel stages x in LDS in the order lanes consume
+// it: a unit reads R 16-byte slots (8 fp16 x each) and Q fp32 sums of x. Slot r of unit u lives
+// at (u / 16) * 16R + r * 16 + u % 16, so the 16 lanes that read slot r of 16 consecutive units
+// in one instruction touch 256 contiguous bytes (every LDS bank once), and a lane's successive
+// units differ by a uniform offset (folded into the ds_read immediate).
+struct UnitX {
+  const u4 *xs;    // slot 0 of the unit; slot r at xs[16 r]
+  const float *sm; // sum 0 of the unit; sum q at sm[16 q]
+  uint32_t mg;     // 0x64006400 held in a VGPR (magic exponent for code -> fp16)
+  const u4 *grid;  // i-quant grid as fp16, pair-permuted like x (IQ2_XS)
+  const u4 *sgn;   // i-quant sign masks in the same order (IQ2_XS)
+  DEV u4 slot(int r) const { return xs[16 * r]; }
+  DEV float sum(int q) const { return sm[16 * q]; }
+};
+
+DEV void unpack(u4 a, u4 b, uint32_t *d) {
+  d[0] = a.x, d[1] = a.y, d[2] = a.z, d[3] = a.w, d[4] = b.x, d[5] = b.y, d[6] = b.z, d[7] = b.w;
+}
+
+// x0..x7 (natural) -> (x0,x2,x1,x3, x4,x6,x5,x7): the order of the nibble/byte pairs a mask
+// pulls out of one code word.
+DEV u4 perm0213(u4 a) {
+  u4 r;
+  r.x = (a.x & 0xffffu) | (a.y << 16);
+  r.y = (a.x >> 16) | (a.y & 0xffff0000u);
+  r.z = (a.z & 0xffffu) | (a.w << 16);
+  r.w = (a.z >> 16) | (a.w & 0xffff0000u);
+  return r;
+}
+DEV u2 perm0213(u2 a) {
+  u2 r;
+  r.x = (a.x & 0xffffu) | (a.y << 16);
+  r.y = (a.x >> 16) | (a.y & 0xffff0000u);
+  return r;
+}
+
+template <class F, int LPR, int B, bool RAGGED>
+__global__ __launch_bounds__(256) void gemv_kernel(typename F::Args args, const uint16_t *__restrict__ x,
+                                                   uint16_t *__restrict__ y, int groups_per_wave) {
+  static_assert(LPR % 16 == 0, "lanes per row must be a multiple of 16");
+  extern __shared__ __align__(16) uint32_t smem[];
+  const int K = args.K, N = args.N;
+  const int units = F::units(K);
+  const int ugroups = (units + 15) / 16;
+  u4 *xs = (u4 *)smem;
+  float *xsum = (float *)(xs + ugroups * 16 * F::R);
+  u4 *extra = (u4 *)(xsum + ugroups * 16 * F::Q);  // format tables / scratch
+
+  constexpr int RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane % LPR, rg = lane / LPR;
+  const int nb = (units + B * LPR - 1) / (B * LPR);  // batches per row
+  const int gw = blockIdx.x * (blockDim.x >> 6) + wave;
+  const int g_end = min((gw + 1) * groups_per_wave, (N + RPW - 1) / RPW);
+  const int g_last = max(g_end - 1, 0);
+  const typename F::LaneC lc = F::lane(sub);
+
+  // Unit of batch slot i; an invalid slot (past the row's units) reloads the lane's first unit.
+  auto unit = [&](int bb, int i) {
+    const int k = bb * B + i;
+    if constexpr (RAGGED) return min(sub + k * LPR, units - 1);
+    return sub + (k * LPR < units ? k : 0) * LPR;
+  };
+  auto load_batch = [&](int g, int bb, typename F::Raw *r) {
+    const int row = min(min(g, g_last) * RPW + rg, N - 1);
+#pragma unroll
+    for (int i = 0; i < B; i++) r[i] = F::load(args, row, unit(bb, i));
+  };
+
+  int g = gw * groups_per_wave, bi = 0;
+  typename F::Raw cur[B], alt[B];
+  load_batch(g, 0, cur);
+
+  F::stage(args, x, xs, xsum, extra, units);  // ends with a barrier
+  const uint32_t mg = vconst(0x64006400u);
+  const u4 *grid = extra, *sgn = extra + F::GRID_ENTRIES;
+  const int lane_slot = (sub >> 4) * 16 * F::R + (sub & 15);
+  const int lane_sum = (sub >> 4) * 16 * F::Q + (sub & 15);
+  auto view = [&](int bb, int i) {
+    if constexpr (RAGGED) {
+      const int u = unit(bb, i);
+      return UnitX{xs + (u >> 4) * 16 * F::R + (u & 15), xsum + (u >> 4) * 16 * F::Q + (u & 15), mg, grid, sgn};
+    } else {
+      const int k = bb * B + i;
+      return UnitX{xs + lane_slot + k * LPR * F::R, xsum + lane_sum + k * LPR * F::Q, mg, grid, sgn};
+    }
+  };
+
+  float acc = 0.0f;
+  auto advance = [&](int &gg, int &bb) {
+    if (++bb == nb) {
+      bb = 0;
+      gg++;
+    }
+  };
+  auto consume = [&](int gg, int bb, const typename F::Raw *r) {
+#pragma unroll
+    for (int i = 0; i < B; i++) {
+      if constexpr (RAGGED) {
+        const float v = F::dot(r[i], view(bb, i), lc);
+        acc += sub + (bb * B + i) * LPR < units ? v : 0.0f;
+      } else if ((bb * B + i) * LPR < units) {
+        acc += F::dot(r[i], view(bb, i), lc);
+      }
+    }
+    if (bb == nb - 1) {
+      acc = group_sum<LPR>(acc);
+      const int row = gg * RPW + rg;
+      if (sub == 0 && row < N) y[row] = f2h(acc);
+      acc = 0.0f;
+    }
+  };
+  while (g < g_end) {
+    int g1 = g, b1 = bi;
+    advance(g1, b1);
+    load_batch(g1, b1, alt);
+    consume(g, bi, cur);
+    if (g1 >= g_end) break;
+    int g2 = g1, b2 = b1;
+    advance(g2, b2);
+    load_batch(g2, b2, cur);
+    consume(g1, b1, alt);
+    g = g2;
+    bi = b2;
+  }
+}
+
+int gemv_num_cu();
+int gemv_batch_override();  // ISHZ_GEMV_B (tuning)
+int gemv_occ_override();    // ISHZ_GEMV_OCC: resident waves per SIMD the grid is sized for (tuning)
+
+// Picks lanes per row and the batch size (units per lane per batch, <= F::MAXB) so a row's
+// units divide evenly when they can, and sizes the grid to one resident round of waves with
+// equal shares of row groups.
+// Grid: one resident round of waves (at most what the compiled kernel's registers and this
+// launch's LDS allow), each wave an equal share of row groups.
+template <class F, int LPR, int B, bool RAGGED>
+static int launch_gemv_k(const typename F::Args &a, const void *x, void *y, hipStream_t st) {
+  constexpr int RPW = 64 / LPR;
+  const int units = F::units(a.K);
+  const size_t ug = (size_t)(units + 15) / 16;
+  const size_t lds = ug * 16 * F::R * 16 + ug * 16 * F::Q * 4 + F::extra_lds_bytes(a);
+  if (lds > 160 * 1024) return decline("K too large for the GEMV's LDS copy of x");
+  auto kern = gemv_kernel<F, LPR, B, RAGGED>;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds) != hipSuccess || per_cu < 1)
+    per_cu = 1;
+  const int groups = (a.N + RPW - 1) / RPW;
+  // Two waves per SIMD measured best on MI355X for every format at 17408x5120: fewer, longer
+  // waves amortise the x staging; more add no memory parallelism.
+  const int occ = gemv_occ_override() > 0 ? gemv_occ_override() : 2;
+  const int capacity = gemv_num_cu() * 4 * std::min(occ, per_cu);
+  const int per_wave = (groups + capacity - 1) / capacity;
+  const int waves = (groups + per_wave - 1) / per_wave;
+  hipLaunchKernelGGL(kern, dim3((waves + 3) / 4), dim3(256), lds, st, a, (const uint16_t *)x, (uint16_t *)y,
+                     per_wave);
+  ISHZ_LAUNCH_CHECK("gemv launch");
+  return ISHZ_OK;
+}
+
+template <class F, int LPR, int B>
+static int launch_gemv_lb(const typename F::Args &a, const void *x, void *y, hipStream_t st) {
+  if (F::units(a.K) % LPR) return launch_gemv_k<F, LPR, B, true>(a, x, y, st);
+  return launch_gemv_k<F, LPR, B, false>(a, x, y, st);
+}
+
+
+// Units per batch: ISHZ_GEMV_B, else the largest of F::PREFB, F::PREFB - 1, ... 2 that divides
+// the units each lane streams per row.
+template <class F, int LPR>
+static int launch_gemv_l(const typename F::Args &a, const void *x, void *y, hipStream_t st) {
+  const int upl = (F::units(a.K) + LPR - 1) / LPR;  // units per lane per row
+  int b = gemv_batch_override();
+  if (b < 2 || b > F::MAXB) {
+    b = 2;
+    for (int c = F::PREFB; c > 2; c--)
+      if (upl % c == 0) {
+        b = c;
+        break;
+      }
+  }
+  switch (b) {
+    case 5: if constexpr (F::MAXB >= 5) return launch_gemv_lb<F, LPR, 5>(a, x, y, st);
+    [[fallthrough]];
+    case 4: if constexpr (F::MAXB >= 4) return launch_gemv_lb<F, LPR, 4>(a, x, y, st);
+    [[fallthrough]];
+    case 3: if constexpr (F::MAXB >= 3) return launch_gemv_lb<F, LPR, 3>(a, x, y, st);
+    [[fallthrough]];
+    default: return launch_gemv_lb<F, LPR, 2>(a, x, y, st);
+  }
+}
+
+template <class F>
+static int launch_gemv(const typename F::Args &a, const void *x, void *y, hipStream_t st) {
+  const int units = F::units(a.K);
+  if (units <= 160) return launch_gemv_l<F, 16>(a, x, y, st);
+  if (units <= 384) return launch_gemv_l<F, 32>(a, x, y, st);
+  return launch_gemv_l<F, 64>(a, x, y, st);
+}
+
+}  // namespace ishz

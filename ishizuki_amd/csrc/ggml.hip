@@ -37,109 +37,7 @@ DEV void build_iq2xs_tables(u4 *grid, u4 *sgn) {
   }
 }
 
-// ----------------------------------------------------------------------------- GEMV (M = 1)
-// A wave owns a contiguous, equal share of row groups (64/LPR rows each, LPR lanes per row) and
-// streams their units as one sequence: lane `sub` takes units sub, sub + LPR, ... of each row,
-// in batches of F::BATCH units, the next batch's loads in flight while the current one is
-// decoded. The first batch is issued before x is staged into LDS.
-template <class F, int LPR>
-__global__ __launch_bounds__(256) void gemv_kernel(const uint16_t *__restrict__ x,
-                                                   const uint8_t *__restrict__ w, int K, int N,
-                                                   uint16_t *__restrict__ y, int groups_per_wave) {
-  extern __shared__ __align__(16) uint32_t smem[];
-  const int units = (K / F::BS) * F::UPB;
-  const int ugroups = (units + 15) / 16;
-  u4 *xs = (u4 *)smem;
-  float *xsum = (float *)(xs + ugroups * 16 * F::R);
-  u4 *grid = (u4 *)(xsum + (F::XSUM ? ugroups * 16 * F::Q : 0));
-  u4 *sgn = grid + 512;
-
-  constexpr int RPW = 64 / LPR, B = F::BATCH;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int sub = lane % LPR, rg = lane / LPR;
-  const int nb = (units + B * LPR - 1) / (B * LPR);  // batches per row
-  const size_t rb = (size_t)(K / F::BS) * F::TS;
-  const int gw = blockIdx.x * (blockDim.x >> 6) + wave;
-  const int g_end = min((gw + 1) * groups_per_wave, (N + RPW - 1) / RPW);
-
-  // Loads are never predicated: indices past the end are clamped to valid data and the result
-  // discarded. With no branches around them the waitcnt pass can count outstanding loads and
-  // wait only for the buffer being decoded.
-  const int g_last = max(g_end - 1, 0);
-  auto load_batch = [&](int g, int bi, typename F::Raw *r) {
-    const int row = min(min(g, g_last) * RPW + rg, N - 1);
-    const uint8_t *wr = w + (size_t)row * rb;
-#pragma unroll
-    for (int i = 0; i < B; i++) r[i] = F::load(wr, min(sub + (bi * B + i) * LPR, units - 1));
-  };
-
-  int g = gw * groups_per_wave, bi = 0;
-  typename F::Raw cur[B];
-  load_batch(g, 0, cur);
-
-  // x into LDS in consumption order (see GemvShared), with the per-16/32 sums beside it.
-  for (int i = threadIdx.x; i < ugroups * 16 * F::R; i += blockDim.x) {
-    const int u = (i / (16 * F::R)) * 16 + (i & 15), rr = (i >> 4) % F::R;
-    if (u < units) xs[i] = perm0213(*(const u4 *)(x + F::slot_k(u, rr)));
-  }
-  if constexpr (F::XSUM) {
-    for (int i = threadIdx.x; i < ugroups * 16 * F::Q; i += blockDim.x) {
-      const int u = (i / (16 * F::Q)) * 16 + (i & 15), q = (i >> 4) % F::Q;
-      if (u < units) {
-        const u4 *p = (const u4 *)(x + F::sum_k(u, q));
-        float sm = 0.0f;
-#pragma unroll
-        for (int h = 0; h < F::SUM_LEN / 8; h++) {
-          const u4 v = p[h];
-#pragma unroll
-          for (int j = 0; j < 4; j++) sm += (float)as_h2(v[j]).x + (float)as_h2(v[j]).y;
-        }
-        xsum[i] = sm;
-      }
-    }
-  }
-  if constexpr (F::GRID) build_iq2xs_tables<true>(grid, sgn);
-  __syncthreads();
-  const GemvShared S{vconst(0x64006400u), xs, xsum, grid, sgn};
-
-  // Ping-pong between two register buffers (no copies, so the compiler only waits for the
-  // buffer being decoded while the other one's loads stay in flight).
-  typename F::Raw alt[B];
-  float acc = 0.0f;
-  auto advance = [&](int &gg, int &bb) {
-    if (++bb == nb) {
-      bb = 0;
-      gg++;
-    }
-  };
-  auto consume = [&](int gg, int bb, const typename F::Raw *r) {
-#pragma unroll
-    for (int i = 0; i < B; i++) {
-      const int u = sub + (bb * B + i) * LPR;
-      const float v = F::dot(r[i], min(u, units - 1), S);
-      acc += u < units ? v : 0.0f;
-    }
-    if (bb == nb - 1) {
-      acc = group_sum<LPR>(acc);
-      const int row = gg * RPW + rg;
-      if (sub == 0 && row < N) y[row] = f2h(acc);
-      acc = 0.0f;
-    }
-  };
-  while (g < g_end) {
-    int g1 = g, b1 = bi;
-    advance(g1, b1);
-    load_batch(g1, b1, alt);
-    consume(g, bi, cur);
-    if (g1 >= g_end) break;
-    int g2 = g1, b2 = b1;
-    advance(g2, b2);
-    load_batch(g2, b2, cur);
-    consume(g1, b1, alt);
-    g = g2;
-    bi = b2;
-  }
-}
+DEV void build_iq2xs_tables_perm(u4 *grid, u4 *sgn) { build_iq2xs_tables<true>(grid, sgn); }
 
 // ----------------------------------------------------------------------------- verify (MFMA)
 // A workgroup owns T tiles of 16 weight rows; its KS waves split the row's blocks round-robin
@@ -324,41 +222,28 @@ static int num_cu() {
   return g_num_cu;
 }
 
-// Resident waves per SIMD the GEMV grid is sized for (ISHZ_GEMV_OCC overrides, for tuning).
-static int gemv_occ() {
-  static int v = [] {
-    const char *e = getenv("ISHZ_GEMV_OCC");
-    return e ? std::max(1, atoi(e)) : 4;
-  }();
+int gemv_num_cu() { return num_cu(); }
+static int env_int(const char *name) {
+  const char *e = getenv(name);
+  return e ? atoi(e) : 0;
+}
+int gemv_batch_override() {
+  static const int v = env_int("ISHZ_GEMV_B");
+  return v;
+}
+int gemv_occ_override() {
+  static const int v = env_int("ISHZ_GEMV_OCC");
   return v;
 }
 
-// Equal shares: the fewest row groups per wave that fit the grid in one resident round.
-template <class F, int LPR>
-static int launch_gemv(const void *x, int K, const void *w, int N, void *y, hipStream_t st) {
-  constexpr int RPW = 64 / LPR;
-  const int groups = (N + RPW - 1) / RPW;
-  const int capacity = num_cu() * 4 * gemv_occ();
-  const int per_wave = (groups + capacity - 1) / capacity;
-  const int waves = (groups + per_wave - 1) / per_wave;
-  const int blocks = (waves + 3) / 4;
-  const size_t ug = (size_t)(K / F::BS * F::UPB + 15) / 16;
-  size_t lds = ug * 16 * F::R * 16 + (F::XSUM ? ug * 16 * F::Q * 4 : 0) + (F::GRID ? (512 + 128) * 16 : 0);
-  if (lds > 160 * 1024) return decline("K too large for the GEMV's LDS copy of x");
-  hipLaunchKernelGGL((gemv_kernel<F, LPR>), dim3(blocks), dim3(256), lds, st, (const uint16_t *)x,
-                     (const uint8_t *)w, K, N, (uint16_t *)y, per_wave);
-  ISHZ_LAUNCH_CHECK("gemv launch");
-  return ISHZ_OK;
-}
+template <class F>
+static int verify(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st);
 
-// Lanes per row: enough that a row is a few batches deep, not so many that lanes idle.
 template <class F>
 static int gemv(const void *x, int K, const void *w, int N, void *y, hipStream_t st) {
-  const int units = K / F::BS * F::UPB;
-  if (units <= 48) return launch_gemv<F, 8>(x, K, w, N, y, st);
-  if (units <= 160) return launch_gemv<F, 16>(x, K, w, N, y, st);
-  if (units <= 384) return launch_gemv<F, 32>(x, K, w, N, y, st);
-  return launch_gemv<F, 64>(x, K, w, N, y, st);
+  if (K % F::GEMV_K_MULT) return verify<F>(x, 1, K, w, N, y, st);
+  const typename F::Args a{(const uint8_t *)w, (size_t)(K / F::BS) * F::TS, K, N};
+  return launch_gemv<F>(a, x, y, st);
 }
 
 template <class F, int T>

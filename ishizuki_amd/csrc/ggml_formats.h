@@ -15,46 +15,12 @@
 //    C column j and applies that row's scale itself. A step is one scale group (32 or 16
 //    weights); B holds exact integer codes and the scale multiplies the fp32 C tile.
 #pragma once
-#include "common.h"
 #include <algorithm>
 
+#include "common.h"
+#include "gemv.h"
+
 namespace ishz {
-
-// LDS working set of the GEMV kernel. x is stored in the order lanes consume it: a unit reads R
-// 16-byte slots (8 fp16 x each, pair-permuted) and Q sums of 16 x. Slot r of unit u lives at
-// (u / 16) * 16R + r * 16 + u % 16, so the 16 lanes that read slot r of 16 consecutive units in
-// one instruction touch 256 contiguous bytes: every LDS bank once, no conflicts.
-struct GemvShared {
-  uint32_t mg;           // 0x64006400 held in a VGPR (magic exponent for code -> fp16)
-  const u4 *x;
-  const float *xsum;
-  const u4 *grid;        // i-quant grid as fp16, permuted like x (IQ2_XS only)
-  const u4 *sgn;         // i-quant sign masks for the same order (IQ2_XS only)
-  template <int R>
-  DEV u4 slot(int u, int r) const { return x[(u >> 4) * 16 * R + r * 16 + (u & 15)]; }
-  template <int Q>
-  DEV float sum(int u, int q) const { return xsum[(u >> 4) * 16 * Q + q * 16 + (u & 15)]; }
-};
-
-DEV void unpack(u4 a, u4 b, uint32_t *d) {
-  d[0] = a.x, d[1] = a.y, d[2] = a.z, d[3] = a.w, d[4] = b.x, d[5] = b.y, d[6] = b.z, d[7] = b.w;
-}
-
-// x0..x7 (natural) -> (x0,x2,x1,x3, x4,x6,x5,x7): the order of the nibble/byte pairs below.
-DEV u4 perm0213(u4 a) {
-  u4 r;
-  r.x = (a.x & 0xffffu) | (a.y << 16);
-  r.y = (a.x >> 16) | (a.y & 0xffff0000u);
-  r.z = (a.z & 0xffffu) | (a.w << 16);
-  r.w = (a.z >> 16) | (a.w & 0xffff0000u);
-  return r;
-}
-DEV u2 perm0213(u2 a) {
-  u2 r;
-  r.x = (a.x & 0xffffu) | (a.y << 16);
-  r.y = (a.x >> 16) | (a.y & 0xffff0000u);
-  return r;
-}
 
 // Sum over the 8 fp16 x pairs of a lane's operand (as dwords) times codes.
 DEV float dot8(const uint32_t *c, const uint32_t *x, float acc) {
@@ -77,42 +43,119 @@ DEV void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, int &sc, in
   }
 }
 
+// What the GEMV skeleton needs from a GGML format: row pointers, unit count and the x staging
+// (x slots in consumption order, per-group sums, i-quant tables).
+DEV void build_iq2xs_tables_perm(u4 *grid, u4 *sgn);
+
+template <class D>
+struct GgmlGemv {
+  struct Args {
+    const uint8_t *w;
+    size_t rb;  // bytes per row
+    int K, N;
+  };
+  static constexpr int GRID_ENTRIES = 512;
+  static __host__ __device__ int units(int K) { return K / D::BS * D::UPB / D::UNIT_BLOCKS; }
+  static size_t extra_lds_bytes(const Args &) { return D::GRID ? (512 + 128) * 16 : 0; }
+  static DEV auto load(const Args &a, int row, int u) { return D::load_row(a.w + (size_t)row * a.rb, u); }
+  // Loads for U slots (sums) per thread are issued together before any is stored, so staging
+  // costs a memory latency per U items rather than one each.
+  static DEV void stage(const Args &a, const uint16_t *x, u4 *xs, float *xsum, u4 *extra, int units) {
+    const int ug = (units + 15) / 16, bd = blockDim.x;
+    constexpr int U = 4, US = 2, SL = D::SUM_LEN / 8;
+    const int ns = ug * 16 * D::R;
+    for (int i0 = threadIdx.x; i0 < ns; i0 += U * bd) {
+      u4 v[U];
+#pragma unroll
+      for (int j = 0; j < U; j++) {
+        const int i = min(i0 + j * bd, ns - 1);
+        const int u = min((i / (16 * D::R)) * 16 + (i & 15), units - 1), r = (i >> 4) % D::R;
+        v[j] = *(const u4 *)(x + D::slot_k(u, r));
+      }
+#pragma unroll
+      for (int j = 0; j < U; j++) {
+        const int i = i0 + j * bd;
+        if (i < ns && (i / (16 * D::R)) * 16 + (i & 15) < units) xs[i] = perm0213(v[j]);
+      }
+    }
+    if constexpr (D::XSUM) {
+      const int nq = ug * 16 * D::Q;
+      for (int i0 = threadIdx.x; i0 < nq; i0 += US * bd) {
+        u4 v[US][SL];
+#pragma unroll
+        for (int j = 0; j < US; j++) {
+          const int i = min(i0 + j * bd, nq - 1);
+          const int u = min((i / (16 * D::Q)) * 16 + (i & 15), units - 1), q = (i >> 4) % D::Q;
+          const u4 *p = (const u4 *)(x + D::sum_k(u, q));
+#pragma unroll
+          for (int h = 0; h < SL; h++) v[j][h] = p[h];
+        }
+#pragma unroll
+        for (int j = 0; j < US; j++) {
+          const int i = i0 + j * bd;
+          if (i < nq && (i / (16 * D::Q)) * 16 + (i & 15) < units) {
+            float sm = 0.0f;
+#pragma unroll
+            for (int h = 0; h < SL; h++)
+#pragma unroll
+              for (int e = 0; e < 4; e++) sm += (float)as_h2(v[j][h][e]).x + (float)as_h2(v[j][h][e]).y;
+            xsum[i] = sm;
+          }
+        }
+      }
+    }
+    if constexpr (D::GRID) build_iq2xs_tables_perm(extra, extra + 512);
+    __syncthreads();
+  }
+};
+
 // ------------------------------------------------------------------------------------- Q4_0
 // ggml block_q4_0: fp16 d at 0, qs[16] at 2; element j = (lo(qs[j]) - 8) d, j + 16 = hi.
-struct FQ4_0 {
+struct FQ4_0 : GgmlGemv<FQ4_0> {
   static constexpr uint32_t TYPE = ISHZ_GGML_Q4_0;
-  static constexpr int BS = 32, TS = 18, UPB = 1;  // unit: the whole block, 32 weights
-  static constexpr int BATCH = 4;  // units per lane per batch (two batches in flight)
+  static constexpr int BS = 32, TS = 18;
+  // GEMV unit: two blocks (36 bytes, dword aligned when rows hold an even number of blocks),
+  // 64 weights; so the GEMV needs K % 64 == 0 (the verify kernel takes any K % 32 == 0).
+  static constexpr int UPB = 1, UNIT_BLOCKS = 2, GEMV_K_MULT = 64;
+  static constexpr int MAXB = 5, PREFB = 2;
   static constexpr bool XSUM = true, GRID = false;
-  static constexpr int R = 4, Q = 2;  // x slots: lo run k0, k0+8, hi run k0+16, k0+24
-  static DEV int slot_k(int u, int r) { return 32 * u + 8 * r; }
-  static DEV int sum_k(int u, int q) { return 32 * u + 16 * q; }
+  static constexpr int R = 8, Q = 4;  // slots k0 + 8r; sums of 16 at k0 + 16q
+  static DEV int slot_k(int u, int r) { return 64 * u + 8 * r; }
+  static DEV int sum_k(int u, int q) { return 64 * u + 16 * q; }
   static constexpr int SUM_LEN = 16;
   struct Raw {
-    u4 q;
-    uint32_t d;
+    u4 a, b;
+    uint32_t c;
   };
-  static DEV Raw load(const uint8_t *row, int u) {
-    const uint8_t *p = row + (size_t)u * TS;
-    return {ld16<2>(p + 2), ld2(p)};
+  static DEV Raw load_row(const uint8_t *row, int u) {
+    const uint8_t *p = row + (size_t)u * 2 * TS;
+    return {ld16<4>(p), ld16<4>(p + 16), ld4<4>(p + 32)};
   }
-  // Low nibbles become 1024 + q and high nibbles 1024 + 16q (masked in place, no shift); the
-  // offsets come back out through the per-16 sums of x.
-  static DEV float dot(const Raw &r, int u, const GemvShared &s) {
-    uint32_t xl[8], xh[8], lo[8], hi[8];
-    unpack(s.slot<R>(u, 0), s.slot<R>(u, 1), xl);
-    unpack(s.slot<R>(u, 2), s.slot<R>(u, 3), xh);
+  struct LaneC {};
+  static DEV LaneC lane(int sub) { return {}; }
+  // Block A: d = bytes 0-1, qs = bytes 2..17 (realigned by two bytes); block B: d = bytes
+  // 18-19, qs = bytes 20..35 (dword aligned). Low nibbles become 1024 + q, high ones 1024 + 16q;
+  // the offsets come back out through the per-16 sums of x.
+  static DEV float half_dot(const uint32_t *qs, const UnitX &s, int r0, int q0) {
+    uint32_t xl[8], xh[8];
+    unpack(s.slot(r0), s.slot(r0 + 1), xl);
+    unpack(s.slot(r0 + 2), s.slot(r0 + 3), xh);
+    float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-      const uint32_t q = r.q[t], q8 = q >> 8;
-      lo[2 * t] = and_or(q, 0x000F000Fu, s.mg);
-      lo[2 * t + 1] = and_or(q8, 0x000F000Fu, s.mg);
-      hi[2 * t] = and_or(q, 0x00F000F0u, s.mg);
-      hi[2 * t + 1] = and_or(q8, 0x00F000F0u, s.mg);
+      const uint32_t q = qs[t], q8 = q >> 8;
+      a0 = dot2(and_or(q, 0x000F000Fu, s.mg), xl[2 * t], a0);
+      a1 = dot2(and_or(q8, 0x000F000Fu, s.mg), xl[2 * t + 1], a1);
+      b0 = dot2(and_or(q, 0x00F000F0u, s.mg), xh[2 * t], b0);
+      b1 = dot2(and_or(q8, 0x00F000F0u, s.mg), xh[2 * t + 1], b1);
     }
-    const float sl = dot8(lo, xl, 0.0f), sh = dot8(hi, xh, 0.0f);
-    const float xs_l = s.sum<Q>(u, 0), xs_h = s.sum<Q>(u, 1);
-    return h2f(r.d) * ((sl - 1032.0f * xs_l) + (0.0625f * sh - 72.0f * xs_h));
+    return ((a0 + a1) - 1032.0f * s.sum(q0)) + (0.0625f * (b0 + b1) - 72.0f * s.sum(q0 + 1));
+  }
+  static DEV float dot(const Raw &r, const UnitX &s, const LaneC &) {
+    const uint32_t qa[4] = {__builtin_amdgcn_alignbyte(r.a.y, r.a.x, 2), __builtin_amdgcn_alignbyte(r.a.z, r.a.y, 2),
+                            __builtin_amdgcn_alignbyte(r.a.w, r.a.z, 2), __builtin_amdgcn_alignbyte(r.b.x, r.a.w, 2)};
+    const uint32_t qb[4] = {r.b.y, r.b.z, r.b.w, r.c};
+    return h2f(r.a.x & 0xffff) * half_dot(qa, s, 0, 0) + h2f(r.b.x >> 16) * half_dot(qb, s, 4, 2);
   }
 
   // Verify: one MFMA 16x16x32 per block. Lane group g takes k = 8g..8g+7: lo nibbles of bytes
@@ -144,10 +187,11 @@ struct FQ4_0 {
 // GGMLDequant.q4K (Core/GGMLDequant.swift:187-220): d, dmin fp16 at 0, 2; 12 B of 6-bit
 // scales/mins at 4; qs[128] at 16. 64-weight chunk jj: low nibbles of qs[32jj+l] are weights
 // 64jj+l (sub-block 2jj), high nibbles 64jj+32+l (sub-block 2jj+1); w = d*sc*q - dmin*m.
-struct FQ4_K {
+struct FQ4_K : GgmlGemv<FQ4_K> {
   static constexpr uint32_t TYPE = ISHZ_GGML_Q4_K;
   static constexpr int BS = 256, TS = 144, UPB = 4;  // unit: 32 B of qs (chunk jj), 64 weights
-  static constexpr int BATCH = 2;
+  static constexpr int UNIT_BLOCKS = 1, GEMV_K_MULT = 256;
+  static constexpr int MAXB = 5, PREFB = 2;
   static constexpr bool XSUM = true, GRID = false;
   static constexpr int R = 8, Q = 2;  // slots: lo run k0 + 8i (i < 4), hi run k0 + 32 + 8i
   static DEV int k0_of(int u) { return (u >> 2) * 256 + (u & 3) * 64; }
@@ -160,48 +204,57 @@ struct FQ4_K {
     u4 q0, q1;
     uint32_t h;
   };
-  static DEV Raw load(const uint8_t *row, int u) {
+  static DEV Raw load_row(const uint8_t *row, int u) {
     const uint8_t *p = row + (size_t)(u >> 2) * TS;
     const uint8_t *qs = p + 16 + 32 * (u & 3);
     return {ld16<16>(qs), ld16<16>(qs + 16), ld4<4>(p + 4 * (u & 3))};
   }
+  // Lane constants: a lane always decodes the same chunk jj = sub % 4 of a block, so the
+  // placement of its two sub-blocks' 6-bit scale/min fields (GGMLDequant.q4K.scaleMin,
+  // Core/GGMLDequant.swift:193-205) is fixed per lane: sub-block j < 4 reads bits [8j, 8j+6) of
+  // words 1/2 of the header; j >= 4 reads 4 bits of word 3 and the top 2 bits of words 1/2.
+  struct LaneC {
+    bool lo;             // jj < 2
+    uint32_t sh, wa, wh;  // bit offset of sub-block 2jj, low-field width (6 or 4), high width (0 or 2)
+  };
+  static DEV LaneC lane(int sub) {
+    const int jj = sub & 3;
+    return {jj < 2, (uint32_t)(16 * (jj & 1)), jj < 2 ? 6u : 4u, jj < 2 ? 0u : 2u};
+  }
   // Chunk jj: low nibbles of its 32 bytes are sub-block 2jj (weights k0..k0+31), high nibbles
   // sub-block 2jj+1 (k0+32..k0+63). Low nibbles become 1024 + q, high ones 1024 + 16q, and
   // with S = sum code * x and X = sum x over the sub-block: sum q x = S - 1024 X, or S/16 - 64 X.
-  static DEV float dot(const Raw &r, int u, const GemvShared &s) {
-    const int jj = u & 3;
-    uint32_t qw[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-    float sl = 0.0f, sh = 0.0f;
+  static DEV float dot(const Raw &r, const UnitX &s, const LaneC &c) {
+    const uint32_t qw[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
 #pragma unroll
     for (int hb = 0; hb < 2; hb++) {
       uint32_t xl[8], xh[8];
-      unpack(s.slot<R>(u, 2 * hb), s.slot<R>(u, 2 * hb + 1), xl);
-      unpack(s.slot<R>(u, 4 + 2 * hb), s.slot<R>(u, 5 + 2 * hb), xh);
+      unpack(s.slot(2 * hb), s.slot(2 * hb + 1), xl);
+      unpack(s.slot(4 + 2 * hb), s.slot(5 + 2 * hb), xh);
 #pragma unroll
       for (int t = 0; t < 4; t++) {
         const uint32_t q = qw[4 * hb + t], q8 = q >> 8;
-        sl = dot2(and_or(q, 0x000F000Fu, s.mg), xl[2 * t], sl);
-        sl = dot2(and_or(q8, 0x000F000Fu, s.mg), xl[2 * t + 1], sl);
-        sh = dot2(and_or(q, 0x00F000F0u, s.mg), xh[2 * t], sh);
-        sh = dot2(and_or(q8, 0x00F000F0u, s.mg), xh[2 * t + 1], sh);
+        a0 = dot2(and_or(q, 0x000F000Fu, s.mg), xl[2 * t], a0);
+        a1 = dot2(and_or(q8, 0x000F000Fu, s.mg), xl[2 * t + 1], a1);
+        b0 = dot2(and_or(q, 0x00F000F0u, s.mg), xh[2 * t], b0);
+        b1 = dot2(and_or(q8, 0x00F000F0u, s.mg), xh[2 * t + 1], b1);
       }
     }
-    // scales/mins of sub-blocks 2jj, 2jj+1 (GGMLDequant.q4K.scaleMin), branch-free
     const uint32_t h0 = quad_bcast<0>(r.h), s0 = quad_bcast<1>(r.h), s1 = quad_bcast<2>(r.h),
                    s2 = quad_bcast<3>(r.h);
-    const bool lo4 = jj < 2;
-    const uint32_t sh0 = 16 * (jj & 1);  // byte 2jj & 3 of the scale words
-    const uint32_t a0 = s0 >> sh0, b0 = s1 >> sh0, c0 = s2 >> sh0;
-    const uint32_t a1 = a0 >> 8, b1 = b0 >> 8, c1 = c0 >> 8;
-    const uint32_t sc0 = lo4 ? (a0 & 63) : ((c0 & 15) | ((a0 >> 2) & 48));
-    const uint32_t m0 = lo4 ? (b0 & 63) : (((c0 >> 4) & 15) | ((b0 >> 2) & 48));
-    const uint32_t sc1 = lo4 ? (a1 & 63) : ((c1 & 15) | ((a1 >> 2) & 48));
-    const uint32_t m1 = lo4 ? (b1 & 63) : (((c1 >> 4) & 15) | ((b1 >> 2) & 48));
+    const uint32_t A = c.lo ? s0 : s2, B = c.lo ? s1 : s2;
+    const uint32_t mo = c.lo ? 0u : 4u;  // the min's low field sits 4 bits up in word 3
+    auto field = [&](uint32_t w, uint32_t off, uint32_t wd, uint32_t top, uint32_t sh) {
+      return __builtin_amdgcn_ubfe(w, off, wd) | (__builtin_amdgcn_ubfe(top, sh + 6, c.wh) << 4);
+    };
+    const uint32_t sc0 = field(A, c.sh, c.wa, s0, c.sh), m0 = field(B, c.sh + mo, c.wa, s1, c.sh);
+    const uint32_t sc1 = field(A, c.sh + 8, c.wa, s0, c.sh + 8), m1 = field(B, c.sh + 8 + mo, c.wa, s1, c.sh + 8);
     const float d = h2f(h0 & 0xffff), dmin = h2f(h0 >> 16);
-    const float xs_l = s.sum<Q>(u, 0), xs_h = s.sum<Q>(u, 1);
     const float dl0 = d * (float)sc0, dl1 = d * (float)sc1;
-    return dl0 * (sl - 1024.0f * xs_l) - (dmin * (float)m0) * xs_l +
-           dl1 * (0.0625f * sh - 64.0f * xs_h) - (dmin * (float)m1) * xs_h;
+    const float xs_l = s.sum(0), xs_h = s.sum(1);
+    return dl0 * ((a0 + a1) - 1024.0f * xs_l) - (dmin * (float)m0) * xs_l +
+           dl1 * (0.0625f * (b0 + b1) - 64.0f * xs_h) - (dmin * (float)m1) * xs_h;
   }
 
   // Verify: one MFMA 16x16x32 per sub-block; lane group g takes l = 8g..8g+7 of it, i.e. the
@@ -257,22 +310,25 @@ struct FQ4_K {
 // at 192, fp16 d at 208. Half n (128 weights), l in 0..31: weights 128n + l + 32qq take the low
 // (qq 0,1) or high (qq 2,3) nibble of ql[64n + 32(qq&1) + l] and bits 2qq..2qq+1 of
 // qh[32n + l]; w = d * sc[8n + l/16 + 2qq] * (q - 32).
-struct FQ6_K {
+struct FQ6_K : GgmlGemv<FQ6_K> {
   static constexpr uint32_t TYPE = ISHZ_GGML_Q6_K;
   static constexpr int BS = 256, TS = 210, UPB = 4;  // unit: (n, l-half), 64 weights
-  static constexpr int BATCH = 2;
+  static constexpr int UNIT_BLOCKS = 1, GEMV_K_MULT = 256;
+  static constexpr int MAXB = 5, PREFB = 2;
   static constexpr bool XSUM = true, GRID = false;
   static constexpr int R = 8, Q = 4;  // slot 2qq + i: k0 + 32qq + 8i; sum qq: k0 + 32qq
   static DEV int k0_of(int u) { return (u >> 2) * 256 + ((u >> 1) & 1) * 128 + (u & 1) * 16; }
   static DEV int slot_k(int u, int r) { return k0_of(u) + 32 * (r >> 1) + 8 * (r & 1); }
   static DEV int sum_k(int u, int q) { return k0_of(u) + 32 * q; }
   static constexpr int SUM_LEN = 16;
+  // Odd blocks sit two bytes off dword alignment (unaligned 16-byte loads; re-aligning in
+  // registers was measured slower here, the kernel being VALU-bound).
   struct Raw {
     u4 qa, qb, qh;
     u2 sc;
     uint32_t d;
   };
-  static DEV Raw load(const uint8_t *row, int u) {
+  static DEV Raw load_row(const uint8_t *row, int u) {
     const uint8_t *p = row + (size_t)(u >> 2) * TS;
     const int n = (u >> 1) & 1, lh = u & 1;
     Raw r;
@@ -283,33 +339,40 @@ struct FQ6_K {
     r.d = ld2(p + 208);
     return r;
   }
-  // Each 6-bit code becomes 1024 + q; sum (q - 32) x = S - 1056 X over a 16-weight group.
-  static DEV float dot(const Raw &r, int u, const GemvShared &s) {
-    const int lh = u & 1;
-    float S[4] = {0, 0, 0, 0};
-    uint32_t xv[4][8];
-#pragma unroll
-    for (int qq = 0; qq < 4; qq++) unpack(s.slot<R>(u, 2 * qq), s.slot<R>(u, 2 * qq + 1), xv[qq]);
+  struct LaneC {
+    uint32_t sh;  // 8 * lh: byte of the scale words this lane's l-half reads
+  };
+  static DEV LaneC lane(int sub) { return {(uint32_t)(8 * (sub & 1))}; }
+  // Codes are assembled in place as fp16 halves: q1, q2 (low nibbles + qh bits) become 1024 + q,
+  // q3, q4 (high nibbles + qh bits) 1024 + 16q with no shift of the nibble; sum (q - 32) x over a
+  // 16-weight group is S - 1056 X, or S/16 - 96 X.
+  static DEV float dot(const Raw &r, const UnitX &s, const LaneC &c) {
+    float S[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
+    const u4 QA = r.qa, QB = r.qb, QH = r.qh;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-      const uint32_t a = r.qa[t], bq = r.qb[t], h = r.qh[t];
-      const uint32_t v[4] = {(a & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u),
-                             (bq & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u),
-                             ((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u),
-                             ((bq >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u)};
-#pragma unroll
-      for (int qq = 0; qq < 4; qq++) {
-        S[qq] = dot2(and_or(v[qq], 0x003F003Fu, s.mg), xv[qq][2 * t], S[qq]);
-        S[qq] = dot2(and_or(v[qq] >> 8, 0x003F003Fu, s.mg), xv[qq][2 * t + 1], S[qq]);
-      }
+      const u4 x0 = s.slot(t >> 1), x1 = s.slot(2 + (t >> 1)), x2 = s.slot(4 + (t >> 1)),
+               x3 = s.slot(6 + (t >> 1));
+      const int o = 2 * (t & 1);
+      const uint32_t a = QA[t], b = QB[t], h4 = QH[t] << 4, h2 = QH[t] << 2;
+      const uint32_t a8 = a >> 8, b8 = b >> 8, h48 = QH[t] >> 4, h28 = QH[t] >> 6;
+      S[0][0] = dot2(and_or(a, 0x000F000Fu, and_or(h4, 0x00300030u, s.mg)), x0[o], S[0][0]);
+      S[0][1] = dot2(and_or(a8, 0x000F000Fu, and_or(h48, 0x00300030u, s.mg)), x0[o + 1], S[0][1]);
+      S[1][0] = dot2(and_or(b, 0x000F000Fu, and_or(h2, 0x00300030u, s.mg)), x1[o], S[1][0]);
+      S[1][1] = dot2(and_or(b8, 0x000F000Fu, and_or(h28, 0x00300030u, s.mg)), x1[o + 1], S[1][1]);
+      S[2][0] = dot2(and_or(a, 0x00F000F0u, and_or(h4, 0x03000300u, s.mg)), x2[o], S[2][0]);
+      S[2][1] = dot2(and_or(a8, 0x00F000F0u, and_or(h48, 0x03000300u, s.mg)), x2[o + 1], S[2][1]);
+      S[3][0] = dot2(and_or(b, 0x00F000F0u, and_or(h2, 0x03000300u, s.mg)), x3[o], S[3][0]);
+      S[3][1] = dot2(and_or(b8, 0x00F000F0u, and_or(h28, 0x03000300u, s.mg)), x3[o + 1], S[3][1]);
     }
     // sc[8n + lh + 2qq]: bytes lh, lh+2 of the low word, lh, lh+2 of the high word.
     const float d = h2f(r.d);
-    const int sh = 8 * lh;
-    const float s0 = (float)(int8_t)(r.sc.x >> sh), s1 = (float)(int8_t)(r.sc.x >> (sh + 16));
-    const float s2 = (float)(int8_t)(r.sc.y >> sh), s3 = (float)(int8_t)(r.sc.y >> (sh + 16));
-    return (d * s0) * (S[0] - 1056.0f * s.sum<Q>(u, 0)) + (d * s1) * (S[1] - 1056.0f * s.sum<Q>(u, 1)) +
-           (d * s2) * (S[2] - 1056.0f * s.sum<Q>(u, 2)) + (d * s3) * (S[3] - 1056.0f * s.sum<Q>(u, 3));
+    const float s0 = (float)(int8_t)(r.sc.x >> c.sh), s1 = (float)(int8_t)(r.sc.x >> (c.sh + 16));
+    const float s2 = (float)(int8_t)(r.sc.y >> c.sh), s3 = (float)(int8_t)(r.sc.y >> (c.sh + 16));
+    return (d * s0) * ((S[0][0] + S[0][1]) - 1056.0f * s.sum(0)) +
+           (d * s1) * ((S[1][0] + S[1][1]) - 1056.0f * s.sum(1)) +
+           (d * s2) * (0.0625f * (S[2][0] + S[2][1]) - 96.0f * s.sum(2)) +
+           (d * s3) * (0.0625f * (S[3][0] + S[3][1]) - 96.0f * s.sum(3));
   }
 
   // Verify: MFMA 16x16x16, one per 16-weight scale group (n, qq, lh); lane group g takes
@@ -365,10 +428,11 @@ struct FQ6_K {
 // index, 7-bit sign index), scales u8[8] at 66. Entry l of group ib (weights 32ib + 8l + j) is
 // d*(0.5+nibble)*0.25 * grid[q&511][j] * sign(ksigns[q>>9], j), nibble = scales[ib] lo for
 // l < 2, hi otherwise.
-struct FIQ2_XS {
+struct FIQ2_XS : GgmlGemv<FIQ2_XS> {
   static constexpr uint32_t TYPE = ISHZ_GGML_IQ2_XS;
   static constexpr int BS = 256, TS = 74, UPB = 4;  // unit: two groups, 16 B of qs, 64 weights
-  static constexpr int BATCH = 2;
+  static constexpr int UNIT_BLOCKS = 1, GEMV_K_MULT = 256;
+  static constexpr int MAXB = 5, PREFB = 2;
   static constexpr bool XSUM = false, GRID = true;
   static constexpr int R = 8, Q = 1;  // slot l: k0 + 8l
   static DEV int slot_k(int u, int r) { return (u >> 2) * 256 + (u & 3) * 64 + 8 * r; }
@@ -378,19 +442,22 @@ struct FIQ2_XS {
     u4 q;
     uint32_t sc, d;
   };
-  static DEV Raw load(const uint8_t *row, int u) {
+  static DEV Raw load_row(const uint8_t *row, int u) {
     const uint8_t *p = row + (size_t)(u >> 2) * TS;
     const int pp = u & 3;
     return {ld16<2>(p + 2 + 16 * pp), ld2(p + 66 + 2 * pp), ld2(p)};
   }
-  static DEV float dot(const Raw &r, int u, const GemvShared &s) {
+  struct LaneC {};
+  static DEV LaneC lane(int sub) { return {}; }
+  static DEV float dot(const Raw &r, const UnitX &s, const LaneC &) {
     const float d = h2f(r.d);
+    const u4 QS = r.q;
     float acc = 0.0f;
 #pragma unroll
     for (int l = 0; l < 8; l++) {
-      const uint32_t q = (r.q[l >> 1] >> (16 * (l & 1))) & 0xffffu;
+      const uint32_t q = (QS[l >> 1] >> (16 * (l & 1))) & 0xffffu;
       const u4 G = s.grid[q & 511], M = s.sgn[q >> 9];
-      const u4 X = s.slot<R>(u, l);
+      const u4 X = s.slot(l);
       float e = dot2(G.x ^ M.x, X.x, 0.0f);
       e = dot2(G.y ^ M.y, X.y, e);
       e = dot2(G.z ^ M.z, X.z, e);
