@@ -63,15 +63,18 @@ def verify_apply(x, weight, scales, biases, group_size=64, bits=2):
     return quantized_matmul(x, weight, scales, biases, group_size, bits)
 
 
-def linear(x, weight, scales, biases, signs=None, block=0, group_size=64, bits=2):
-    """Rotated PackedLinear forward: rotate (fused for one row) then the quantized matmul."""
+def linear(x, weight, scales, biases, signs=None, block=0, group_size=64, bits=2, _prestage=True):
+    """Rotated PackedLinear forward: rotate (fused for one row) then the quantized matmul.
+
+    For one row with block <= 128 the workspace holds x rotated and staged once for every
+    workgroup; `_prestage=False` passes none, so each workgroup rotates x itself (test hook)."""
     require_cuda(x, weight, scales, biases)
     x = x.contiguous()
     M, K = x.shape
     N = weight.shape[0]
     y = torch.empty((M, N), dtype=x.dtype, device=x.device)
     L = _lib.lib()
-    ws_bytes = L.ishz_affine_workspace_size(M, K) if block else 0
+    ws_bytes = L.ishz_affine_workspace_size(M, K) if block and (_prestage or M > 1) else 0
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
     s = None
     if block and signs is not None:

@@ -133,14 +133,20 @@ struct FAffine {
     const float *signs;
     int block;  // Hadamard block (0: x is not rotated)
     int K, N;
+    const u4 *img;  // x already staged by affine_prestage_kernel (the LDS image), or null
   };
   struct Raw {
     u4 q;
     uint32_t s, b;
   };
   struct LaneC {};
-  static constexpr int R = 8, Q = 2, MAXB = 5, PREFB = 5, GRID_ENTRIES = 0;
+  static constexpr int R = 8, Q = 2, MAXB = 5, PREFB = 2, DEPTH = 2, GRID_ENTRIES = 0;
   static __host__ __device__ int units(int K) { return K / 64; }
+  // 16-byte words of the staged x: slots, then the two sums per unit.
+  static __host__ __device__ int img_words(int K) { return (units(K) + 15) / 16 * (16 * R + 4 * Q); }
+  // Resident waves per SIMD the grid is sized for: with a prestaged x, many short waves balance
+  // the SIMDs best; staging in-kernel favours fewer, longer waves.
+  static int occ(const Args &a) { return a.img ? 4 : 2; }
   // Blocks above 128 are rotated in an LDS copy of x (one fp32 per element).
   static size_t extra_lds_bytes(const Args &a) { return a.block > 128 ? (size_t)a.K * 4 : 0; }
   static DEV LaneC lane(int) { return {}; }
@@ -186,9 +192,10 @@ struct FAffine {
 #pragma unroll
     for (int p = 0; p < 8; p++) {
       h[p] = f2h(__builtin_ldexpf(v[p], -2 * (p < 5 ? p : p - 5)));  // x / 4^i, exact
-      c += h2f(h[p]);
       xsm += v[p];
     }
+#pragma unroll
+    for (int p = 0; p < 8; p += 2) c = dot2(h[p] | h[p + 1] << 16, 0x3C003C00u, c);  // + h_p + h_p+1
     // Selects by mask (a select between two elements of h would become a dynamic index, i.e.
     // scratch memory).
     const uint32_t hm = 0u - (uint32_t)hf;
@@ -246,8 +253,92 @@ struct FAffine {
   // (h = 1, 2, 4 in-lane, 8 .. 64 across lanes) and 1/sqrt(block), rounded to fp16 as the
   // reference's rotated activation is, then written to the slots. Loads for PF passes are issued
   // before any is used. One barrier.
-  static DEV void stage(const Args &a, const uint16_t *x, u4 *xs, float *xsum, u4 *extra, int) {
+  static constexpr int PF = 4;
+  struct XPre {
+    u4 xv[PF];
+    f4 sg[PF][2];
+  };
+  static DEV XPre load_group(const Args &a, const uint16_t *x, int c0, int nw) {
+    const int lane = threadIdx.x & 63;
+    const int npass = (a.K + 511) / 512;
+    XPre p;
+#pragma unroll
+    for (int j = 0; j < PF; j++) {
+      const int k = min(min(c0 + j * nw, npass - 1) * 512 + 8 * lane, a.K - 8);
+      p.xv[j] = *(const u4 *)(x + k);
+      if (a.signs) {
+        p.sg[j][0] = *(const f4 *)(a.signs + k);
+        p.sg[j][1] = *(const f4 *)(a.signs + k + 4);
+      }
+    }
+    return p;
+  }
+  // Rotates and stages passes c0, c0 + nw, ... (PF of them) of this wave from their loads, into
+  // LDS or (prestage) into the global image.
+  static DEV void stage_group(const Args &a, u4 *xs, float *xsum, int c0, int nw, const XPre &cur) {
+    const int lane = threadIdx.x & 63;
+    const int bl = a.block;
+    const float scale = bl > 1 ? 1.0f / __builtin_sqrtf((float)bl) : 1.0f;
+    const int npass = (a.K + 511) / 512;
+#pragma unroll
+    for (int j = 0; j < PF; j++) {
+      if (c0 + j * nw >= npass) break;
+      const int k = (c0 + j * nw) * 512 + 8 * lane;
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const h2 hv = as_h2(cur.xv[j][e]);
+        v[2 * e] = (float)hv.x;
+        v[2 * e + 1] = (float)hv.y;
+      }
+      if (bl > 0) {
+        if (a.signs)
+#pragma unroll
+          for (int e = 0; e < 8; e++) v[e] *= cur.sg[j][e >> 2][e & 3];
+        if (bl > 1) lbfly<1>(v);
+        if (bl > 2) lbfly<2>(v);
+        if (bl > 4) lbfly<4>(v);
+        if (bl > 8)
+#pragma unroll
+          for (int e = 0; e < 8; e++) v[e] = xbfly<1>(v[e], lane);
+        if (bl > 16)
+#pragma unroll
+          for (int e = 0; e < 8; e++) v[e] = xbfly<2>(v[e], lane);
+        if (bl > 32)
+#pragma unroll
+          for (int e = 0; e < 8; e++) v[e] = xbfly<4>(v[e], lane);
+        if (bl > 64)
+#pragma unroll
+          for (int e = 0; e < 8; e++) v[e] = xbfly<8>(v[e], lane);
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = (float)(_Float16)(v[e] * scale);
+      }
+      put8(xs, xsum, k, v, k < a.K);
+    }
+  }
+
+  static DEV XPre stage_load(const Args &a, const uint16_t *x, int) {
+    XPre p{};
+    if (a.img) {
+      const int n = img_words(a.K);
+#pragma unroll
+      for (int j = 0; j < PF; j++) p.xv[j] = a.img[min((int)threadIdx.x + j * (int)blockDim.x, n - 1)];
+      return p;
+    }
+    if (a.block > 128) return p;
+    return load_group(a, x, threadIdx.x >> 6, blockDim.x >> 6);
+  }
+  static DEV void stage(const Args &a, const uint16_t *x, u4 *xs, float *xsum, u4 *extra, int, const XPre &pre) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if (a.img) {  // xs and xsum are contiguous, laid out as the image
+      const int n = img_words(a.K), bd = blockDim.x;
+#pragma unroll
+      for (int j = 0; j < PF; j++)
+        if ((int)threadIdx.x + j * bd < n) xs[threadIdx.x + j * bd] = pre.xv[j];
+      for (int i = threadIdx.x + PF * bd; i < n; i += bd) xs[i] = a.img[i];
+      __syncthreads();
+      return;
+    }
     if (a.block > 128) {
       uint16_t *xh = (uint16_t *)xs;
       float *xr = (float *)extra;
@@ -262,58 +353,10 @@ struct FAffine {
       __syncthreads();
       return;
     }
-    constexpr int PF = 4;
-    const int bl = a.block;
-    const float scale = bl > 1 ? 1.0f / __builtin_sqrtf((float)bl) : 1.0f;
     const int npass = (a.K + 511) / 512;
-    for (int c0 = wave; c0 < npass; c0 += PF * nw) {
-      u4 xv[PF];
-      f4 sg[PF][2];
-#pragma unroll
-      for (int j = 0; j < PF; j++) {
-        const int k = min(min(c0 + j * nw, npass - 1) * 512 + 8 * lane, a.K - 8);
-        xv[j] = *(const u4 *)(x + k);
-        if (a.signs) {
-          sg[j][0] = *(const f4 *)(a.signs + k);
-          sg[j][1] = *(const f4 *)(a.signs + k + 4);
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < PF; j++) {
-        if (c0 + j * nw >= npass) break;
-        const int k = (c0 + j * nw) * 512 + 8 * lane;
-        float v[8];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const h2 hv = as_h2(xv[j][e]);
-          v[2 * e] = (float)hv.x;
-          v[2 * e + 1] = (float)hv.y;
-        }
-        if (bl > 0) {
-          if (a.signs)
-#pragma unroll
-            for (int e = 0; e < 8; e++) v[e] *= sg[j][e >> 2][e & 3];
-          if (bl > 1) lbfly<1>(v);
-          if (bl > 2) lbfly<2>(v);
-          if (bl > 4) lbfly<4>(v);
-          if (bl > 8)
-#pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = xbfly<1>(v[e], lane);
-          if (bl > 16)
-#pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = xbfly<2>(v[e], lane);
-          if (bl > 32)
-#pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = xbfly<4>(v[e], lane);
-          if (bl > 64)
-#pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = xbfly<8>(v[e], lane);
-#pragma unroll
-          for (int e = 0; e < 8; e++) v[e] = (float)(_Float16)(v[e] * scale);
-        }
-        put8(xs, xsum, k, v, k < a.K);
-      }
-    }
+    stage_group(a, xs, xsum, wave, nw, pre);  // first group: loads issued by stage_load
+    for (int c0 = wave + PF * nw; c0 < npass; c0 += PF * nw)
+      stage_group(a, xs, xsum, c0, nw, load_group(a, x, c0, nw));
     __syncthreads();
   }
 
@@ -431,15 +474,25 @@ static int num_cu_aff() {
 
 static bool pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
+// x staged once for every workgroup of the GEMV: one wave per 512-value pass writes the slots
+// and sums, laid out exactly as the GEMV's LDS (block <= 128).
+__global__ __launch_bounds__(64) void affine_prestage_kernel(FAffine<64, false>::Args a, const uint16_t *__restrict__ x,
+                                                             u4 *__restrict__ img) {
+  using F = FAffine<64, false>;
+  const int ug = (F::units(a.K) + 15) / 16;
+  const int c0 = blockIdx.x, nw = gridDim.x;
+  F::stage_group(a, img, (float *)(img + ug * 16 * F::R), c0, nw, F::load_group(a, x, c0, nw));
+}
+
 template <int GS>
 static int affine_gemv(const void *x, const float *signs, int block, const uint32_t *codes,
                        const void *scales, const void *biases, int bf16s, int K, int N, void *y,
-                       hipStream_t st) {
+                       hipStream_t st, const u4 *img = nullptr) {
   if (bf16s) {
-    const typename FAffine<GS, true>::Args a{codes, (const uint16_t *)scales, (const uint16_t *)biases, signs, block, K, N};
+    const typename FAffine<GS, true>::Args a{codes, (const uint16_t *)scales, (const uint16_t *)biases, signs, block, K, N, img};
     return launch_gemv<FAffine<GS, true>>(a, x, y, st);
   }
-  const typename FAffine<GS, false>::Args a{codes, (const uint16_t *)scales, (const uint16_t *)biases, signs, block, K, N};
+  const typename FAffine<GS, false>::Args a{codes, (const uint16_t *)scales, (const uint16_t *)biases, signs, block, K, N, img};
   return launch_gemv<FAffine<GS, false>>(a, x, y, st);
 }
 
@@ -515,8 +568,11 @@ extern "C" int ishz_affine_matmul(const void *x, int x_dtype, int M, int K, cons
                          group, y, S(stream));
 }
 
+// M > 1: the rotated activations (fp16). M = 1: the staged x image the GEMV's workgroups copy
+// (a null or smaller workspace at M = 1 stages x inside every workgroup instead).
 extern "C" size_t ishz_affine_workspace_size(int M, int K) {
-  return M > 1 ? (size_t)M * K * 2 : 0;
+  if (K <= 0 || M <= 0) return 0;
+  return M > 1 ? (size_t)M * K * 2 : (size_t)FAffine<64, false>::img_words(K) * 16;
 }
 
 extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, const float *signs,
@@ -529,6 +585,15 @@ extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, cons
   if (block > 0 && (!pow2(block) || block > 4096 || K % block)) return decline("bad Hadamard block");
   const int bf16s = scale_dtype == ISHZ_DT_BF16;
   hipStream_t st = S(stream);
+  if (M == 1 && block > 0 && block <= 128 && workspace && workspace_bytes >= ishz_affine_workspace_size(1, K)) {
+    const FAffine<64, false>::Args a{codes, nullptr, nullptr, signs, block, K, N, nullptr};
+    const int npass = (K + 511) / 512;
+    hipLaunchKernelGGL(affine_prestage_kernel, dim3(npass), dim3(64), 0, st, a, (const uint16_t *)x, (u4 *)workspace);
+    ISHZ_LAUNCH_CHECK("affine prestage launch");
+    const u4 *img = (const u4 *)workspace;
+    return group == 64 ? affine_gemv<64>(x, signs, block, codes, scales, biases, bf16s, K, N, y, st, img)
+                       : affine_gemv<128>(x, signs, block, codes, scales, biases, bf16s, K, N, y, st, img);
+  }
   if (block == 0 || M == 1)
     return affine_dispatch(x, M, K, signs, block, codes, scales, biases, bf16s, N, group, y, st);
   if (!workspace || workspace_bytes < ishz_affine_workspace_size(M, K))

@@ -2,14 +2,15 @@
 //
 // A wave owns a contiguous, equal share of row groups (64/LPR rows each, LPR lanes per row) and
 // streams their units as one sequence: lane `sub` takes units sub, sub + LPR, ... of each row, in
-// batches of B units; two register batches ping-pong, so the next batch's loads are in flight
-// while one is decoded. Loads are never predicated: a batch slot is valid for all lanes or none
+// batches of B units held in a ring of D register batches, so D - 1 batches' loads are in
+// flight while one is decoded. Loads are never predicated: a batch slot is valid for all lanes or none
 // (unless RAGGED), and an invalid slot reloads the lane's first unit, so the waitcnt pass only
-// waits for the batch being decoded. The first batch is issued before x is staged into LDS.
+// waits for the batch being decoded. The first batches are issued before x is staged into LDS.
 //
 // A format F provides: Args (pointers and sizes), Raw (one unit's registers), LaneC (per-lane
-// constants), units(K), load(args, row, u), dot(raw, UnitX, LaneC), stage(...) (fills the LDS
-// slots and sums of x, see UnitX), extra_lds_bytes(args), and R / Q (slots and sums per unit).
+// constants), units(K), load(args, row, u), dot(raw, UnitX, LaneC), stage_load(...) (x loads
+// issued first, kept in an XPre) and stage(...) (fills the LDS slots and sums of x, see UnitX),
+// extra_lds_bytes(args), and R / Q (slots and sums per unit).
 #pragma once
 #include <algorithm>
 #include <cstdlib>
@@ -54,7 +55,7 @@ DEV u2 perm0213(u2 a) {
   return r;
 }
 
-template <class F, int LPR, int B, bool RAGGED>
+template <class F, int LPR, int B, int D, bool RAGGED>
 __global__ __launch_bounds__(256) void gemv_kernel(typename F::Args args, const uint16_t *__restrict__ x,
                                                    uint16_t *__restrict__ y, int groups_per_wave) {
   static_assert(LPR % 16 == 0, "lanes per row must be a multiple of 16");
@@ -87,11 +88,27 @@ __global__ __launch_bounds__(256) void gemv_kernel(typename F::Args args, const 
     for (int i = 0; i < B; i++) r[i] = F::load(args, row, unit(bb, i));
   };
 
-  int g = gw * groups_per_wave, bi = 0;
-  typename F::Raw cur[B], alt[B];
-  load_batch(g, 0, cur);
+  // Ring of D register batches: batch i sits in buf[i % D]; before batch i is decoded, batch
+  // i + D - 1 is issued into the slot batch i - 1 freed. Load and consume cursors (group,
+  // batch-in-row) advance in step. x's first staging loads go out before the weight batches:
+  // the memory counter is in order, so staging then waits only for x.
+  const int g0 = gw * groups_per_wave;
+  auto advance = [&](int &gg, int &bb) {
+    if (++bb == nb) {
+      bb = 0;
+      gg++;
+    }
+  };
+  const typename F::XPre pre = F::stage_load(args, x, units);
+  typename F::Raw buf[D][B];
+  int gl = g0, bl = 0;
+#pragma unroll
+  for (int d = 0; d < D - 1; d++) {
+    load_batch(gl, bl, buf[d]);
+    advance(gl, bl);
+  }
 
-  F::stage(args, x, xs, xsum, extra, units);  // ends with a barrier
+  F::stage(args, x, xs, xsum, extra, units, pre);  // ends with a barrier
   const uint32_t mg = vconst(0x64006400u);
   const u4 *grid = extra, *sgn = extra + F::GRID_ENTRIES;
   const int lane_slot = (sub >> 4) * 16 * F::R + (sub & 15);
@@ -107,12 +124,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(typename F::Args args, const 
   };
 
   float acc = 0.0f;
-  auto advance = [&](int &gg, int &bb) {
-    if (++bb == nb) {
-      bb = 0;
-      gg++;
-    }
-  };
   auto consume = [&](int gg, int bb, const typename F::Raw *r) {
 #pragma unroll
     for (int i = 0; i < B; i++) {
@@ -130,18 +141,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(typename F::Args args, const 
       acc = 0.0f;
     }
   };
-  while (g < g_end) {
-    int g1 = g, b1 = bi;
-    advance(g1, b1);
-    load_batch(g1, b1, alt);
-    consume(g, bi, cur);
-    if (g1 >= g_end) break;
-    int g2 = g1, b2 = b1;
-    advance(g2, b2);
-    load_batch(g2, b2, cur);
-    consume(g1, b1, alt);
-    g = g2;
-    bi = b2;
+  int gc = g0, bc = 0;
+  while (gc < g_end) {
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+      load_batch(gl, bl, buf[(d + D - 1) % D]);
+      advance(gl, bl);
+      if (gc < g_end) consume(gc, bc, buf[d]);
+      advance(gc, bc);
+    }
   }
 }
 
@@ -149,26 +157,21 @@ int gemv_num_cu();
 int gemv_batch_override();  // ISHZ_GEMV_B (tuning)
 int gemv_occ_override();    // ISHZ_GEMV_OCC: resident waves per SIMD the grid is sized for (tuning)
 
-// Picks lanes per row and the batch size (units per lane per batch, <= F::MAXB) so a row's
-// units divide evenly when they can, and sizes the grid to one resident round of waves with
-// equal shares of row groups.
 // Grid: one resident round of waves (at most what the compiled kernel's registers and this
 // launch's LDS allow), each wave an equal share of row groups.
-template <class F, int LPR, int B, bool RAGGED>
-static int launch_gemv_k(const typename F::Args &a, const void *x, void *y, hipStream_t st) {
+template <class F, int LPR, int B, int D, bool RAGGED>
+static int launch_gemv_kd(const typename F::Args &a, const void *x, void *y, hipStream_t st) {
   constexpr int RPW = 64 / LPR;
   const int units = F::units(a.K);
   const size_t ug = (size_t)(units + 15) / 16;
   const size_t lds = ug * 16 * F::R * 16 + ug * 16 * F::Q * 4 + F::extra_lds_bytes(a);
   if (lds > 160 * 1024) return decline("K too large for the GEMV's LDS copy of x");
-  auto kern = gemv_kernel<F, LPR, B, RAGGED>;
+  auto kern = gemv_kernel<F, LPR, B, D, RAGGED>;
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds) != hipSuccess || per_cu < 1)
     per_cu = 1;
   const int groups = (a.N + RPW - 1) / RPW;
-  // Two waves per SIMD measured best on MI355X for every format at 17408x5120: fewer, longer
-  // waves amortise the x staging; more add no memory parallelism.
-  const int occ = gemv_occ_override() > 0 ? gemv_occ_override() : 2;
+  const int occ = gemv_occ_override() > 0 ? gemv_occ_override() : F::occ(a);
   const int capacity = gemv_num_cu() * 4 * std::min(occ, per_cu);
   const int per_wave = (groups + capacity - 1) / capacity;
   const int waves = (groups + per_wave - 1) / per_wave;
@@ -176,6 +179,17 @@ static int launch_gemv_k(const typename F::Args &a, const void *x, void *y, hipS
                      per_wave);
   ISHZ_LAUNCH_CHECK("gemv launch");
   return ISHZ_OK;
+}
+
+int gemv_depth_override();  // ISHZ_GEMV_D (tuning)
+
+template <class F, int LPR, int B, bool RAGGED>
+static int launch_gemv_k(const typename F::Args &a, const void *x, void *y, hipStream_t st) {
+  switch (gemv_depth_override() ? gemv_depth_override() : F::DEPTH) {
+    case 4: return launch_gemv_kd<F, LPR, B, 4, RAGGED>(a, x, y, st);
+    case 3: return launch_gemv_kd<F, LPR, B, 3, RAGGED>(a, x, y, st);
+    default: return launch_gemv_kd<F, LPR, B, 2, RAGGED>(a, x, y, st);
+  }
 }
 
 template <class F, int LPR, int B>

@@ -231,6 +231,10 @@ int gemv_batch_override() {
   static const int v = env_int("ISHZ_GEMV_B");
   return v;
 }
+int gemv_depth_override() {
+  static const int v = env_int("ISHZ_GEMV_D");
+  return v;
+}
 int gemv_occ_override() {
   static const int v = env_int("ISHZ_GEMV_OCC");
   return v;

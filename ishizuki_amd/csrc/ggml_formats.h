@@ -55,53 +55,90 @@ struct GgmlGemv {
     int K, N;
   };
   static constexpr int GRID_ENTRIES = 512;
+  // Resident waves per SIMD the grid is sized for: two measured best on MI355X at 17408x5120
+  // (fewer, longer waves amortise the x staging every workgroup repeats).
+  static int occ(const Args &) { return 2; }
   static __host__ __device__ int units(int K) { return K / D::BS * D::UPB / D::UNIT_BLOCKS; }
   static size_t extra_lds_bytes(const Args &) { return D::GRID ? (512 + 128) * 16 : 0; }
   static DEV auto load(const Args &a, int row, int u) { return D::load_row(a.w + (size_t)row * a.rb, u); }
-  // Loads for U slots (sums) per thread are issued together before any is stored, so staging
-  // costs a memory latency per U items rather than one each.
-  static DEV void stage(const Args &a, const uint16_t *x, u4 *xs, float *xsum, u4 *extra, int units) {
+  // Loads for U slots (US sums) per thread are issued together before any is stored, so
+  // staging costs a memory latency per U items rather than one each; the first round's loads
+  // are issued by stage_load, ahead of the weight batches.
+  static constexpr int U = 4, US = 2, SLMAX = 4;  // SUM_LEN <= 32
+  struct XPre {
+    u4 v[U];
+    u4 sv[US][SLMAX];
+  };
+  static DEV void load_slots(const uint16_t *x, int units, int i0, u4 *v) {
+    const int ns = (units + 15) / 16 * 16 * D::R;
+#pragma unroll
+    for (int j = 0; j < U; j++) {
+      const int i = min(i0 + j * (int)blockDim.x, ns - 1);
+      const int u = min((i / (16 * D::R)) * 16 + (i & 15), units - 1), r = (i >> 4) % D::R;
+      v[j] = *(const u4 *)(x + D::slot_k(u, r));
+    }
+  }
+  static DEV void load_sums(const uint16_t *x, int units, int i0, u4 (*v)[SLMAX]) {
+    constexpr int SL = D::SUM_LEN / 8;
+    if constexpr (D::XSUM) {
+      const int nq = (units + 15) / 16 * 16 * D::Q;
+#pragma unroll
+      for (int j = 0; j < US; j++) {
+        const int i = min(i0 + j * (int)blockDim.x, nq - 1);
+        const int u = min((i / (16 * D::Q)) * 16 + (i & 15), units - 1), q = (i >> 4) % D::Q;
+        const u4 *p = (const u4 *)(x + D::sum_k(u, q));
+#pragma unroll
+        for (int h = 0; h < SL; h++) v[j][h] = p[h];
+      }
+    }
+  }
+  static DEV XPre stage_load(const Args &, const uint16_t *x, int units) {
+    XPre p;
+    load_slots(x, units, threadIdx.x, p.v);
+    load_sums(x, units, threadIdx.x, p.sv);
+    return p;
+  }
+  static DEV void store_slots(u4 *xs, int units, int i0, const u4 *v) {
+    const int ns = (units + 15) / 16 * 16 * D::R;
+#pragma unroll
+    for (int j = 0; j < U; j++) {
+      const int i = i0 + j * (int)blockDim.x;
+      if (i < ns && (i / (16 * D::R)) * 16 + (i & 15) < units) xs[i] = perm0213(v[j]);
+    }
+  }
+  static DEV void store_sums(float *xsum, int units, int i0, const u4 (*v)[SLMAX]) {
+    constexpr int SL = D::SUM_LEN / 8;
+    const int nq = (units + 15) / 16 * 16 * D::Q;
+#pragma unroll
+    for (int j = 0; j < US; j++) {
+      const int i = i0 + j * (int)blockDim.x;
+      if (i < nq && (i / (16 * D::Q)) * 16 + (i & 15) < units) {
+        float sm = 0.0f;
+#pragma unroll
+        for (int h = 0; h < SL; h++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) sm = dot2(v[j][h][e], 0x3C003C00u, sm);  // + both halves
+        xsum[i] = sm;
+      }
+    }
+  }
+  static DEV void stage(const Args &a, const uint16_t *x, u4 *xs, float *xsum, u4 *extra, int units,
+                        const XPre &pre) {
     const int ug = (units + 15) / 16, bd = blockDim.x;
-    constexpr int U = 4, US = 2, SL = D::SUM_LEN / 8;
     const int ns = ug * 16 * D::R;
-    for (int i0 = threadIdx.x; i0 < ns; i0 += U * bd) {
+    store_slots(xs, units, threadIdx.x, pre.v);  // first round: loads issued by stage_load
+    for (int i0 = threadIdx.x + U * bd; i0 < ns; i0 += U * bd) {
       u4 v[U];
-#pragma unroll
-      for (int j = 0; j < U; j++) {
-        const int i = min(i0 + j * bd, ns - 1);
-        const int u = min((i / (16 * D::R)) * 16 + (i & 15), units - 1), r = (i >> 4) % D::R;
-        v[j] = *(const u4 *)(x + D::slot_k(u, r));
-      }
-#pragma unroll
-      for (int j = 0; j < U; j++) {
-        const int i = i0 + j * bd;
-        if (i < ns && (i / (16 * D::R)) * 16 + (i & 15) < units) xs[i] = perm0213(v[j]);
-      }
+      load_slots(x, units, i0, v);
+      store_slots(xs, units, i0, v);
     }
     if constexpr (D::XSUM) {
       const int nq = ug * 16 * D::Q;
-      for (int i0 = threadIdx.x; i0 < nq; i0 += US * bd) {
-        u4 v[US][SL];
-#pragma unroll
-        for (int j = 0; j < US; j++) {
-          const int i = min(i0 + j * bd, nq - 1);
-          const int u = min((i / (16 * D::Q)) * 16 + (i & 15), units - 1), q = (i >> 4) % D::Q;
-          const u4 *p = (const u4 *)(x + D::sum_k(u, q));
-#pragma unroll
-          for (int h = 0; h < SL; h++) v[j][h] = p[h];
-        }
-#pragma unroll
-        for (int j = 0; j < US; j++) {
-          const int i = i0 + j * bd;
-          if (i < nq && (i / (16 * D::Q)) * 16 + (i & 15) < units) {
-            float sm = 0.0f;
-#pragma unroll
-            for (int h = 0; h < SL; h++)
-#pragma unroll
-              for (int e = 0; e < 4; e++) sm += (float)as_h2(v[j][h][e]).x + (float)as_h2(v[j][h][e]).y;
-            xsum[i] = sm;
-          }
-        }
+      store_sums(xsum, units, threadIdx.x, pre.sv);
+      for (int i0 = threadIdx.x + US * bd; i0 < nq; i0 += US * bd) {
+        u4 v[US][SLMAX];
+        load_sums(x, units, i0, v);
+        store_sums(xsum, units, i0, v);
       }
     }
     if constexpr (D::GRID) build_iq2xs_tables_perm(extra, extra + 512);
@@ -117,7 +154,7 @@ struct FQ4_0 : GgmlGemv<FQ4_0> {
   // GEMV unit: two blocks (36 bytes, dword aligned when rows hold an even number of blocks),
   // 64 weights; so the GEMV needs K % 64 == 0 (the verify kernel takes any K % 32 == 0).
   static constexpr int UPB = 1, UNIT_BLOCKS = 2, GEMV_K_MULT = 64;
-  static constexpr int MAXB = 5, PREFB = 2;
+  static constexpr int MAXB = 5, PREFB = 2, DEPTH = 2;
   static constexpr bool XSUM = true, GRID = false;
   static constexpr int R = 8, Q = 4;  // slots k0 + 8r; sums of 16 at k0 + 16q
   static DEV int slot_k(int u, int r) { return 64 * u + 8 * r; }
@@ -191,7 +228,7 @@ struct FQ4_K : GgmlGemv<FQ4_K> {
   static constexpr uint32_t TYPE = ISHZ_GGML_Q4_K;
   static constexpr int BS = 256, TS = 144, UPB = 4;  // unit: 32 B of qs (chunk jj), 64 weights
   static constexpr int UNIT_BLOCKS = 1, GEMV_K_MULT = 256;
-  static constexpr int MAXB = 5, PREFB = 2;
+  static constexpr int MAXB = 5, PREFB = 2, DEPTH = 2;
   static constexpr bool XSUM = true, GRID = false;
   static constexpr int R = 8, Q = 2;  // slots: lo run k0 + 8i (i < 4), hi run k0 + 32 + 8i
   static DEV int k0_of(int u) { return (u >> 2) * 256 + (u & 3) * 64; }
@@ -314,7 +351,7 @@ struct FQ6_K : GgmlGemv<FQ6_K> {
   static constexpr uint32_t TYPE = ISHZ_GGML_Q6_K;
   static constexpr int BS = 256, TS = 210, UPB = 4;  // unit: (n, l-half), 64 weights
   static constexpr int UNIT_BLOCKS = 1, GEMV_K_MULT = 256;
-  static constexpr int MAXB = 5, PREFB = 2;
+  static constexpr int MAXB = 5, PREFB = 2, DEPTH = 2;
   static constexpr bool XSUM = true, GRID = false;
   static constexpr int R = 8, Q = 4;  // slot 2qq + i: k0 + 32qq + 8i; sum qq: k0 + 32qq
   static DEV int k0_of(int u) { return (u >> 2) * 256 + ((u >> 1) & 1) * 128 + (u & 1) * 16; }
@@ -432,7 +469,7 @@ struct FIQ2_XS : GgmlGemv<FIQ2_XS> {
   static constexpr uint32_t TYPE = ISHZ_GGML_IQ2_XS;
   static constexpr int BS = 256, TS = 74, UPB = 4;  // unit: two groups, 16 B of qs, 64 weights
   static constexpr int UNIT_BLOCKS = 1, GEMV_K_MULT = 256;
-  static constexpr int MAXB = 5, PREFB = 2;
+  static constexpr int MAXB = 5, PREFB = 2, DEPTH = 2;
   static constexpr bool XSUM = false, GRID = true;
   static constexpr int R = 8, Q = 1;  // slot l: k0 + 8l
   static DEV int slot_k(int u, int r) { return (u >> 2) * 256 + (u & 3) * 64 + 8 * r; }

@@ -72,6 +72,21 @@ def test_affine_rotated_linear(M, signs_seed):
     assert_close(y.float().cpu().numpy(), ref, what=f"rotated M={M}")
 
 
+@pytest.mark.parametrize("block", [2, 32, 64, 128, 512])
+@pytest.mark.parametrize("prestage", [True, False])
+@pytest.mark.parametrize("K", [1152, 5120])
+def test_affine_rotated_gemv_staging(block, prestage, K):
+    """M = 1 with x staged by the prestage kernel or inside every workgroup; K = 1152 leaves a
+    partial 512-value pass."""
+    if K % block:
+        pytest.skip("the rotation block must divide K")
+    N = 700
+    (x, w, s, b), signs, ref = affine_case(N, K, 1, 64, seed=block + K, block=block, signs_seed=3)
+    y = affine.linear(x, w, s, b, signs=torch.from_numpy(signs), block=block, group_size=64, _prestage=prestage)
+    assert y is not None
+    assert_close(y.float().cpu().numpy(), ref, what=f"gemv block={block} prestage={prestage} K={K}")
+
+
 def test_affine_bf16_scales():
     N, K = 300, 1024
     codes, s, b = synth.affine_pack(N, K, group=64, seed=3)
