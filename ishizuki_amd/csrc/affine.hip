@@ -75,7 +75,7 @@ __global__ __launch_bounds__(256) void hadamard_wave_kernel(const void *__restri
                                                             const float *__restrict__ signs,
                                                             int inverse, void *__restrict__ y,
                                                             int out_dt) {
-  const size_t c = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const size_t c = (size_t)blockIdx.x * 4 + wave_id();
   if (c >= chunks) return;
   const int lane = threadIdx.x & 63;
   const size_t base = c * 128 + 2 * lane;
@@ -329,7 +329,7 @@ struct FAffine {
     return load_group(a, x, threadIdx.x >> 6, blockDim.x >> 6);
   }
   static DEV void stage(const Args &a, const uint16_t *x, u4 *xs, float *xsum, u4 *extra, int, const XPre &pre) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id(), nw = blockDim.x >> 6;
     if (a.img) {  // xs and xsum are contiguous, laid out as the image
       const int n = img_words(a.K), bd = blockDim.x;
 #pragma unroll
@@ -392,7 +392,7 @@ __global__ __launch_bounds__(1024) void affine_verify(const uint16_t *__restrict
                                                       const uint16_t *__restrict__ biases,
                                                       int bf16s, int N, uint16_t *__restrict__ y) {
   extern __shared__ __align__(16) float red[];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, KS = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id(), KS = blockDim.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int groups = K / 64, gpr = K / GS;
   const int n0 = blockIdx.x * 16 * T;
@@ -460,6 +460,182 @@ __global__ __launch_bounds__(1024) void affine_verify(const uint16_t *__restrict
   }
 }
 
+// ------------------------------------------------------------------- verify v2 (MFMA, M <= 16)
+// Streaming MFMA GEMM for 2..16 drafted rows: each weight is decoded once into an MFMA B operand
+// and multiplied against every token. A workgroup (8 waves) owns a run of 16-row tiles; its waves
+// split each tile's K steps (step j of a tile goes to wave j % 8) and sum their partials in LDS.
+//
+// Step = 4 units (256 weights) of the tile's 16 rows: lane (n, g) = (lane % 16, lane / 16) loads
+// the 16 code bytes of unit 4j + g of row n, i.e. one 128-bit load per lane, and decodes slot r
+// (r < 8) of it into the B operand of MFMA r. A is "diagonal": A row m = 4 tt + gg holds token
+// tt's staged x (the GEMV's slot image) for k-slot gg only, so C row 4 tt + gg collects token
+// tt's dot with unit 4j + gg alone, and lane (n, G) ends each step with token G's four unit
+// partials of row n in its four C registers, ready for the units' scale and bias. Four tokens
+// per MFMA; NQ token quads reuse the same decoded B.
+template <int GS, bool BF16S, int NQ, int D>
+__global__ __launch_bounds__(512) void affine_vgemm(const uint16_t *__restrict__ x, int M, int K,
+                                                    const uint32_t *__restrict__ codes,
+                                                    const uint16_t *__restrict__ scales,
+                                                    const uint16_t *__restrict__ biases, int N,
+                                                    uint16_t *__restrict__ y, int Kc, int tiles_per_wg) {
+  using F = FAffine<GS, BF16S>;
+  constexpr int R = F::R;
+  extern __shared__ __align__(16) u4 vlds[];
+  const int lane = threadIdx.x & 63, wave = wave_id(), nw = blockDim.x >> 6;
+  const int n = lane & 15, G = lane >> 4;
+  const int units = K / 64, gpr = K / GS;
+  const int ntiles = (N + 15) / 16;
+  const int tb = blockIdx.x * tiles_per_wg, te = min(tb + tiles_per_wg, ntiles);
+  // token images IW + 1 words apart: consecutive tokens start 16 bytes apart in the LDS banks
+  const int IW = F::img_words(Kc) + 1, ugc = (Kc / 64 + 15) / 16;
+  u4 *zero = vlds + M * IW;                            // 8 slots x 16 lanes of zeros
+  float *accb = (float *)(zero + 128);                 // [wave][tile][quad][lane] partials
+  const uint32_t mg = vconst(0x64006400u);
+
+  for (int i = threadIdx.x; i < 128; i += blockDim.x) zero[i] = u4{0, 0, 0, 0};
+  for (int i = threadIdx.x; i < nw * tiles_per_wg * NQ * 64; i += blockDim.x) accb[i] = 0.0f;
+  // A row of this lane: token tt = n / 4 of each quad, unit group gg = n % 4; only gg == G holds x.
+  const int tt = n >> 2, gg = n & 3;
+
+  for (int kc0 = 0; kc0 < K; kc0 += Kc) {
+    const int klen = min(Kc, K - kc0), ucs = klen / 64, steps = ucs / 4;
+    // ---- stage x[tk][kc0 .. kc0 + klen) of every token: 8 values per lane per item
+    {
+      const int per_tok = (klen + 511) / 512, items = M * per_tok;
+      constexpr int PF = 4;
+      for (int i0 = wave; i0 < items; i0 += PF * nw) {
+        u4 xv[PF];
+#pragma unroll
+        for (int j = 0; j < PF; j++) {
+          const int it = min(i0 + j * nw, items - 1), tk = it / per_tok, ps = it % per_tok;
+          const int k = min(ps * 512 + 8 * lane, klen - 8);
+          xv[j] = *(const u4 *)(x + (size_t)tk * K + kc0 + k);
+        }
+#pragma unroll
+        for (int j = 0; j < PF; j++) {
+          const int it = i0 + j * nw;
+          if (it >= items) break;
+          const int tk = it / per_tok, ps = it % per_tok, k = ps * 512 + 8 * lane;
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const h2 hv = as_h2(xv[j][e]);
+            v[2 * e] = (float)hv.x;
+            v[2 * e + 1] = (float)hv.y;
+          }
+          u4 *img = vlds + tk * IW;
+          F::put8(img, (float *)(img + ugc * 16 * R), k, v, k < klen);
+        }
+      }
+      __syncthreads();
+    }
+
+    // ---- stream: this wave's (tile, step) sequence, steps wave, wave + nw, ... of each tile.
+    // Load and consume cursors (tile, step) advance in step; loads past the end re-read the
+    // wave's last step (always in range) and are dropped.
+    struct Raw {
+      u4 q;
+      uint32_t s[2], b[2];
+    };
+    const bool active = wave < steps && tb < te;
+    const int j_last = wave + (steps - 1 - wave) / nw * nw;  // this wave's last step of a tile
+    auto load = [&](int tile, int j, Raw &r) {
+      const int row = min(min(tile, te - 1) * 16 + n, N - 1);
+      const int u = kc0 / 64 + 4 * min(j, j_last);  // first unit of the step
+      r.q = *(const u4 *)(codes + (size_t)row * (K / 16) + 4 * (u + G));
+      if constexpr (GS == 64) {
+        const u2 sv = *(const u2 *)(scales + (size_t)row * gpr + u), bv = *(const u2 *)(biases + (size_t)row * gpr + u);
+        r.s[0] = sv.x, r.s[1] = sv.y, r.b[0] = bv.x, r.b[1] = bv.y;
+      } else {
+        r.s[0] = scales[(size_t)row * gpr + u / 2] | (uint32_t)scales[(size_t)row * gpr + u / 2 + 1] << 16;
+        r.b[0] = biases[(size_t)row * gpr + u / 2] | (uint32_t)biases[(size_t)row * gpr + u / 2 + 1] << 16;
+        r.s[1] = r.s[0], r.b[1] = r.b[0];
+      }
+    };
+    auto advance = [&](int &tile, int &j) {
+      j += nw;
+      if (j > j_last) {
+        j = wave;
+        tile++;
+      }
+    };
+    Raw ring[D];
+    int lt = tb, lj = wave;
+    if (active) {
+#pragma unroll
+      for (int d = 0; d < D - 1; d++) {
+        load(lt, lj, ring[d]);
+        advance(lt, lj);
+      }
+    }
+    float acc[NQ];
+    int ct = tb, cj = wave;
+    while (active && ct < te) {
+#pragma unroll
+      for (int d = 0; d < D; d++) {
+        load(lt, lj, ring[(d + D - 1) % D]);
+        advance(lt, lj);
+        if (ct >= te) break;
+        const int tl = ct - tb, j = cj;
+        if (j == wave) {
+#pragma unroll
+          for (int q = 0; q < NQ; q++) acc[q] = accb[((wave * tiles_per_wg + tl) * NQ + q) * 64 + lane];
+        }
+        const Raw &r = ring[d];
+        // B operands: slot r2 of the unit (word r2 / 2, pairs 4 (r2 % 2) .. + 3)
+        u4 B[8];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const uint32_t w = r.q[t], w10 = w >> 10;
+          B[2 * t] = u4{and_or(w, 0x00030003u, mg), and_or(w, 0x000C000Cu, mg), and_or(w, 0x00300030u, mg),
+                        and_or(w, 0x00C000C0u, mg)};
+          B[2 * t + 1] = u4{and_or(w, 0x03000300u, mg), and_or(w10, 0x00030003u, mg),
+                            and_or(w10, 0x000C000Cu, mg), and_or(w10, 0x00300030u, mg)};
+        }
+        const int ua = 4 * j + gg;  // chunk-relative unit of this lane's A row
+        float sc[4], bi[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const uint32_t sv = GS == 64 ? (r.s[e >> 1] >> (16 * (e & 1))) : (r.s[0] >> (16 * (e >> 1)));
+          const uint32_t bv = GS == 64 ? (r.b[e >> 1] >> (16 * (e & 1))) : (r.b[0] >> (16 * (e >> 1)));
+          sc[e] = F::ld_s(sv & 0xffffu);
+          bi[e] = F::ld_s(bv & 0xffffu);
+        }
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {
+          const int tka = 4 * q + tt;  // token of this lane's A row
+          const u4 *ab = (gg == G && tka < M) ? vlds + tka * IW + (ua >> 4) * 16 * R + (ua & 15) : zero;
+          f4 C = f4{0, 0, 0, 0};
+#pragma unroll
+          for (int r2 = 0; r2 < 8; r2++) C = mfma32(as_h8(ab[16 * r2]), as_h8(B[r2]), C);
+          // lane (n, G): token 4q + G, units 4j .. 4j + 3 of row n
+          const int tkc = min(4 * q + G, M - 1);
+          const float *sm = (const float *)(vlds + tkc * IW + ugc * 16 * R) + ((4 * j) >> 4) * 32 + ((4 * j) & 15);
+          const f4 off = *(const f4 *)sm, X = *(const f4 *)(sm + 16);
+          float a = acc[q];
+#pragma unroll
+          for (int e = 0; e < 4; e++) a += sc[e] * (C[e] - off[e]) + bi[e] * X[e];
+          acc[q] = a;
+        }
+        if (j == j_last) {
+#pragma unroll
+          for (int q = 0; q < NQ; q++) accb[((wave * tiles_per_wg + tl) * NQ + q) * 64 + lane] = acc[q];
+        }
+        advance(ct, cj);
+      }
+    }
+    __syncthreads();  // partials written; x image free for the next chunk
+  }
+  // ---- sum the waves' partials and write y
+  for (int o = threadIdx.x; o < (te - tb) * NQ * 64; o += blockDim.x) {
+    const int tl = o / (NQ * 64), q = (o / 64) % NQ, l = o % 64;
+    float s = 0.0f;
+    for (int w = 0; w < nw; w++) s += accb[((w * tiles_per_wg + tl) * NQ + q) * 64 + l];
+    const int tk = 4 * q + (l >> 4), row = (tb + tl) * 16 + (l & 15);
+    if (tk < M && row < N) y[(size_t)tk * N + row] = f2h(s);
+  }
+}
+
 // ------------------------------------------------------------------- host
 static int num_cu_aff() {
   static int n = [] {
@@ -496,10 +672,46 @@ static int affine_gemv(const void *x, const float *signs, int block, const uint3
   return launch_gemv<FAffine<GS, false>>(a, x, y, st);
 }
 
+template <int GS, bool BF16S, int NQ>
+static int affine_vgemm_launch(const void *x, int M, int K, const uint32_t *codes, const void *scales,
+                               const void *biases, int N, void *y, hipStream_t st) {
+  using F = FAffine<GS, BF16S>;
+  constexpr int D = 4;
+  const int ntiles = (N + 15) / 16;
+  const int T = (ntiles + num_cu_aff() - 1) / num_cu_aff();  // tiles per workgroup: one round of CUs
+  const int wgs = (ntiles + T - 1) / T;
+  constexpr int NW = 8;  // waves per workgroup: two per SIMD, so one issues while the other waits
+  const size_t fixed = 128 * 16 + (size_t)NW * T * NQ * 64 * 4;
+  const size_t budget = 150 * 1024;
+  int Kc = K;
+  auto need = [&](int kc) { return fixed + (size_t)M * (F::img_words(kc) + 1) * 16; };
+  while (Kc > 256 && need(Kc) > budget) Kc -= 256;
+  if (need(Kc) > budget) return decline("verify workspace does not fit in LDS");
+  const size_t lds = need(Kc);
+  hipLaunchKernelGGL((affine_vgemm<GS, BF16S, NQ, D>), dim3(wgs), dim3(64 * NW), lds, st, (const uint16_t *)x, M, K,
+                     codes, (const uint16_t *)scales, (const uint16_t *)biases, N, (uint16_t *)y, Kc, T);
+  ISHZ_LAUNCH_CHECK("affine verify launch");
+  return ISHZ_OK;
+}
+
+template <int GS, bool BF16S>
+static int affine_vgemm_nq(const void *x, int M, int K, const uint32_t *codes, const void *scales,
+                           const void *biases, int N, void *y, hipStream_t st) {
+  switch ((M + 3) / 4) {
+    case 1: return affine_vgemm_launch<GS, BF16S, 1>(x, M, K, codes, scales, biases, N, y, st);
+    case 2: return affine_vgemm_launch<GS, BF16S, 2>(x, M, K, codes, scales, biases, N, y, st);
+    case 3: return affine_vgemm_launch<GS, BF16S, 3>(x, M, K, codes, scales, biases, N, y, st);
+    default: return affine_vgemm_launch<GS, BF16S, 4>(x, M, K, codes, scales, biases, N, y, st);
+  }
+}
+
 template <int GS>
 static int affine_verify_launch(const void *x, int M, int K, const uint32_t *codes,
                                 const void *scales, const void *biases, int bf16s, int N, void *y,
                                 hipStream_t st) {
+  if (K % 256 == 0 && !getenv("ISHZ_OLD_VERIFY"))
+    return bf16s ? affine_vgemm_nq<GS, true>(x, M, K, codes, scales, biases, N, y, st)
+                 : affine_vgemm_nq<GS, false>(x, M, K, codes, scales, biases, N, y, st);
   constexpr int T = 2;
   const int wgs = (N + 16 * T - 1) / (16 * T);
   const int groups = K / 64;

@@ -87,6 +87,10 @@ DEV uint32_t vconst(uint32_t c) {
   return r;
 }
 
+// Wave index within the workgroup as a wave-uniform (scalar) value, so that everything derived
+// from it is computed on the scalar unit.
+DEV int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
 // fp32 += a.lo*b.lo + a.hi*b.hi (v_dot2_f32_f16).
 DEV float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);

@@ -77,7 +77,7 @@ __global__ __launch_bounds__(1024) void exl3_mm(const uint16_t *__restrict__ xh,
                                                 float *__restrict__ yh) {
   using TR = Trellis<KA, HALF>;
   extern __shared__ __align__(16) float red[];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, KS = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id(), KS = blockDim.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int tn = blockIdx.x, tiles_n = N / 16, tiles_k = K / 16;
   const typename TR::Win wn = TR::window(8 * (4 * (j & 7) + g) + 4 * (j >> 3));
@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256) void exl3_dequant_kernel(const uint32_t *__res
                                                            int K, int N, int cb, void *out,
                                                            int dt) {
   using TR = Trellis<KA, HALF>;
-  const size_t tile = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const size_t tile = blockIdx.x * 4 + wave_id();
   const int tiles_n = N / 16;
   if (tile >= (size_t)(K / 16) * tiles_n) return;
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
@@ -157,7 +157,7 @@ __global__ __launch_bounds__(256) void exl3_rotate_kernel(const void *__restrict
                                                           const uint16_t *__restrict__ scales,
                                                           int before, void *__restrict__ y,
                                                           int out_dt) {
-  const size_t blk = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const size_t blk = (size_t)blockIdx.x * 4 + wave_id();
   if (blk >= blocks) return;
   const int lane = threadIdx.x & 63;
   const size_t base = blk * 128 + 2 * lane;

@@ -68,7 +68,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(typename F::Args args, const 
   u4 *extra = (u4 *)(xsum + ugroups * 16 * F::Q);  // format tables / scratch
 
   constexpr int RPW = 64 / LPR;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int sub = lane % LPR, rg = lane / LPR;
   const int nb = (units + B * LPR - 1) / (B * LPR);  // batches per row
   const int gw = blockIdx.x * (blockDim.x >> 6) + wave;

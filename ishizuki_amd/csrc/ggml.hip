@@ -47,7 +47,7 @@ __global__ __launch_bounds__(1024) void verify_kernel(const uint16_t *__restrict
                                                       const uint8_t *__restrict__ w, int N,
                                                       uint16_t *__restrict__ y) {
   extern __shared__ __align__(16) uint32_t vsm[];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, KS = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id(), KS = blockDim.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   u4 *grid = (u4 *)vsm, *sgn = grid + 512;
   float *red = (float *)(vsm + (F::GRID ? (512 + 128) * 4 : 0));

@@ -41,7 +41,7 @@ DEV void argmax_merge(float &v, int &e, float ov, int oe) {
 __global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict__ logits, int T,
                                                          int E, int k, int normalize, MoeRoute R) {
   extern __shared__ int32_t cnt[];  // E counts
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id(), waves = blockDim.x >> 6;
   for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
   __syncthreads();
   for (int t = wave; t < T; t += waves) {
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(1024) void moe_gate_up_kernel(const uint16_t *__res
   const int a = blockIdx.y;
   if (a >= R.count[0]) return;
   const int e = R.active[a], p0 = R.offs[e], p1 = R.offs[e + 1];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, KS = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id(), KS = blockDim.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int nblk = H / F::BS;
   const size_t rb = (size_t)nblk * F::TS;
@@ -176,7 +176,7 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(const uint16_t *__restri
   const int a = blockIdx.y;
   if (a >= R.count[0]) return;
   const int e = R.active[a], p0 = R.offs[e], p1 = R.offs[e + 1];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, KS = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id(), KS = blockDim.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int nblk = I / F::BS;
   const size_t rb = (size_t)nblk * F::TS;
