@@ -66,15 +66,16 @@ def verify_apply(x, weight, scales, biases, group_size=64, bits=2):
 def linear(x, weight, scales, biases, signs=None, block=0, group_size=64, bits=2, _prestage=True):
     """Rotated PackedLinear forward: rotate (fused for one row) then the quantized matmul.
 
-    For one row with block <= 128 the workspace holds x rotated and staged once for every
-    workgroup; `_prestage=False` passes none, so each workgroup rotates x itself (test hook)."""
+    With block <= 128 the workspace holds every row's x rotated and staged once for all
+    workgroups; `_prestage=False` passes none, so each workgroup rotates x itself (test hook; the
+    general path for other blocks needs the workspace)."""
     require_cuda(x, weight, scales, biases)
     x = x.contiguous()
     M, K = x.shape
     N = weight.shape[0]
     y = torch.empty((M, N), dtype=x.dtype, device=x.device)
     L = _lib.lib()
-    ws_bytes = L.ishz_affine_workspace_size(M, K) if block and (_prestage or M > 1) else 0
+    ws_bytes = L.ishz_affine_workspace_size(M, K) if block and _prestage else 0
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
     s = None
     if block and signs is not None:

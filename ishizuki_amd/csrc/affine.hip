@@ -249,6 +249,31 @@ struct FAffine {
     return (lane & M) ? t - v : v + t;
   }
 
+  // hadamardRotate on a lane's eight consecutive values: sign flip, butterflies (h = 1, 2, 4
+  // in-lane, 8 .. 64 across lanes) and 1/sqrt(block), rounded to fp16 (block <= 128).
+  static DEV void rot8(float *v, const f4 *sg, int bl, float scale, int lane) {
+    if (sg)
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] *= sg[e >> 2][e & 3];
+    if (bl > 1) lbfly<1>(v);
+    if (bl > 2) lbfly<2>(v);
+    if (bl > 4) lbfly<4>(v);
+    if (bl > 8)
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] = xbfly<1>(v[e], lane);
+    if (bl > 16)
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] = xbfly<2>(v[e], lane);
+    if (bl > 32)
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] = xbfly<4>(v[e], lane);
+    if (bl > 64)
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] = xbfly<8>(v[e], lane);
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = (float)(_Float16)(v[e] * scale);
+  }
+
   // Eight consecutive x per lane, 512 per wave pass: hadamardRotate's sign flip, butterflies
   // (h = 1, 2, 4 in-lane, 8 .. 64 across lanes) and 1/sqrt(block), rounded to fp16 as the
   // reference's rotated activation is, then written to the slots. Loads for PF passes are issued
@@ -291,28 +316,7 @@ struct FAffine {
         v[2 * e] = (float)hv.x;
         v[2 * e + 1] = (float)hv.y;
       }
-      if (bl > 0) {
-        if (a.signs)
-#pragma unroll
-          for (int e = 0; e < 8; e++) v[e] *= cur.sg[j][e >> 2][e & 3];
-        if (bl > 1) lbfly<1>(v);
-        if (bl > 2) lbfly<2>(v);
-        if (bl > 4) lbfly<4>(v);
-        if (bl > 8)
-#pragma unroll
-          for (int e = 0; e < 8; e++) v[e] = xbfly<1>(v[e], lane);
-        if (bl > 16)
-#pragma unroll
-          for (int e = 0; e < 8; e++) v[e] = xbfly<2>(v[e], lane);
-        if (bl > 32)
-#pragma unroll
-          for (int e = 0; e < 8; e++) v[e] = xbfly<4>(v[e], lane);
-        if (bl > 64)
-#pragma unroll
-          for (int e = 0; e < 8; e++) v[e] = xbfly<8>(v[e], lane);
-#pragma unroll
-        for (int e = 0; e < 8; e++) v[e] = (float)(_Float16)(v[e] * scale);
-      }
+      if (bl > 0) rot8(v, a.signs ? cur.sg[j] : nullptr, bl, scale, lane);
       put8(xs, xsum, k, v, k < a.K);
     }
   }
@@ -477,7 +481,9 @@ __global__ __launch_bounds__(512) void affine_vgemm(const uint16_t *__restrict__
                                                     const uint32_t *__restrict__ codes,
                                                     const uint16_t *__restrict__ scales,
                                                     const uint16_t *__restrict__ biases, int N,
-                                                    uint16_t *__restrict__ y, int Kc, int tiles_per_wg) {
+                                                    uint16_t *__restrict__ y, int Kc, int tiles_per_wg,
+                                                    const float *__restrict__ signs, int block,
+                                                    const u4 *__restrict__ img) {
   using F = FAffine<GS, BF16S>;
   constexpr int R = F::R;
   extern __shared__ __align__(16) u4 vlds[];
@@ -499,17 +505,35 @@ __global__ __launch_bounds__(512) void affine_vgemm(const uint16_t *__restrict__
 
   for (int kc0 = 0; kc0 < K; kc0 += Kc) {
     const int klen = min(Kc, K - kc0), ucs = klen / 64, steps = ucs / 4;
-    // ---- stage x[tk][kc0 .. kc0 + klen) of every token: 8 values per lane per item
-    {
+    // ---- stage x[tk][kc0 .. kc0 + klen) of every token: copied from the prestaged images (Kc a
+    // multiple of 1024, so a chunk's slots and sums are two runs of each image), or computed
+    // (rotated first when block > 0), 8 values per lane per item
+    if (img) {
+      const int IWf = F::img_words(K), ugf = (K / 64 + 15) / 16, g0 = kc0 / 1024;
+      const int ugt = (ucs + 15) / 16;  // groups in this chunk (the last may be short)
+      const int ns = ugt * 16 * R, nq = ugt * 16 * F::Q / 4, per = ns + nq;
+      for (int i = threadIdx.x; i < M * per; i += blockDim.x) {
+        const int tk = i / per, o = i % per;
+        const u4 *src = img + (size_t)tk * IWf + (o < ns ? g0 * 16 * R + o : ugf * 16 * R + g0 * 16 * F::Q / 4 + (o - ns));
+        vlds[tk * IW + (o < ns ? o : ugc * 16 * R + (o - ns))] = *src;
+      }
+      __syncthreads();
+    } else {
       const int per_tok = (klen + 511) / 512, items = M * per_tok;
+      const float scale = block > 1 ? 1.0f / __builtin_sqrtf((float)block) : 1.0f;
       constexpr int PF = 4;
       for (int i0 = wave; i0 < items; i0 += PF * nw) {
         u4 xv[PF];
+        f4 sg[PF][2];
 #pragma unroll
         for (int j = 0; j < PF; j++) {
           const int it = min(i0 + j * nw, items - 1), tk = it / per_tok, ps = it % per_tok;
           const int k = min(ps * 512 + 8 * lane, klen - 8);
           xv[j] = *(const u4 *)(x + (size_t)tk * K + kc0 + k);
+          if (signs) {
+            sg[j][0] = *(const f4 *)(signs + kc0 + k);
+            sg[j][1] = *(const f4 *)(signs + kc0 + k + 4);
+          }
         }
 #pragma unroll
         for (int j = 0; j < PF; j++) {
@@ -523,6 +547,7 @@ __global__ __launch_bounds__(512) void affine_vgemm(const uint16_t *__restrict__
             v[2 * e] = (float)hv.x;
             v[2 * e + 1] = (float)hv.y;
           }
+          if (block > 0) F::rot8(v, signs ? sg[j] : nullptr, block, scale, lane);
           u4 *img = vlds + tk * IW;
           F::put8(img, (float *)(img + ugc * 16 * R), k, v, k < klen);
         }
@@ -650,13 +675,16 @@ static int num_cu_aff() {
 
 static bool pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
-// x staged once for every workgroup of the GEMV: one wave per 512-value pass writes the slots
-// and sums, laid out exactly as the GEMV's LDS (block <= 128).
+// x staged once for every workgroup of the GEMV or verify kernel: one wave per 512-value pass
+// (blockIdx.y = token) writes the slots and sums, laid out exactly as those kernels' LDS
+// (block <= 128; one image of img_words(K) 16-byte words per token).
 __global__ __launch_bounds__(64) void affine_prestage_kernel(FAffine<64, false>::Args a, const uint16_t *__restrict__ x,
                                                              u4 *__restrict__ img) {
   using F = FAffine<64, false>;
   const int ug = (F::units(a.K) + 15) / 16;
   const int c0 = blockIdx.x, nw = gridDim.x;
+  x += (size_t)blockIdx.y * a.K;  // token
+  img += (size_t)blockIdx.y * F::img_words(a.K);
   F::stage_group(a, img, (float *)(img + ug * 16 * F::R), c0, nw, F::load_group(a, x, c0, nw));
 }
 
@@ -674,7 +702,8 @@ static int affine_gemv(const void *x, const float *signs, int block, const uint3
 
 template <int GS, bool BF16S, int NQ>
 static int affine_vgemm_launch(const void *x, int M, int K, const uint32_t *codes, const void *scales,
-                               const void *biases, int N, void *y, hipStream_t st) {
+                               const void *biases, int N, void *y, hipStream_t st, const float *signs,
+                               int block, const u4 *img) {
   using F = FAffine<GS, BF16S>;
   constexpr int D = 4;
   const int ntiles = (N + 15) / 16;
@@ -685,23 +714,26 @@ static int affine_vgemm_launch(const void *x, int M, int K, const uint32_t *code
   const size_t budget = 150 * 1024;
   int Kc = K;
   auto need = [&](int kc) { return fixed + (size_t)M * (F::img_words(kc) + 1) * 16; };
-  while (Kc > 256 && need(Kc) > budget) Kc -= 256;
+  const int kstep = img ? 1024 : 256;  // image chunks must start on a 16-unit group
+  while (Kc > kstep && need(Kc) > budget) Kc = (Kc - 1) / kstep * kstep;
   if (need(Kc) > budget) return decline("verify workspace does not fit in LDS");
   const size_t lds = need(Kc);
   hipLaunchKernelGGL((affine_vgemm<GS, BF16S, NQ, D>), dim3(wgs), dim3(64 * NW), lds, st, (const uint16_t *)x, M, K,
-                     codes, (const uint16_t *)scales, (const uint16_t *)biases, N, (uint16_t *)y, Kc, T);
+                     codes, (const uint16_t *)scales, (const uint16_t *)biases, N, (uint16_t *)y, Kc, T, signs,
+                     block, img);
   ISHZ_LAUNCH_CHECK("affine verify launch");
   return ISHZ_OK;
 }
 
 template <int GS, bool BF16S>
 static int affine_vgemm_nq(const void *x, int M, int K, const uint32_t *codes, const void *scales,
-                           const void *biases, int N, void *y, hipStream_t st) {
+                           const void *biases, int N, void *y, hipStream_t st, const float *signs = nullptr,
+                           int block = 0, const u4 *img = nullptr) {
   switch ((M + 3) / 4) {
-    case 1: return affine_vgemm_launch<GS, BF16S, 1>(x, M, K, codes, scales, biases, N, y, st);
-    case 2: return affine_vgemm_launch<GS, BF16S, 2>(x, M, K, codes, scales, biases, N, y, st);
-    case 3: return affine_vgemm_launch<GS, BF16S, 3>(x, M, K, codes, scales, biases, N, y, st);
-    default: return affine_vgemm_launch<GS, BF16S, 4>(x, M, K, codes, scales, biases, N, y, st);
+    case 1: return affine_vgemm_launch<GS, BF16S, 1>(x, M, K, codes, scales, biases, N, y, st, signs, block, img);
+    case 2: return affine_vgemm_launch<GS, BF16S, 2>(x, M, K, codes, scales, biases, N, y, st, signs, block, img);
+    case 3: return affine_vgemm_launch<GS, BF16S, 3>(x, M, K, codes, scales, biases, N, y, st, signs, block, img);
+    default: return affine_vgemm_launch<GS, BF16S, 4>(x, M, K, codes, scales, biases, N, y, st, signs, block, img);
   }
 }
 
@@ -780,11 +812,11 @@ extern "C" int ishz_affine_matmul(const void *x, int x_dtype, int M, int K, cons
                          group, y, S(stream));
 }
 
-// M > 1: the rotated activations (fp16). M = 1: the staged x image the GEMV's workgroups copy
-// (a null or smaller workspace at M = 1 stages x inside every workgroup instead).
+// Room for the rotated activations (fp16, general path) or every row's staged x image (what the
+// GEMV and verify workgroups copy; a null or smaller workspace stages x in every workgroup).
 extern "C" size_t ishz_affine_workspace_size(int M, int K) {
   if (K <= 0 || M <= 0) return 0;
-  return M > 1 ? (size_t)M * K * 2 : (size_t)FAffine<64, false>::img_words(K) * 16;
+  return std::max((size_t)M * K * 2, (size_t)M * FAffine<64, false>::img_words(K) * 16);
 }
 
 extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, const float *signs,
@@ -808,6 +840,23 @@ extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, cons
   }
   if (block == 0 || M == 1)
     return affine_dispatch(x, M, K, signs, block, codes, scales, biases, bf16s, N, group, y, st);
+  if (block <= 128 && K % 256 == 0 && !getenv("ISHZ_OLD_VERIFY")) {
+    // x rotated and staged once into the workspace (every token's image), else the rotation is
+    // fused into each workgroup's staging
+    const u4 *img = nullptr;
+    if (workspace && workspace_bytes >= ishz_affine_workspace_size(M, K)) {
+      const FAffine<64, false>::Args a{codes, nullptr, nullptr, signs, block, K, N, nullptr};
+      hipLaunchKernelGGL(affine_prestage_kernel, dim3((K + 511) / 512, M), dim3(64), 0, st, a, (const uint16_t *)x,
+                         (u4 *)workspace);
+      ISHZ_LAUNCH_CHECK("affine prestage launch");
+      img = (const u4 *)workspace;
+    }
+    if (group == 64)
+      return bf16s ? affine_vgemm_nq<64, true>(x, M, K, codes, scales, biases, N, y, st, signs, block, img)
+                   : affine_vgemm_nq<64, false>(x, M, K, codes, scales, biases, N, y, st, signs, block, img);
+    return bf16s ? affine_vgemm_nq<128, true>(x, M, K, codes, scales, biases, N, y, st, signs, block, img)
+                 : affine_vgemm_nq<128, false>(x, M, K, codes, scales, biases, N, y, st, signs, block, img);
+  }
   if (!workspace || workspace_bytes < ishz_affine_workspace_size(M, K))
     return einval("workspace too small (ishz_affine_workspace_size)");
   rc = ishz_hadamard(x, ISHZ_DT_F16, M, K, block, signs, 0, workspace, stream);

@@ -87,6 +87,21 @@ def test_affine_rotated_gemv_staging(block, prestage, K):
     assert_close(y.float().cpu().numpy(), ref, what=f"gemv block={block} prestage={prestage} K={K}")
 
 
+@pytest.mark.parametrize("M", [2, 5, 16])
+@pytest.mark.parametrize("block", [2, 32, 128])
+@pytest.mark.parametrize("K,prestage", [(1152, True), (5120, True), (5120, False)])
+def test_affine_rotated_verify(M, block, K, prestage):
+    """2..16 rows: x rotated and staged once by the prestage kernel, or the rotation fused into
+    the verify kernel's staging (K % 256 == 0, block <= 128), else the rotation kernel into the
+    workspace and the general verify kernel (K = 1152). M = 16 at K = 5120 stages x in two K
+    chunks."""
+    N = 530
+    (x, w, s, b), signs, ref = affine_case(N, K, M, 64, seed=M + block + K, block=block, signs_seed=5)
+    y = affine.linear(x, w, s, b, signs=torch.from_numpy(signs), block=block, group_size=64, _prestage=prestage)
+    assert y is not None
+    assert_close(y.float().cpu().numpy(), ref, what=f"verify M={M} block={block} K={K} prestage={prestage}")
+
+
 def test_affine_bf16_scales():
     N, K = 300, 1024
     codes, s, b = synth.affine_pack(N, K, group=64, seed=3)
