@@ -829,7 +829,8 @@ extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, cons
   if (block > 0 && (!pow2(block) || block > 4096 || K % block)) return decline("bad Hadamard block");
   const int bf16s = scale_dtype == ISHZ_DT_BF16;
   hipStream_t st = S(stream);
-  if (M == 1 && block > 0 && block <= 128 && workspace && workspace_bytes >= ishz_affine_workspace_size(1, K)) {
+  if (M == 1 && block > 0 && block <= 128 && workspace && workspace_bytes >= ishz_affine_workspace_size(1, K) &&
+      !getenv("ISHZ_M1_MFMA")) {
     const FAffine<64, false>::Args a{codes, nullptr, nullptr, signs, block, K, N, nullptr};
     const int npass = (K + 511) / 512;
     hipLaunchKernelGGL(affine_prestage_kernel, dim3(npass), dim3(64), 0, st, a, (const uint16_t *)x, (u4 *)workspace);
@@ -838,7 +839,7 @@ extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, cons
     return group == 64 ? affine_gemv<64>(x, signs, block, codes, scales, biases, bf16s, K, N, y, st, img)
                        : affine_gemv<128>(x, signs, block, codes, scales, biases, bf16s, K, N, y, st, img);
   }
-  if (block == 0 || M == 1)
+  if (block == 0 || (M == 1 && !getenv("ISHZ_M1_MFMA")))
     return affine_dispatch(x, M, K, signs, block, codes, scales, biases, bf16s, N, group, y, st);
   if (block <= 128 && K % 256 == 0 && !getenv("ISHZ_OLD_VERIFY")) {
     // x rotated and staged once into the workspace (every token's image), else the rotation is

@@ -12,6 +12,8 @@
 // which are rows 2g + {0,1,8,9} of column j: every weight of a tile is decoded exactly once per
 // wave, already in MFMA B-operand order (k rows by lane group, column j by lane).
 #include <algorithm>
+#include <type_traits>
+#include <cstdlib>
 
 #include "common.h"
 
@@ -120,6 +122,144 @@ __global__ __launch_bounds__(1024) void exl3_mm(const uint16_t *__restrict__ xh,
       float s = 0.0f;
       for (int v = 0; v < KS; v++) s += red[v * 16 + threadIdx.x];
       yh[tn * 16 + threadIdx.x] = s;
+    }
+  }
+}
+
+// ------------------------------------------------------------------- streaming matvec / verify
+// For rates whose four lane states span at most 32 bits: a lane's window is one v_alignbit of
+// two tile words, each state one bit-field extract, and two weights are decoded per packed fp16
+// operation. A workgroup owns TN column tiles and its waves split the K tiles (tk = wave, wave +
+// KS, ...), keeping D steps of tile words and x in flight; partials meet in LDS at the end.
+template <int KA, bool HALF>
+struct Trellis32 {
+  using TR = Trellis<KA, HALF>;
+  static constexpr bool FITS = TR::rel(3) <= 32;
+  struct Win {
+    int ja, jb, amt;
+  };
+  static DEV Win window(int p0) {
+    const int lo = (TR::end(p0) + TR::RING - 16) % TR::RING;
+    const int ja = lo >> 5, sh = lo & 31;
+    return sh ? Win{ja, (ja + 1) % TR::WORDS, 32 - sh} : Win{ja, ja, 0};
+  }
+};
+
+// Codebook images of two states, packed as fp16 (a in the low half): exl3_decode, pairwise.
+template <int CB>
+DEV uint32_t exl3_decode2(uint32_t sa, uint32_t sb) {
+  if constexpr (CB == 2) {
+    auto p = [](uint32_t s) {
+      const uint32_t x = s * 0x83DCD12Du;
+      const uint32_t q = (x & 0x00ff00ffu) + ((x >> 8) & 0x00ff00ffu);
+      return ((q & 0xffffu) + (q >> 16) + 0x6400u) & 0xffffu;
+    };
+    const h2 h = as_h2(p(sa) | p(sb) << 16);
+    const h2 m = as_h2(0x1eee1eeeu), c = as_h2(0xc931c931u);
+    return __builtin_bit_cast(uint32_t, (h2)__builtin_elementwise_fma(h, m, c));
+  } else {
+    auto x = [](uint32_t s) {
+      const uint32_t v = CB == 1 ? s * 0xCBAC1FEDu : s * 89226354u + 64248484u;
+      return (v & 0x8fff8fffu) ^ 0x3b603b60u;
+    };
+    const uint32_t xa = x(sa), xb = x(sb);
+    const uint32_t lo = __builtin_amdgcn_perm(xb, xa, 0x05040100u), hi = __builtin_amdgcn_perm(xb, xa, 0x07060302u);
+    return __builtin_bit_cast(uint32_t, as_h2(lo) + as_h2(hi));
+  }
+}
+
+template <int KA, bool HALF, int CB, bool MF, int TN, int D>
+__global__ __launch_bounds__(1024) void exl3_mm2(const uint16_t *__restrict__ xh, int M, int K,
+                                                const uint32_t *__restrict__ trellis, int N,
+                                                float *__restrict__ yh) {
+  using TR = Trellis<KA, HALF>;
+  using T32 = Trellis32<KA, HALF>;
+  extern __shared__ __align__(16) float red2[];
+  const int lane = threadIdx.x & 63, wave = wave_id(), KS = blockDim.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int tn0 = blockIdx.x * TN, tiles_n = N / 16, tiles_k = K / 16;
+  const typename T32::Win wn = T32::window(8 * (4 * (j & 7) + g) + 4 * (j >> 3));
+  const int tok = MF ? (j < M ? j : 0) : 0;
+  const uint16_t *xr = xh + (size_t)tok * K + 2 * g;
+  const size_t tstride = (size_t)tiles_n * TR::WORDS;
+  const uint32_t *base = trellis + (size_t)tn0 * TR::WORDS;
+
+  struct Raw {
+    uint32_t w[TN][2];
+    uint32_t xa, xb;
+  };
+  const int nsteps = tiles_k > wave ? (tiles_k - wave + KS - 1) / KS : 0;
+  auto load = [&](int i, Raw &r) {
+    const int tk = wave + KS * min(i, nsteps - 1);
+    const uint32_t *tp = base + tk * tstride;
+#pragma unroll
+    for (int t = 0; t < TN; t++) {
+      r.w[t][0] = tp[t * TR::WORDS + wn.ja];
+      r.w[t][1] = tp[t * TR::WORDS + wn.jb];
+    }
+    r.xa = *(const uint32_t *)(xr + 16 * tk);
+    r.xb = *(const uint32_t *)(xr + 16 * tk + 8);
+  };
+  using Acc = typename std::conditional<MF, f4, float>::type;
+  Acc acc[TN];
+#pragma unroll
+  for (int t = 0; t < TN; t++) acc[t] = Acc{};
+  Raw ring[D];
+  if (nsteps > 0) {
+#pragma unroll
+    for (int d = 0; d < D - 1; d++) load(d, ring[d]);
+  }
+  const bool live = MF ? j < M : true;
+  for (int i0 = 0; i0 < nsteps; i0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+      const int i = i0 + d;
+      if (i >= nsteps) break;
+      load(i + D - 1, ring[(d + D - 1) % D]);
+      const Raw &r = ring[d];
+#pragma unroll
+      for (int t = 0; t < TN; t++) {
+        const uint32_t win = __builtin_amdgcn_alignbit(r.w[t][0], r.w[t][1], wn.amt);
+        const uint32_t s0 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(0), 16);
+        const uint32_t s1 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(1), 16);
+        const uint32_t s2 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(2), 16);
+        const uint32_t s3 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(3), 16);
+        const uint32_t b01 = exl3_decode2<CB>(s0, s1), b23 = exl3_decode2<CB>(s2, s3);
+        if constexpr (MF) {
+          const u2 A = live ? u2{r.xa, r.xb} : u2{0, 0};
+          acc[t] = mfma16(as_h4(A), as_h4(u2{b01, b23}), acc[t]);
+        } else {
+          acc[t] = dot2(b23, r.xb, dot2(b01, r.xa, acc[t]));
+        }
+      }
+    }
+  }
+  if constexpr (MF) {
+#pragma unroll
+    for (int t = 0; t < TN; t++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) red2[((wave * TN + t) * 4 + q) * 64 + lane] = acc[t][q];
+    __syncthreads();
+    for (int o = threadIdx.x; o < TN * 256; o += blockDim.x) {
+      const int t = o >> 8, q = (o >> 6) & 3, l = o & 63;
+      float sum = 0.0f;
+      for (int v = 0; v < KS; v++) sum += red2[((v * TN + t) * 4 + q) * 64 + l];
+      const int tk = 4 * (l >> 4) + q;
+      if (tk < M) yh[(size_t)tk * N + (tn0 + t) * 16 + (l & 15)] = sum;
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < TN; t++) {
+      float a = acc[t];
+      a += __shfl_xor(a, 16, 64);
+      a += __shfl_xor(a, 32, 64);
+      if (g == 0) red2[(wave * TN + t) * 16 + j] = a;
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < TN * 16; o += blockDim.x) {
+      float sum = 0.0f;
+      for (int v = 0; v < KS; v++) sum += red2[(v * TN + (o >> 4)) * 16 + (o & 15)];
+      yh[(tn0 + (o >> 4)) * 16 + (o & 15)] = sum;
     }
   }
 }
@@ -284,6 +424,35 @@ extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const
   int ks = 1;
   while (ks < 16 && ks < tiles_k && wgs * ks < num_cu_e() * 16) ks *= 2;
   return by_rate(bits2, [&]<int KA, bool HALF>() -> int {
+    if constexpr (Trellis32<KA, HALF>::FITS) {
+      if (!getenv("ISHZ_EXL3_OLD")) {
+        // TN = 4 column tiles per workgroup (N % 128 == 0 makes N / 16 a multiple of 8); 8 waves
+        // split the K tiles.
+        constexpr int TN = 4;
+        static const int cfg = [] {
+          const char *e = getenv("ISHZ_EXL3_CFG");  // tuning: waves per workgroup x 100 + ring depth
+          return e ? atoi(e) : 404;
+        }();
+        const int KS2 = cfg / 100;
+        const size_t lds = M == 1 ? (size_t)KS2 * TN * 16 * 4 : (size_t)KS2 * TN * 256 * 4;
+        auto go = [&]<int CB>() -> int {
+          auto launch = [&]<int D>() {
+            if (M == 1)
+              hipLaunchKernelGGL((exl3_mm2<KA, HALF, CB, false, TN, D>), dim3(N / 16 / TN), dim3(64 * KS2), lds,
+                                 S(stream), (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, yh);
+            else
+              hipLaunchKernelGGL((exl3_mm2<KA, HALF, CB, true, TN, D>), dim3(N / 16 / TN), dim3(64 * KS2), lds,
+                                 S(stream), (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, yh);
+          };
+          if (cfg % 100 == 4) launch.template operator()<4>();
+          else launch.template operator()<8>();
+          ISHZ_LAUNCH_CHECK("exl3 matvec launch");
+          return ISHZ_OK;
+        };
+        return codebook == 0 ? go.template operator()<0>()
+                             : codebook == 1 ? go.template operator()<1>() : go.template operator()<2>();
+      }
+    }
     if (M == 1)
       hipLaunchKernelGGL((exl3_mm<KA, HALF, false>), dim3(wgs), dim3(64 * ks), (size_t)ks * 16 * 4,
                          S(stream), (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, codebook, yh);
