@@ -1,6 +1,7 @@
 // GGML quantized matmul on gfx950: streaming GEMV (M = 1), MFMA verify (M = 2..16), dequant and
 // gather writers. Replaces GGMLKernels (Sources/IshizukiKit/Core/GGMLKernels.swift).
 #include "ggml_formats.h"
+#include "vgemm.h"
 
 #include <cstdlib>
 
@@ -38,6 +39,7 @@ DEV void build_iq2xs_tables(u4 *grid, u4 *sgn) {
 }
 
 DEV void build_iq2xs_tables_perm(u4 *grid, u4 *sgn) { build_iq2xs_tables<true>(grid, sgn); }
+DEV void build_iq2xs_tables_nat(u4 *grid, u4 *sgn) { build_iq2xs_tables<false>(grid, sgn); }
 
 // ----------------------------------------------------------------------------- verify (MFMA)
 // A workgroup owns T tiles of 16 weight rows; its KS waves split the row's blocks round-robin
@@ -265,6 +267,8 @@ static int launch_verify(const void *x, int M, int K, const void *w, int N, void
 
 template <class F>
 static int verify(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st) {
+  static const bool old = getenv("ISHZ_OLD_VERIFY") != nullptr;
+  if (M >= 2 && K % 256 == 0 && !old) return vgemm<F>(x, M, K, w, N, y, st);
   if (N >= 4096) return launch_verify<F, 2>(x, M, K, w, N, y, st);
   return launch_verify<F, 1>(x, M, K, w, N, y, st);
 }

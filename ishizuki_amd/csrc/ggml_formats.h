@@ -146,6 +146,15 @@ struct GgmlGemv {
   }
 };
 
+// Verify staging: perm0213 of 8 consecutive x (the pair order of nibble codes), natural order.
+DEV u4 vx8p(const uint16_t *x, float &X) {
+  const u4 v = *(const u4 *)x;
+#pragma unroll
+  for (int e = 0; e < 4; e++) X = dot2(v[e], 0x3C003C00u, X);
+  return perm0213(v);
+}
+DEV u4 vx8n(const uint16_t *x) { return *(const u4 *)x; }
+
 // ------------------------------------------------------------------------------------- Q4_0
 // ggml block_q4_0: fp16 d at 0, qs[16] at 2; element j = (lo(qs[j]) - 8) d, j + 16 = hi.
 struct FQ4_0 : GgmlGemv<FQ4_0> {
@@ -193,6 +202,41 @@ struct FQ4_0 : GgmlGemv<FQ4_0> {
                             __builtin_amdgcn_alignbyte(r.a.w, r.a.z, 2), __builtin_amdgcn_alignbyte(r.b.x, r.a.w, 2)};
     const uint32_t qb[4] = {r.b.y, r.b.z, r.b.w, r.c};
     return h2f(r.a.x & 0xffff) * half_dot(qa, s, 0, 0) + h2f(r.b.x >> 16) * half_dot(qb, s, 4, 2);
+  }
+
+  // Streaming verify: a lane's quarter of a 256-weight step is its GEMV unit (blocks 8j + 2g,
+  // 8j + 2g + 1); sub-units (block, low / high nibbles), two MFMAs each. High nibbles decode to
+  // 1024 + 16q, so their scale carries the 1/16.
+  static constexpr int VNS = 4, VSTEP_BYTES = 8 * TS;
+  static constexpr bool VGRID = false;
+  typedef Raw VRaw;
+  static DEV VRaw vload(const uint8_t *row, int j, int g) { return load_row(row + (size_t)j * VSTEP_BYTES, g); }
+  static DEV void vdecode(const VRaw &r, u4 *B, uint32_t mg, const u4 *, const u4 *) {
+    const uint32_t q[8] = {__builtin_amdgcn_alignbyte(r.a.y, r.a.x, 2), __builtin_amdgcn_alignbyte(r.a.z, r.a.y, 2),
+                           __builtin_amdgcn_alignbyte(r.a.w, r.a.z, 2), __builtin_amdgcn_alignbyte(r.b.x, r.a.w, 2),
+                           r.b.y, r.b.z, r.b.w, r.c};
+#pragma unroll
+    for (int blk = 0; blk < 2; blk++)
+#pragma unroll
+      for (int hi = 0; hi < 2; hi++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+          const uint32_t m = hi ? 0x00F000F0u : 0x000F000Fu;
+          const uint32_t q0 = q[4 * blk + 2 * b], q1 = q[4 * blk + 2 * b + 1];
+          B[(2 * blk + hi) * 2 + b] = u4{and_or(q0, m, mg), and_or(q0 >> 8, m, mg), and_or(q1, m, mg), and_or(q1 >> 8, m, mg)};
+        }
+  }
+  static DEV void vstage(const uint16_t *x, int j, int g, int s, u4 *A, float &off1, float &X) {
+    const uint16_t *p = x + 256 * j + 64 * g + 32 * (s >> 1) + 16 * (s & 1);
+    X = 0.0f;
+    A[0] = vx8p(p, X);
+    A[1] = vx8p(p + 8, X);
+    off1 = 1024.0f * X;
+  }
+  static DEV void vscale(const VRaw &r, int, int s, float &sc, float &mn) {
+    const float d = h2f(s >> 1 ? r.b.x >> 16 : r.a.x & 0xffff);
+    sc = (s & 1) ? 0.0625f * d : d;
+    mn = -8.0f * d;
   }
 
   // Verify: one MFMA 16x16x32 per block. Lane group g takes k = 8g..8g+7: lo nibbles of bytes
@@ -292,6 +336,43 @@ struct FQ4_K : GgmlGemv<FQ4_K> {
     const float xs_l = s.sum(0), xs_h = s.sum(1);
     return dl0 * ((a0 + a1) - 1024.0f * xs_l) - (dmin * (float)m0) * xs_l +
            dl1 * (0.0625f * (b0 + b1) - 64.0f * xs_h) - (dmin * (float)m1) * xs_h;
+  }
+
+  // Streaming verify: step = one super-block; a lane's quarter is chunk g (32 bytes of qs):
+  // sub-unit 0 = sub-block 2g (low nibbles), 1 = sub-block 2g + 1 (high, 1024 + 16q).
+  static constexpr int VNS = 2, VSTEP_BYTES = TS;
+  static constexpr bool VGRID = false;
+  struct VRaw {
+    u4 h, q0, q1;
+  };
+  static DEV VRaw vload(const uint8_t *row, int j, int g) {
+    const uint8_t *p = row + (size_t)j * TS;
+    return {ld16<16>(p), ld16<16>(p + 16 + 32 * g), ld16<16>(p + 32 + 32 * g)};
+  }
+  static DEV void vdecode(const VRaw &r, u4 *B, uint32_t mg, const u4 *, const u4 *) {
+    const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+#pragma unroll
+    for (int hi = 0; hi < 2; hi++)
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        const uint32_t m = hi ? 0x00F000F0u : 0x000F000Fu;
+        const uint32_t q0 = q[2 * b], q1 = q[2 * b + 1];
+        B[hi * 4 + b] = u4{and_or(q0, m, mg), and_or(q0 >> 8, m, mg), and_or(q1, m, mg), and_or(q1 >> 8, m, mg)};
+      }
+  }
+  static DEV void vstage(const uint16_t *x, int j, int g, int s, u4 *A, float &off1, float &X) {
+    const uint16_t *p = x + 256 * j + 64 * g + 32 * s;
+    X = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 4; b++) A[b] = vx8p(p + 8 * b, X);
+    off1 = 1024.0f * X;
+  }
+  static DEV void vscale(const VRaw &r, int g, int s, float &sc, float &mn) {
+    int scv, m;
+    q4k_scale_min(r.h.y, r.h.z, r.h.w, 2 * g + s, scv, m);
+    const float d = h2f(r.h.x & 0xffff), dmin = h2f(r.h.x >> 16);
+    sc = d * (float)scv * (s ? 0.0625f : 1.0f);
+    mn = -(dmin * (float)m);
   }
 
   // Verify: one MFMA 16x16x32 per sub-block; lane group g takes l = 8g..8g+7 of it, i.e. the
@@ -410,6 +491,53 @@ struct FQ6_K : GgmlGemv<FQ6_K> {
            (d * s1) * ((S[1][0] + S[1][1]) - 1056.0f * s.sum(1)) +
            (d * s2) * (0.0625f * (S[2][0] + S[2][1]) - 96.0f * s.sum(2)) +
            (d * s3) * (0.0625f * (S[3][0] + S[3][1]) - 96.0f * s.sum(3));
+  }
+
+  // Streaming verify: step = one super-block; lane group g takes half n = g / 2, l in
+  // 16 (g % 2) .. + 15: sub-unit qq (scale sc[8n + g % 2 + 2qq]) = weights 128n + 32qq + l, two
+  // MFMAs (l halves). Codes decode to 1024 + q (q = 0..63) from a nibble of ql and two bits of qh.
+  static constexpr int VNS = 4, VSTEP_BYTES = TS;
+  static constexpr bool VGRID = false;
+  struct VRaw {
+    u4 ql0, ql1, qh, sc;
+    uint32_t d;
+  };
+  static DEV VRaw vload(const uint8_t *row, int j, int g) {
+    const uint8_t *p = row + (size_t)j * TS;
+    const int n = g >> 1, lh = g & 1;
+    return {ld16<2>(p + 64 * n + 16 * lh), ld16<2>(p + 64 * n + 32 + 16 * lh), ld16<2>(p + 128 + 32 * n + 16 * lh),
+            ld16<2>(p + 192), ld2(p + 208)};
+  }
+  static DEV void vdecode(const VRaw &r, u4 *B, uint32_t mg, const u4 *, const u4 *) {
+#pragma unroll
+    for (int qq = 0; qq < 4; qq++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        uint32_t o[4];
+#pragma unroll
+        for (int t2 = 0; t2 < 2; t2++) {
+          const int t = 2 * h + t2;
+          const uint32_t a = ((qq & 1) ? r.ql1[t] : r.ql0[t]) >> (qq >= 2 ? 4 : 0);
+          const uint32_t hq = r.qh[t];
+          const uint32_t hs = qq == 0 ? hq << 4 : qq == 1 ? hq << 2 : qq == 2 ? hq : hq >> 2;
+          o[2 * t2] = and_or(a, 0x000F000Fu, and_or(hs, 0x00300030u, mg));
+          o[2 * t2 + 1] = and_or(a >> 8, 0x000F000Fu, and_or(hs >> 8, 0x00300030u, mg));
+        }
+        B[qq * 2 + h] = u4{o[0], o[1], o[2], o[3]};
+      }
+  }
+  static DEV void vstage(const uint16_t *x, int j, int g, int s, u4 *A, float &off1, float &X) {
+    const uint16_t *p = x + 256 * j + 128 * (g >> 1) + 16 * (g & 1) + 32 * s;
+    X = 0.0f;
+    A[0] = vx8p(p, X);
+    A[1] = vx8p(p + 8, X);
+    off1 = 1024.0f * X;
+  }
+  static DEV void vscale(const VRaw &r, int g, int s, float &sc, float &mn) {
+    const int bi = 8 * (g >> 1) + (g & 1) + 2 * s;  // scale byte
+    const float d = h2f(r.d) * (float)(int8_t)(r.sc[bi >> 2] >> (8 * (bi & 3)));
+    sc = d;
+    mn = -32.0f * d;
   }
 
   // Verify: MFMA 16x16x16, one per 16-weight scale group (n, qq, lh); lane group g takes
@@ -537,6 +665,39 @@ struct FIQ2_XS : GgmlGemv<FIQ2_XS> {
         }
       }
     }
+  }
+
+  // Streaming verify: step = one super-block; lane group g takes groups 2g, 2g + 1 (entries
+  // e = 0..7, 8 weights each, one MFMA each); sub-unit e / 2 shares one 4-bit scale. B is the
+  // grid entry with its signs (exact small integers in fp16); A is x in natural order.
+  static constexpr int VNS = 4, VSTEP_BYTES = TS;
+  static constexpr bool VGRID = true;
+  struct VRaw {
+    u4 q;
+    uint32_t sc, d;
+  };
+  static DEV VRaw vload(const uint8_t *row, int j, int g) {
+    const uint8_t *p = row + (size_t)j * TS;
+    return {ld16<2>(p + 2 + 16 * g), ld2(p + 66 + 2 * g), ld2(p)};
+  }
+  static DEV void vdecode(const VRaw &r, u4 *B, uint32_t, const u4 *grid, const u4 *sgn) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const uint32_t q = (r.q[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+      B[e] = grid[q & 511] ^ sgn[q >> 9];
+    }
+  }
+  static DEV void vstage(const uint16_t *x, int j, int g, int s, u4 *A, float &off1, float &X) {
+    const uint16_t *p = x + 256 * j + 64 * g + 16 * s;
+    A[0] = vx8n(p);
+    A[1] = vx8n(p + 8);
+    off1 = 0.0f;
+    X = 0.0f;
+  }
+  static DEV void vscale(const VRaw &r, int, int s, float &sc, float &mn) {
+    const uint32_t nib = (r.sc >> (8 * (s >> 1) + 4 * (s & 1))) & 15;
+    sc = h2f(r.d) * (0.5f + (float)nib) * 0.25f;
+    mn = 0.0f;
   }
 };
 

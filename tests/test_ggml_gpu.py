@@ -95,6 +95,23 @@ def test_verify_rows(t, M):
     assert_close(y, ref, what=f"verify t={t} M={M}")
 
 
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("M", [8, 16])
+def test_verify_long_k_chunks(t, M):
+    """K = 25600 (the down projection): x is staged in several K chunks per workgroup."""
+    N, K = 300, 25600
+    print(f"verify long K type={t} M={M}", flush=True)
+    y, ref = run_matvec(t, M, N, K, seed=M + t)
+    assert_close(y, ref, what=f"verify long K t={t} M={M}")
+
+
+@pytest.mark.parametrize("M", [2, 7])
+def test_verify_q4_0_k_not_multiple_of_256(M):
+    """K % 256 != 0 takes the per-block verify kernel."""
+    y, ref = run_matvec(ggml.Q4_0, M, 130, 32 * 13, seed=M)
+    assert_close(y, ref, what=f"q4_0 K=416 M={M}")
+
+
 @pytest.mark.parametrize("t", [ggml.Q4_K, ggml.Q6_K, ggml.IQ2_XS])
 def test_matmul_few_ragged(t):
     # GGMLKernelTests.matmulFew (:145-175): N = 17, a ragged tile
