@@ -207,7 +207,7 @@ struct FQ4_0 : GgmlGemv<FQ4_0> {
   // Streaming verify: a lane's quarter of a 256-weight step is its GEMV unit (blocks 8j + 2g,
   // 8j + 2g + 1); sub-units (block, low / high nibbles), two MFMAs each. High nibbles decode to
   // 1024 + 16q, so their scale carries the 1/16.
-  static constexpr int VNS = 4, VSTEP_BYTES = 8 * TS;
+  static constexpr int VNS = 4, VSTEP_BYTES = 8 * TS, VDEPTH = 4;
   static constexpr bool VGRID = false;
   typedef Raw VRaw;
   static DEV VRaw vload(const uint8_t *row, int j, int g) { return load_row(row + (size_t)j * VSTEP_BYTES, g); }
@@ -340,7 +340,7 @@ struct FQ4_K : GgmlGemv<FQ4_K> {
 
   // Streaming verify: step = one super-block; a lane's quarter is chunk g (32 bytes of qs):
   // sub-unit 0 = sub-block 2g (low nibbles), 1 = sub-block 2g + 1 (high, 1024 + 16q).
-  static constexpr int VNS = 2, VSTEP_BYTES = TS;
+  static constexpr int VNS = 2, VSTEP_BYTES = TS, VDEPTH = 4;
   static constexpr bool VGRID = false;
   struct VRaw {
     u4 h, q0, q1;
@@ -496,7 +496,7 @@ struct FQ6_K : GgmlGemv<FQ6_K> {
   // Streaming verify: step = one super-block; lane group g takes half n = g / 2, l in
   // 16 (g % 2) .. + 15: sub-unit qq (scale sc[8n + g % 2 + 2qq]) = weights 128n + 32qq + l, two
   // MFMAs (l halves). Codes decode to 1024 + q (q = 0..63) from a nibble of ql and two bits of qh.
-  static constexpr int VNS = 4, VSTEP_BYTES = TS;
+  static constexpr int VNS = 4, VSTEP_BYTES = TS, VDEPTH = 2;
   static constexpr bool VGRID = false;
   struct VRaw {
     u4 ql0, ql1, qh, sc;
@@ -670,7 +670,7 @@ struct FIQ2_XS : GgmlGemv<FIQ2_XS> {
   // Streaming verify: step = one super-block; lane group g takes groups 2g, 2g + 1 (entries
   // e = 0..7, 8 weights each, one MFMA each); sub-unit e / 2 shares one 4-bit scale. B is the
   // grid entry with its signs (exact small integers in fp16); A is x in natural order.
-  static constexpr int VNS = 4, VSTEP_BYTES = TS;
+  static constexpr int VNS = 4, VSTEP_BYTES = TS, VDEPTH = 4;
   static constexpr bool VGRID = true;
   struct VRaw {
     u4 q;

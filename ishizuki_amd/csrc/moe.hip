@@ -12,8 +12,10 @@
 // down (active experts x tiles of H); combine (weighted sum per token). Only routed experts'
 // blocks are ever read.
 #include <algorithm>
+#include <cstdlib>
 
 #include "ggml_formats.h"
+#include "vgemm.h"
 
 namespace ishz {
 
@@ -44,22 +46,48 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict
   const int lane = threadIdx.x & 63, wave = wave_id(), waves = blockDim.x >> 6;
   for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
   __syncthreads();
+  int32_t *ids_l = cnt + E;  // T*k ids kept in LDS for the placement below (when R.offs)
+  constexpr int EPL = 8;     // logits a lane keeps in registers (E <= 512)
   for (int t = wave; t < T; t += waves) {
     const float *l = logits + (size_t)t * E;
+    const bool cached = E <= 64 * EPL;
+    float lv[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; i++) lv[i] = cached && lane + 64 * i < E ? l[lane + 64 * i] : -INFINITY;
     float mx = -INFINITY;
-    for (int e = lane; e < E; e += 64) mx = fmaxf(mx, l[e]);
+    if (cached) {
+#pragma unroll
+      for (int i = 0; i < EPL; i++) mx = fmaxf(mx, lv[i]);
+    } else {
+      for (int e = lane; e < E; e += 64) mx = fmaxf(mx, l[e]);
+    }
     for (int m = 32; m; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
     float sum = 0.0f;
-    for (int e = lane; e < E; e += 64) sum += expf(l[e] - mx);
+    if (cached) {
+#pragma unroll
+      for (int i = 0; i < EPL; i++)
+        if (lane + 64 * i < E) sum += expf(lv[i] - mx);
+    } else {
+      for (int e = lane; e < E; e += 64) sum += expf(l[e] - mx);
+    }
     for (int m = 32; m; m >>= 1) sum += __shfl_xor(sum, m, 64);
     float prev_v = INFINITY, tot = 0.0f, wsel = 0.0f;
     int prev_e = -1;
     for (int s = 0; s < k; s++) {
       float bv = -INFINITY;
       int be = -1;
-      for (int e = lane; e < E; e += 64) {
-        const float v = l[e];
-        if (v < prev_v || (v == prev_v && e > prev_e)) argmax_merge(bv, be, v, e);
+      if (cached) {
+#pragma unroll
+        for (int i = 0; i < EPL; i++) {
+          const int e = lane + 64 * i;
+          const float v = lv[i];
+          if (e < E && (v < prev_v || (v == prev_v && e > prev_e))) argmax_merge(bv, be, v, e);
+        }
+      } else {
+        for (int e = lane; e < E; e += 64) {
+          const float v = l[e];
+          if (v < prev_v || (v == prev_v && e > prev_e)) argmax_merge(bv, be, v, e);
+        }
       }
       for (int m = 32; m; m >>= 1) {
         const float ov = __shfl_xor(bv, m, 64);
@@ -73,7 +101,10 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict
       prev_e = be;
       if (lane == 0) {
         R.ids[t * k + s] = be;
-        if (R.offs) atomicAdd(&cnt[be], 1);
+        if (R.offs) {
+          ids_l[t * k + s] = be;
+          atomicAdd(&cnt[be], 1);
+        }
       }
     }
     if (lane < k) R.w[t * k + lane] = normalize ? wsel / tot : wsel;
@@ -81,7 +112,6 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict
   if (!R.offs) return;  // routing only
   __syncthreads();
   // exclusive prefix of the counts by wave 0 (64 experts per round), active list by rank
-  int32_t *ids_l = cnt + E;  // T*k ids copied to LDS for the placement below
   if (wave == 0) {
     int carry = 0, nact = 0;
     for (int e0 = 0; e0 < E; e0 += 64) {
@@ -108,7 +138,6 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict
     }
   }
   const int P = T * k;
-  for (int q = threadIdx.x; q < P; q += blockDim.x) ids_l[q] = R.ids[q];
   __syncthreads();
   for (int q = threadIdx.x; q < P; q += blockDim.x) {
     const int e = ids_l[q];
@@ -217,6 +246,90 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__rest
   }
 }
 
+// ------------------------------------------------------------------- streaming (MFMA) FFN
+// The same two projections as problems of the streaming verify kernel: one group per active
+// expert (blockIdx.y), its routed tokens gathered through the pair list.
+//
+// gate + up: the expert's gate and up rows interleave by tile (tile 2i = gate rows 16i .., tile
+// 2i + 1 = the same up rows), so a workgroup holds both halves of each SwiGLU pair.
+struct VMoeGateUp {
+  const uint16_t *x;
+  const uint8_t *gate, *up;
+  size_t rb;
+  int H, I;
+  MoeRoute R;
+  uint16_t *h;
+  struct Group {
+    int e, p0, p1;
+  };
+  DEV bool group(int a, Group &g) const {
+    if (a >= R.count[0]) return false;
+    g.e = R.active[a];
+    g.p0 = R.offs[g.e];
+    g.p1 = R.offs[g.e + 1];
+    return true;
+  }
+  DEV int count(const Group &g) const { return g.p1 - g.p0; }
+  DEV int rows(const Group &) const { return 2 * ((I + 15) / 16) * 16; }
+  DEV const uint16_t *xrow(const Group &g, int tk) const { return x + (size_t)R.pair_tok[g.p0 + tk] * H; }
+  DEV const uint8_t *wrow(const Group &g, int row) const {
+    const int tile = row >> 4, i = min((tile >> 1) * 16 + (row & 15), I - 1);
+    return ((tile & 1) ? up : gate) + ((size_t)g.e * I + i) * rb;
+  }
+  DEV void finish(const Group &g, int c0, int m, int tb, int te, const float *out) const {
+    for (int o = threadIdx.x; o < (te - tb) / 2 * 256; o += blockDim.x) {
+      const int pr = o >> 8, tk = (o >> 4) & 15, nn = o & 15;
+      const int i = ((tb >> 1) + pr) * 16 + nn;
+      if (tk < m && i < I) {
+        const float g16 = r16(out[(2 * pr) * 256 + tk * 16 + nn]), u16 = r16(out[(2 * pr + 1) * 256 + tk * 16 + nn]);
+        const float sg = r16(1.0f / (1.0f + __expf(-g16)));
+        h[(size_t)(g.p0 + c0 + tk) * I + i] = f2h(r16(g16 * sg) * u16);
+      }
+    }
+  }
+};
+
+// down: o[pair][H] = h[pair] . down_e^T (fp16).
+struct VMoeDown {
+  const uint16_t *h;
+  const uint8_t *down;
+  size_t rb;
+  int I, H;
+  MoeRoute R;
+  uint16_t *o;
+  struct Group {
+    int e, p0, p1;
+  };
+  DEV bool group(int a, Group &g) const {
+    if (a >= R.count[0]) return false;
+    g.e = R.active[a];
+    g.p0 = R.offs[g.e];
+    g.p1 = R.offs[g.e + 1];
+    return true;
+  }
+  DEV int count(const Group &g) const { return g.p1 - g.p0; }
+  DEV int rows(const Group &) const { return H; }
+  DEV const uint16_t *xrow(const Group &g, int tk) const { return h + (size_t)(g.p0 + tk) * I; }
+  DEV const uint8_t *wrow(const Group &g, int row) const { return down + ((size_t)g.e * H + row) * rb; }
+  DEV void finish(const Group &g, int c0, int m, int tb, int te, const float *out) const {
+    for (int q = threadIdx.x; q < (te - tb) * 256; q += blockDim.x) {
+      const int tk = (q >> 4) & 15, row = (tb + (q >> 8)) * 16 + (q & 15);
+      if (tk < m && row < H) o[(size_t)(g.p0 + c0 + tk) * H + row] = f2h(out[q]);
+    }
+  }
+};
+
+// Token quads per pass: an expert receives at most T tokens (one slot per token).
+template <class F, class P>
+static int moe_vgemm(const P &p, int T, int K, int rows, int groups, int tiles_per_wg, hipStream_t st) {
+  switch (std::min(4, (T + 3) / 4)) {
+    case 1: return launch_vgemm_p<F, P, 1>(p, K, rows, groups, tiles_per_wg, st);
+    case 2: return launch_vgemm_p<F, P, 2>(p, K, rows, groups, tiles_per_wg, st);
+    case 3: return launch_vgemm_p<F, P, 3>(p, K, rows, groups, tiles_per_wg, st);
+    default: return launch_vgemm_p<F, P, 4>(p, K, rows, groups, tiles_per_wg, st);
+  }
+}
+
 // ------------------------------------------------------------------- host
 struct MoeLayout {
   size_t ids, w, count, active, offs, pair_tok, inv, h, o, total;
@@ -257,14 +370,34 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
                    const void *up, const void *down, MoeRoute R, uint16_t *h, uint16_t *o, void *y,
                    hipStream_t st) {
   const int amax = std::min(E, T * k);
-  int ks = ks_for((I / 16) * amax, H / F::BS);
-  hipLaunchKernelGGL((moe_gate_up_kernel<F>), dim3(I / 16, amax), dim3(64 * ks), (size_t)ks * 2 * 256 * 4, st,
-                     (const uint16_t *)x, H, (const uint8_t *)gate, (const uint8_t *)up, I, R, h);
-  ISHZ_LAUNCH_CHECK("moe gate/up launch");
-  ks = ks_for((H / 32) * amax, I / F::BS);
-  hipLaunchKernelGGL((moe_down_kernel<F>), dim3((H + 31) / 32, amax), dim3(64 * ks), (size_t)ks * 2 * 256 * 4,
-                     st, h, I, (const uint8_t *)down, H, R, o);
-  ISHZ_LAUNCH_CHECK("moe down launch");
+  static const bool old = getenv("ISHZ_OLD_MOE") != nullptr;
+  if (H % 256 == 0 && I % 256 == 0 && !old) {
+    // tiles per workgroup: about two workgroups per CU over the routed experts (gate/up: an even
+    // count, whole SwiGLU pairs); with 8 or more a wave takes whole tiles
+    const int tiles_gu = 2 * ((I + 15) / 16), tiles_dn = (H + 15) / 16;
+    const int act = std::min(amax, 128);
+    auto pick = [&](int tiles, int even) {
+      int t = std::max(1, std::min(32, tiles * act / (gemv_num_cu() * 2)));
+      if (even) t = std::max(2, t & ~1);
+      return t;
+    };
+    const VMoeGateUp gu{(const uint16_t *)x, (const uint8_t *)gate, (const uint8_t *)up,
+                        (size_t)(H / F::BS) * F::TS, H, I, R, h};
+    int rc = moe_vgemm<F>(gu, T, H, tiles_gu * 16, amax, pick(tiles_gu, 1), st);
+    if (rc) return rc;
+    const VMoeDown dn{h, (const uint8_t *)down, (size_t)(I / F::BS) * F::TS, I, H, R, o};
+    rc = moe_vgemm<F>(dn, T, I, H, amax, pick(tiles_dn, 0), st);
+    if (rc) return rc;
+  } else {
+    int ks = ks_for((I / 16) * amax, H / F::BS);
+    hipLaunchKernelGGL((moe_gate_up_kernel<F>), dim3(I / 16, amax), dim3(64 * ks), (size_t)ks * 2 * 256 * 4, st,
+                       (const uint16_t *)x, H, (const uint8_t *)gate, (const uint8_t *)up, I, R, h);
+    ISHZ_LAUNCH_CHECK("moe gate/up launch");
+    ks = ks_for((H / 32) * amax, I / F::BS);
+    hipLaunchKernelGGL((moe_down_kernel<F>), dim3((H + 31) / 32, amax), dim3(64 * ks), (size_t)ks * 2 * 256 * 4,
+                       st, h, I, (const uint8_t *)down, H, R, o);
+    ISHZ_LAUNCH_CHECK("moe down launch");
+  }
   const size_t total = (size_t)T * H;
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)std::min<size_t>((total + 255) / 256, 4096)), dim3(256), 0,
                      st, o, H, T, k, R, (uint16_t *)y);

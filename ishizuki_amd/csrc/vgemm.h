@@ -11,8 +11,8 @@
 // NQ token quads reuse the same decoded B. The lane-group partials of a row are summed by
 // shuffles once per tile.
 //
-// A workgroup (NW waves) owns a run of tiles; its waves split each tile's steps (step j goes to
-// wave j % NW) and sum their partials in LDS. x is staged in LDS per K chunk, in A-operand order:
+// A workgroup (NW waves) owns a run of tiles; its waves share the tiles' steps and sum their
+// partials in LDS. x is staged in LDS per K chunk, in A-operand order:
 // token image [step][g][mfma] of 16-byte words, plus per (step, g, sub-unit) the sums the
 // epilogue needs for every token (1024 * sum of the staged A values, the magic-number offset;
 // and the plain sum of x).
@@ -24,6 +24,7 @@
 //   void vstage(xrow, j, g, s, A, off1, X)   A words of sub-unit s (8 / VNS of them) and sums
 //   void vscale(r, g, s, sc, mn)     value of sub-unit s = sc * (C - off1) + mn * X
 //   VGRID                            LDS tables (IQ2_XS grid and signs, natural order)
+//   VDEPTH                           steps kept in flight (register ring)
 #pragma once
 #include <algorithm>
 #include <cstdlib>
@@ -34,170 +35,230 @@ namespace ishz {
 
 DEV void build_iq2xs_tables_nat(u4 *grid, u4 *sgn);
 
-template <class F, int NQ, int D, int NW>
-__global__ __launch_bounds__(64 * NW) void vgemm_kernel(const uint16_t *__restrict__ x, int M, int K,
-                                                       const uint8_t *__restrict__ w, size_t rb, int N,
-                                                       uint16_t *__restrict__ y, int Kc, int tiles_per_wg) {
+// What is multiplied: a "problem" P supplies, per workgroup row blockIdx.y (a group: the whole
+// matrix, or one routed expert), the token rows of x, the weight rows, and the output writer.
+//   bool group(gy, Group &)      false: nothing to do (an expert slot past the active count)
+//   int count(g), rows(g)         tokens (any number; 16 per pass) and weight rows of the group
+//   const uint16_t *xrow(g, tk)   token tk's activations (K of them)
+//   const uint8_t *wrow(g, row)   weight row (row < rows(g))
+//   void finish(g, c0, M, tb, te, out)   write tokens c0 .. c0 + M - 1 of tiles tb .. te - 1;
+//                                 out[(tile - tb) * 256 + tk * 16 + n] is row 16 tile + n
+//   PAIRS                         tiles_per_wg must be even and start even (SwiGLU pairs)
+// Work split: a workgroup owns tiles tb .. te - 1 of its group; the (tile, step) items go to its
+// waves round-robin (item i to wave i % NW), so short K still uses every wave.
+template <class F, class P, int NQ, int D, int NW>
+__global__ __launch_bounds__(64 * NW) void vgemm_kernel(P p, int K, int Kc, int tiles_per_wg) {
   constexpr int NS = F::VNS, MPS = 8 / NS;  // MFMAs per sub-unit
-  constexpr int MT = 4 * NQ;                // tokens padded to whole quads
+  constexpr int MT = 4 * NQ;                // tokens per pass, padded to whole quads
+  typedef typename P::Group Group;
+  Group gp;
+  if (!p.group(blockIdx.y, gp)) return;
   extern __shared__ __align__(16) u4 vgsm[];
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int n = lane & 15, G = lane >> 4;
-  const int ntiles = (N + 15) / 16;
+  const int N = p.rows(gp), ntiles = (N + 15) / 16;
   const int tb = blockIdx.x * tiles_per_wg, te = min(tb + tiles_per_wg, ntiles);
-  const int cs = Kc / 256;                   // steps per chunk
-  const int IW = cs * 32 + 1;                // token image stride (16-byte words, padded)
-  u4 *zero = vgsm + M * IW;                   // 8 words of zeros (non-diagonal A)
-  float *sums = (float *)(zero + 8);         // [cs][4][NS][2][MT]
-  float *accb = sums + cs * 4 * NS * 2 * MT;  // [wave][tile][quad][4][16]
-  u4 *tabs = (u4 *)(accb + NW * tiles_per_wg * NQ * 64);
+  if (tb >= te) return;
+  const int ntl = te - tb;
+  const int cs = Kc / 256;                    // steps per chunk
+  const int IW = cs * 32 + 1;                 // token image stride (16-byte words, padded)
+  u4 *zero = vgsm + MT * IW;                  // 8 words of zeros (non-diagonal A)
+  float *sums = (float *)(zero + 8);          // [cs][4][NS][2][MT]
+  const bool whole = tiles_per_wg >= NW;      // waves take whole tiles (else they split steps)
+  float *accb = sums + cs * 4 * NS * 2 * MT;  // [wave][tile][quad][4][16], split mode only
+  float *outb = accb + (whole ? 0 : NW * tiles_per_wg * NQ * 64);  // [tile][16 tokens][16 rows]
+  u4 *tabs = (u4 *)(outb + tiles_per_wg * 256);
   const uint32_t mg = vconst(0x64006400u);
 
   for (int i = threadIdx.x; i < 8; i += blockDim.x) zero[i] = u4{0, 0, 0, 0};
-  for (int i = threadIdx.x; i < NW * tiles_per_wg * NQ * 64; i += blockDim.x) accb[i] = 0.0f;
   if constexpr (F::VGRID) build_iq2xs_tables_nat(tabs, tabs + 512);
   // A row of this lane: gg = n / 4 (lane group whose k-slot it fills), token tt = n % 4.
   const int gg = n >> 2, tt = n & 3;
+  const int count = p.count(gp);
 
-  for (int kc0 = 0; kc0 < K; kc0 += Kc) {
-    const int steps = min(Kc, K - kc0) / 256;
-    // ---- stage every token's x for this chunk
-    for (int it = threadIdx.x; it < MT * steps * 4 * NS; it += blockDim.x) {
-      const int s = it % NS, g = (it / NS) % 4, j = (it / (NS * 4)) % steps, tk = it / (NS * 4 * steps);
-      float off1 = 0.0f, X = 0.0f;
-      if (tk < M) {
-        u4 A[MPS];
-        F::vstage(x + (size_t)tk * K + kc0, j, g, s, A, off1, X);
-        u4 *dst = vgsm + tk * IW + (j * 4 + g) * 8 + s * MPS;
+  for (int c0 = 0; c0 < count; c0 += MT) {
+    const int M = min(MT, count - c0);
+    if (whole)
+      for (int i = threadIdx.x; i < ntl * 256; i += blockDim.x) outb[i] = 0.0f;
+    else
+      for (int i = threadIdx.x; i < NW * tiles_per_wg * NQ * 64; i += blockDim.x) accb[i] = 0.0f;
+    for (int kc0 = 0; kc0 < K; kc0 += Kc) {
+      const int steps = min(Kc, K - kc0) / 256;
+      // ---- stage every token's x for this chunk
+      for (int it = threadIdx.x; it < MT * steps * 4 * NS; it += blockDim.x) {
+        const int s = it % NS, g = (it / NS) % 4, j = (it / (NS * 4)) % steps, tk = it / (NS * 4 * steps);
+        float off1 = 0.0f, X = 0.0f;
+        if (tk < M) {
+          u4 A[MPS];
+          F::vstage(p.xrow(gp, c0 + tk) + kc0, j, g, s, A, off1, X);
+          u4 *dst = vgsm + tk * IW + (j * 4 + g) * 8 + s * MPS;
 #pragma unroll
-        for (int b = 0; b < MPS; b++) dst[b] = A[b];
-      }
-      float *sp = sums + (((j * 4 + g) * NS + s) * 2) * MT;
-      sp[tk] = off1;
-      sp[MT + tk] = X;
-    }
-    __syncthreads();
-
-    // ---- stream this wave's (tile, step) sequence: steps wave, wave + NW, ... of each tile
-    typedef typename F::VRaw Raw;
-    const bool active = wave < steps && tb < te;
-    const int j_last = wave + (steps - 1 - wave) / NW * NW;
-    const uint8_t *wc = w + (size_t)(kc0 / 256) * F::VSTEP_BYTES;
-    auto load = [&](int tile, int j, Raw &r) {
-      const int row = min(min(tile, te - 1) * 16 + n, N - 1);
-      r = F::vload(wc + (size_t)row * rb, min(j, j_last), G);
-    };
-    auto advance = [&](int &tile, int &j) {
-      j += NW;
-      if (j > j_last) {
-        j = wave;
-        tile++;
-      }
-    };
-    Raw ring[D];
-    int lt = tb, lj = wave;
-    if (active) {
-#pragma unroll
-      for (int d = 0; d < D - 1; d++) {
-        load(lt, lj, ring[d]);
-        advance(lt, lj);
-      }
-    }
-    f4 acc[NQ];
-    int ct = tb, cj = wave;
-    while (active && ct < te) {
-#pragma unroll
-      for (int d = 0; d < D; d++) {
-        load(lt, lj, ring[(d + D - 1) % D]);
-        advance(lt, lj);
-        if (ct >= te) break;
-        const int tl = ct - tb, j = cj;
-        if (j == wave) {
-#pragma unroll
-          for (int q = 0; q < NQ; q++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) acc[q][r] = 0.0f;
+          for (int b = 0; b < MPS; b++) dst[b] = A[b];
         }
-        const Raw &r = ring[d];
-        u4 B[8];
-        F::vdecode(r, B, mg, tabs, tabs + 512);
-        float sc[NS], mn[NS];
+        float *sp = sums + (((j * 4 + g) * NS + s) * 2) * MT;
+        sp[tk] = off1;
+        sp[MT + tk] = X;
+      }
+      __syncthreads();
+
+      // ---- stream this wave's items (tile, step). With at least NW tiles per workgroup each wave
+      // takes whole tiles (tiles wave, wave + NW, ...; partials go straight to outb); with fewer,
+      // the tiles' steps are dealt round-robin (item i to wave i % NW; partials meet in accb).
+      typedef typename F::VRaw Raw;
+      const int items = ntl * steps;
+      const int cnt = whole ? (ntl > wave ? (ntl - wave + NW - 1) / NW : 0) * steps
+                            : (items > wave ? (items - wave + NW - 1) / NW : 0);
+      auto where = [&](int k, int &tl, int &j) {
+        if (whole) {
+          tl = wave + NW * (k / steps);
+          j = k % steps;
+        } else {
+          const int it = wave + NW * k;
+          tl = it / steps;
+          j = it % steps;
+        }
+      };
+      auto load = [&](int k, Raw &r) {
+        int tl, j;
+        where(min(k, cnt - 1), tl, j);
+        const int row = min((tb + tl) * 16 + n, N - 1);
+        r = F::vload(p.wrow(gp, row) + (size_t)(kc0 / 256) * F::VSTEP_BYTES, j, G);
+      };
+      Raw ring[D];
+      if (cnt > 0) {
 #pragma unroll
-        for (int s = 0; s < NS; s++) F::vscale(r, G, s, sc[s], mn[s]);
+        for (int d = 0; d < D - 1; d++) load(d, ring[d]);
+      }
+      f4 acc[NQ];
 #pragma unroll
-        for (int q = 0; q < NQ; q++) {
-          const int tka = 4 * q + tt;
-          const u4 *ab = (gg == G && tka < M) ? vgsm + tka * IW + (j * 4 + G) * 8 : zero;
+      for (int q = 0; q < NQ; q++) acc[q] = f4{0, 0, 0, 0};
+      for (int k0 = 0; k0 < cnt; k0 += D) {
 #pragma unroll
-          for (int s = 0; s < NS; s++) {
-            f4 C = f4{0, 0, 0, 0};
+        for (int d = 0; d < D; d++) {
+          const int k = k0 + d;
+          if (k >= cnt) break;
+          load(k + D - 1, ring[(d + D - 1) % D]);
+          int tl, j;
+          where(k, tl, j);
+          const Raw &r = ring[d];
+          u4 B[8];
+          F::vdecode(r, B, mg, tabs, tabs + 512);
+          float sc[NS], mn[NS];
 #pragma unroll
-            for (int b = 0; b < MPS; b++) C = mfma32(as_h8(ab[s * MPS + b]), as_h8(B[s * MPS + b]), C);
-            const float *sp = sums + (((j * 4 + G) * NS + s) * 2) * MT + 4 * q;
-            const f4 off = *(const f4 *)sp, X = *(const f4 *)(sp + MT);
+          for (int s = 0; s < NS; s++) F::vscale(r, G, s, sc[s], mn[s]);
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc[q][e] += sc[s] * (C[e] - off[e]) + mn[s] * X[e];
+          for (int q = 0; q < NQ; q++) {
+            if (4 * q >= M) break;
+            const int tka = 4 * q + tt;
+            const u4 *ab = (gg == G && tka < M) ? vgsm + tka * IW + (j * 4 + G) * 8 : zero;
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+              f4 C = f4{0, 0, 0, 0};
+#pragma unroll
+              for (int b = 0; b < MPS; b++) C = mfma32(as_h8(ab[s * MPS + b]), as_h8(B[s * MPS + b]), C);
+              const float *sp = sums + (((j * 4 + G) * NS + s) * 2) * MT + 4 * q;
+              const f4 off = *(const f4 *)sp, X = *(const f4 *)(sp + MT);
+#pragma unroll
+              for (int e = 0; e < 4; e++) acc[q][e] += sc[s] * (C[e] - off[e]) + mn[s] * X[e];
+            }
+          }
+          // park at the wave's last item of a tile: sum the row's four lane-group quarters
+          int tl2 = -1, j2;
+          if (k + 1 < cnt) where(k + 1, tl2, j2);
+          if (tl2 != tl) {
+#pragma unroll
+            for (int q = 0; q < NQ; q++) {
+              if (4 * q >= M) break;
+#pragma unroll
+              for (int e = 0; e < 4; e++) {
+                float a = acc[q][e];
+                a += __shfl_xor(a, 16, 64);
+                a += __shfl_xor(a, 32, 64);
+                if (G == 0) {
+                  if (whole) outb[tl * 256 + (4 * q + e) * 16 + n] += a;
+                  else accb[(((wave * tiles_per_wg + tl) * NQ + q) * 4 + e) * 16 + n] += a;
+                }
+                acc[q][e] = 0.0f;
+              }
+            }
           }
         }
-        if (j == j_last) {
-          // sum the four lane groups' quarters of each row, then park the wave's partial
-#pragma unroll
-          for (int q = 0; q < NQ; q++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-              float a = acc[q][e];
-              a += __shfl_xor(a, 16, 64);
-              a += __shfl_xor(a, 32, 64);
-              if (G == 0) accb[(((wave * tiles_per_wg + tl) * NQ + q) * 4 + e) * 16 + n] += a;
-            }
-        }
-        advance(ct, cj);
       }
+      __syncthreads();  // partials parked; the x image is free for the next chunk
     }
-    __syncthreads();  // partials parked; the x image is free for the next chunk
-  }
-  // ---- sum the waves' partials and write y
-  for (int o = threadIdx.x; o < (te - tb) * NQ * 64; o += blockDim.x) {
-    const int tl = o / (NQ * 64), q = (o / 64) % NQ, e = (o / 16) % 4, nn = o % 16;
-    float s = 0.0f;
-    for (int v = 0; v < NW; v++) s += accb[(((v * tiles_per_wg + tl) * NQ + q) * 4 + e) * 16 + nn];
-    const int tk = 4 * q + e, row = (tb + tl) * 16 + nn;
-    if (tk < M && row < N) y[(size_t)tk * N + row] = f2h(s);
+    if (!whole) {  // sum the waves' partials
+      for (int o = threadIdx.x; o < ntl * 256; o += blockDim.x) {
+        const int tl = o >> 8, tk = (o >> 4) & 15, nn = o & 15;
+        float sm = 0.0f;
+        if (tk < MT)
+          for (int v = 0; v < NW; v++) sm += accb[(((v * tiles_per_wg + tl) * NQ + (tk >> 2)) * 4 + (tk & 3)) * 16 + nn];
+        outb[o] = sm;
+      }
+      __syncthreads();
+    }
+    p.finish(gp, c0, M, tb, te, outb);
+    __syncthreads();
   }
 }
 
 int gemv_num_cu();
 
-template <class F, int NQ>
-static int launch_vgemm(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st) {
-  constexpr int D = 4, NW = 8;
-  constexpr int NS = F::VNS, MT = 4 * NQ;
-  const int ntiles = (N + 15) / 16;
-  const int T = (ntiles + gemv_num_cu() - 1) / gemv_num_cu();  // tiles per workgroup: one round of CUs
-  const int wgs = (ntiles + T - 1) / T;
-  auto need = [&](int kc) {
-    const int cs = kc / 256;
-    return (size_t)M * (cs * 32 + 1) * 16 + 8 * 16 + (size_t)cs * 4 * NS * 2 * MT * 4 +
-           (size_t)NW * T * NQ * 64 * 4 + (F::VGRID ? (512 + 128) * 16 : 0);
-  };
+template <class F, int NQ, int NW>
+static size_t vgemm_lds(int Kc, int T) {
+  constexpr int MT = 4 * NQ;
+  const int cs = Kc / 256;
+  return (size_t)MT * (cs * 32 + 1) * 16 + 8 * 16 + (size_t)cs * 4 * F::VNS * 2 * MT * 4 +
+         (T >= NW ? 0 : (size_t)NW * T * NQ * 64 * 4) + (size_t)T * 256 * 4 + (F::VGRID ? (512 + 128) * 16 : 0);
+}
+
+// Launch over `groups` groups of (up to) `rows` weight rows each; T tiles per workgroup.
+template <class F, class P, int NQ>
+static int launch_vgemm_p(const P &p, int K, int rows, int groups, int T, hipStream_t st) {
+  constexpr int NW = 8;
+  constexpr int D = F::VDEPTH;  // ring depth: what fits the registers with the format's raw
+  const int ntiles = (rows + 15) / 16;
   const size_t budget = 150 * 1024;
   int Kc = K;
-  while (Kc > 256 && need(Kc) > budget) Kc -= 256;
-  if (need(Kc) > budget) return decline("verify x does not fit in LDS");
-  const size_t rb = (size_t)(K / F::BS) * F::TS;
-  hipLaunchKernelGGL((vgemm_kernel<F, NQ, D, NW>), dim3(wgs), dim3(64 * NW), need(Kc), st, (const uint16_t *)x, M, K,
-                     (const uint8_t *)w, rb, N, (uint16_t *)y, Kc, T);
+  while (Kc > 256 && vgemm_lds<F, NQ, NW>(Kc, T) > budget) Kc -= 256;
+  if (vgemm_lds<F, NQ, NW>(Kc, T) > budget) return decline("verify x does not fit in LDS");
+  const size_t lds = vgemm_lds<F, NQ, NW>(Kc, T);
+  hipLaunchKernelGGL((vgemm_kernel<F, P, NQ, D, NW>), dim3((ntiles + T - 1) / T, groups), dim3(64 * NW), lds, st, p,
+                     K, Kc, T);
   ISHZ_LAUNCH_CHECK("vgemm launch");
   return ISHZ_OK;
 }
 
+// The plain problem: y[M][N] = x[M][K] . W^T for 2..16 tokens.
+struct VPlain {
+  const uint16_t *x;
+  const uint8_t *w;
+  size_t rb;
+  int M, K, N;
+  uint16_t *y;
+  struct Group {};
+  DEV bool group(int, Group &) const { return true; }
+  DEV int count(const Group &) const { return M; }
+  DEV int rows(const Group &) const { return N; }
+  DEV const uint16_t *xrow(const Group &, int tk) const { return x + (size_t)tk * K; }
+  DEV const uint8_t *wrow(const Group &, int row) const { return w + (size_t)row * rb; }
+  DEV void finish(const Group &, int c0, int m, int tb, int te, const float *out) const {
+    for (int o = threadIdx.x; o < (te - tb) * 256; o += blockDim.x) {
+      const int tk = (o >> 4) & 15, row = (tb + (o >> 8)) * 16 + (o & 15);
+      if (tk < m && row < N) y[(size_t)(c0 + tk) * N + row] = f2h(out[o]);
+    }
+  }
+};
+
 template <class F>
 static int vgemm(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st) {
+  const VPlain p{(const uint16_t *)x, (const uint8_t *)w, (size_t)(K / F::BS) * F::TS, M, K, N, (uint16_t *)y};
+  const int ntiles = (N + 15) / 16;
+  const int T = (ntiles + gemv_num_cu() - 1) / gemv_num_cu();  // tiles per workgroup: one round of CUs
   switch ((M + 3) / 4) {
-    case 1: return launch_vgemm<F, 1>(x, M, K, w, N, y, st);
-    case 2: return launch_vgemm<F, 2>(x, M, K, w, N, y, st);
-    case 3: return launch_vgemm<F, 3>(x, M, K, w, N, y, st);
-    default: return launch_vgemm<F, 4>(x, M, K, w, N, y, st);
+    case 1: return launch_vgemm_p<F, VPlain, 1>(p, K, N, 1, T, st);
+    case 2: return launch_vgemm_p<F, VPlain, 2>(p, K, N, 1, T, st);
+    case 3: return launch_vgemm_p<F, VPlain, 3>(p, K, N, 1, T, st);
+    default: return launch_vgemm_p<F, VPlain, 4>(p, K, N, 1, T, st);
   }
 }
 
