@@ -29,89 +29,72 @@ struct MoeRoute {
   int32_t *inv;       // [T*k] sorted position of (t, s)
 };
 
-// One workgroup of 1024 threads. Routing: one wave per token (lanes over experts), the top-k by
-// k rounds of a wave-wide arg-max in (logit desc, index asc) order. Pair lists: per-expert counts
-// in LDS, a prefix over experts, then each pair placed at offs[e] + (its rank among earlier pairs
-// of e), so the order inside an expert is (token, slot) and deterministic.
-DEV void argmax_merge(float &v, int &e, float ov, int oe) {
-  if (oe >= 0 && (e < 0 || ov > v || (ov == v && oe < e))) {
-    v = ov;
-    e = oe;
+// Routing ranks each expert against the token's whole logit row (rank = experts with a larger
+// logit, or an equal one at a lower index): the top-k are the experts of rank < k, already in the
+// reference's order (logit descending, ties to the lower index). Softmax max and sum are wave
+// reductions; the top-k probabilities are summed in rank order for the renormalisation.
+DEV float wave_max(float v) {
+  v = fmaxf(v, ISHZ_DPP(v, 0xB1));
+  v = fmaxf(v, ISHZ_DPP(v, 0x4E));
+  v = fmaxf(v, ISHZ_DPP(v, 0x141));
+  v = fmaxf(v, ISHZ_DPP(v, 0x140));
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+
+// Routing: one 64-lane workgroup per token, so tokens route in parallel.
+__global__ __launch_bounds__(64) void moe_route_kernel(const float *__restrict__ logits, int T, int E,
+                                                       int k, int normalize, MoeRoute R) {
+  extern __shared__ __align__(16) float rowb[];  // the token's logits, padded to whole float4; then 64 probs
+  const int lane = threadIdx.x, t = blockIdx.x;
+  const int E4 = (E + 3) & ~3;
+  float *pb = rowb + E4;
+  const float *l = logits + (size_t)t * E;
+  float mx = -INFINITY;
+  for (int e = lane; e < E4; e += 64) {
+    const float v = e < E ? l[e] : -INFINITY;  // -inf never ranks above a logit
+    rowb[e] = v;
+    mx = fmaxf(mx, v);
+  }
+  mx = wave_max(mx);
+  float sum = 0.0f;
+  for (int e = lane; e < E; e += 64) sum += expf(rowb[e] - mx);
+  sum = group_sum<64>(sum);
+  __syncthreads();
+  for (int e = lane; e < E; e += 64) {
+    const float v = rowb[e];
+    int rank = 0;
+#pragma unroll 8
+    for (int f = 0; f < E4; f += 4) {
+      const f4 u = *(const f4 *)(rowb + f);
+#pragma unroll
+      for (int c = 0; c < 4; c++) rank += (u[c] > v) | ((u[c] == v) & (f + c < e));
+    }
+    if (rank < k) {
+      R.ids[t * k + rank] = e;
+      pb[rank] = expf(v - mx) / sum;
+    }
+  }
+  __syncthreads();
+  float tot = 0.0f;  // rank-order sum of the top-k probabilities
+  for (int s = 0; s < k; s++) tot += pb[s];
+  if (lane < k) {
+    const float p = pb[lane];
+    R.w[t * k + lane] = normalize ? p / tot : p;
   }
 }
 
-__global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict__ logits, int T,
-                                                         int E, int k, int normalize, MoeRoute R) {
-  extern __shared__ int32_t cnt[];  // E counts
-  const int lane = threadIdx.x & 63, wave = wave_id(), waves = blockDim.x >> 6;
+// Pair lists (one workgroup): per-expert counts in LDS, an exclusive prefix over experts by wave
+// 0, then each pair takes the next free position of its expert (the order inside an expert does
+// not affect any result: every pair's rows are computed independently).
+__global__ __launch_bounds__(1024) void moe_place_kernel(int T, int E, int k, MoeRoute R) {
+  extern __shared__ int32_t cnt[];  // E counts, then fill cursors
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int P = T * k;
   for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
   __syncthreads();
-  int32_t *ids_l = cnt + E;  // T*k ids kept in LDS for the placement below (when R.offs)
-  constexpr int EPL = 8;     // logits a lane keeps in registers (E <= 512)
-  for (int t = wave; t < T; t += waves) {
-    const float *l = logits + (size_t)t * E;
-    const bool cached = E <= 64 * EPL;
-    float lv[EPL];
-#pragma unroll
-    for (int i = 0; i < EPL; i++) lv[i] = cached && lane + 64 * i < E ? l[lane + 64 * i] : -INFINITY;
-    float mx = -INFINITY;
-    if (cached) {
-#pragma unroll
-      for (int i = 0; i < EPL; i++) mx = fmaxf(mx, lv[i]);
-    } else {
-      for (int e = lane; e < E; e += 64) mx = fmaxf(mx, l[e]);
-    }
-    for (int m = 32; m; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
-    float sum = 0.0f;
-    if (cached) {
-#pragma unroll
-      for (int i = 0; i < EPL; i++)
-        if (lane + 64 * i < E) sum += expf(lv[i] - mx);
-    } else {
-      for (int e = lane; e < E; e += 64) sum += expf(l[e] - mx);
-    }
-    for (int m = 32; m; m >>= 1) sum += __shfl_xor(sum, m, 64);
-    float prev_v = INFINITY, tot = 0.0f, wsel = 0.0f;
-    int prev_e = -1;
-    for (int s = 0; s < k; s++) {
-      float bv = -INFINITY;
-      int be = -1;
-      if (cached) {
-#pragma unroll
-        for (int i = 0; i < EPL; i++) {
-          const int e = lane + 64 * i;
-          const float v = lv[i];
-          if (e < E && (v < prev_v || (v == prev_v && e > prev_e))) argmax_merge(bv, be, v, e);
-        }
-      } else {
-        for (int e = lane; e < E; e += 64) {
-          const float v = l[e];
-          if (v < prev_v || (v == prev_v && e > prev_e)) argmax_merge(bv, be, v, e);
-        }
-      }
-      for (int m = 32; m; m >>= 1) {
-        const float ov = __shfl_xor(bv, m, 64);
-        const int oe = __shfl_xor(be, m, 64);
-        argmax_merge(bv, be, ov, oe);
-      }
-      const float p = expf(bv - mx) / sum;
-      if (lane == s) wsel = p;
-      tot += p;
-      prev_v = bv;
-      prev_e = be;
-      if (lane == 0) {
-        R.ids[t * k + s] = be;
-        if (R.offs) {
-          ids_l[t * k + s] = be;
-          atomicAdd(&cnt[be], 1);
-        }
-      }
-    }
-    if (lane < k) R.w[t * k + lane] = normalize ? wsel / tot : wsel;
-  }
-  if (!R.offs) return;  // routing only
+  for (int q = threadIdx.x; q < P; q += blockDim.x) atomicAdd(&cnt[R.ids[q]], 1);
   __syncthreads();
-  // exclusive prefix of the counts by wave 0 (64 experts per round), active list by rank
   if (wave == 0) {
     int carry = 0, nact = 0;
     for (int e0 = 0; e0 < E; e0 += 64) {
@@ -127,6 +110,7 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict
       }
       if (e < E) {
         R.offs[e] = carry + incl - c;
+        cnt[e] = carry + incl - c;  // fill cursor
         if (c) R.active[nact + act - 1] = e;
       }
       carry += __shfl(incl, 63, 64);
@@ -137,13 +121,9 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict
       R.count[0] = nact;
     }
   }
-  const int P = T * k;
   __syncthreads();
   for (int q = threadIdx.x; q < P; q += blockDim.x) {
-    const int e = ids_l[q];
-    int rank = 0;
-    for (int q2 = 0; q2 < q; q2++) rank += ids_l[q2] == e;
-    const int pos = R.offs[e] + rank;
+    const int pos = atomicAdd(&cnt[R.ids[q]], 1);
     R.pair_tok[pos] = q / k;
     R.inv[q] = pos;
   }
@@ -371,7 +351,9 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
                    hipStream_t st) {
   const int amax = std::min(E, T * k);
   static const bool old = getenv("ISHZ_OLD_MOE") != nullptr;
-  if (H % 256 == 0 && I % 256 == 0 && !old) {
+  // streaming MFMA kernels from 3 tokens up; one or two tokens (a GEMV per expert) run faster on
+  // the per-block kernels below, which start streaming without staging x
+  if (H % 256 == 0 && I % 256 == 0 && T > 2 && !old) {
     // tiles per workgroup: about two workgroups per CU over the routed experts (gate/up: an even
     // count, whole SwiGLU pairs); with 8 or more a wave takes whole tiles
     const int tiles_gu = 2 * ((I + 15) / 16), tiles_dn = (H + 15) / 16;
@@ -415,11 +397,12 @@ extern "C" size_t ishz_moe_workspace_size(int T, int H, int E, int I, int topk) 
 
 extern "C" int ishz_moe_route(const float *logits, int T, int E, int topk, int normalize,
                               int32_t *ids, float *weights, ishz_stream_t stream) {
-  if (T <= 0 || E <= 0 || topk <= 0 || topk > E || E > 4096) return decline("bad routing shape");
+  if (T <= 0 || E <= 0 || topk <= 0 || topk > E || topk > 64) return decline("bad routing shape");
+  if ((size_t)(E + 3 + 64) * 4 > 64 * 1024) return decline("too many experts for one routing workgroup");
   if (!logits || !ids || !weights) return einval("null pointer");
   MoeRoute R{ids, weights, nullptr, nullptr, nullptr, nullptr, nullptr};
-  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(1024), (size_t)E * 4, S(stream), logits, T, E,
-                     topk, normalize, R);
+  hipLaunchKernelGGL(moe_route_kernel, dim3(T), dim3(64), (size_t)(E + 3 + 64) * 4, S(stream), logits, T, E, topk,
+                     normalize, R);
   ISHZ_LAUNCH_CHECK("moe route launch");
   return ISHZ_OK;
 }
@@ -435,7 +418,7 @@ extern "C" int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T,
     return decline("MoE experts must be Q4_0, Q4_K or Q6_K");
   if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
   if (T <= 0 || E <= 0 || topk <= 0 || topk > E || E > 4096) return decline("bad routing shape");
-  if ((size_t)(E + T * topk) * 4 > 64 * 1024) return decline("too many tokens for one routing workgroup");
+  if (topk > 64 || (size_t)(E + 3 + 64) * 4 > 64 * 1024) return decline("too many experts for one routing workgroup");
   if (H <= 0 || I <= 0 || H % bs || I % bs) return decline("H and I must be whole blocks");
   const size_t need = (size_t)I * (H / bs) * ishz_ggml_type_size(type);
   if (expert_bytes < need || (size_t)H * (I / bs) * ishz_ggml_type_size(type) > expert_bytes)
@@ -445,9 +428,11 @@ extern "C" int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T,
   if (!workspace || workspace_bytes < L.total) return einval("workspace too small (ishz_moe_workspace_size)");
   MoeRoute R = moe_route_ptrs(workspace, L);
   hipStream_t st = S(stream);
-  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(1024), (size_t)(E + T * topk) * 4, st, logits, T,
-                     E, topk, normalize, R);
+  hipLaunchKernelGGL(moe_route_kernel, dim3(T), dim3(64), (size_t)(E + 3 + 64) * 4, st, logits, T, E, topk,
+                     normalize, R);
   ISHZ_LAUNCH_CHECK("moe route launch");
+  hipLaunchKernelGGL(moe_place_kernel, dim3(1), dim3(1024), (size_t)E * 4, st, T, E, topk, R);
+  ISHZ_LAUNCH_CHECK("moe place launch");
   uint16_t *h = (uint16_t *)((uint8_t *)workspace + L.h), *o = (uint16_t *)((uint8_t *)workspace + L.o);
   int rc;
   switch (type) {
