@@ -48,6 +48,19 @@ def test_swiglu_small(T, type_):
     assert_close(y.float().cpu().numpy(), ref, what=f"moe T={T}")
 
 
+def test_swiglu_many_tokens_per_expert():
+    """4 experts, top-2 of 40 tokens: about 20 tokens per expert, more than one 16-token pass."""
+    E, H, I, k, T = 4, 512, 256, 2, 40
+    (g, u, d), ex = experts(E, H, I, ggml.Q4_K, seed=77)
+    x = synth.fp16_normal((T, H), seed=78)
+    logits = np.random.default_rng(79).standard_normal((T, E)).astype(np.float32)
+    y = moe.swiglu(torch.from_numpy(x).to(DEV), torch.from_numpy(logits).to(DEV), ex, top_k=k)
+    rid, rw = oracle.moe_route(logits, k)
+    assert np.bincount(rid.reshape(-1), minlength=E).max() > 16
+    ref = oracle.moe_swiglu(ggml.Q4_K, x.astype(np.float32), rid, rw, g, u, d, E, I)
+    assert_close(y.float().cpu().numpy(), ref, what="moe many tokens per expert")
+
+
 def test_swiglu_qwen_shape():
     # Qwen MoE: 128 experts, hidden 2048, expert intermediate 768, top-8, T = 8
     E, H, I, k, T = 128, 2048, 768, 8, 8
