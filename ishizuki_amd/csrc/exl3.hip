@@ -264,6 +264,115 @@ __global__ __launch_bounds__(1024) void exl3_mm2(const uint16_t *__restrict__ xh
   }
 }
 
+// Wide-step matvec / verify for the integer rates of 1, 2 and 4 bits: a wave's step is TN = 32/KA
+// adjacent column tiles of one K tile (1 KB contiguous), fetched with one 128-bit load per lane
+// and spread through LDS, so each wave keeps kilobytes in flight instead of the few hundred
+// bytes that per-lane word loads give. Lanes decode as in exl3_mm2 (32-bit windows, pairwise
+// codebook). The K tiles split over workgroups (blockIdx.y) and over a workgroup's waves; partial
+// outputs are summed into yh with atomic adds (yh zeroed first), in no fixed order.
+template <int KA, int CB, bool MF, int D>
+__global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh, int M, int K,
+                                               const uint32_t *__restrict__ trellis, int N,
+                                               float *__restrict__ yh, int tk_per_wg) {
+  using TR = Trellis<KA, false>;
+  using T32 = Trellis32<KA, false>;
+  constexpr int TN = 32 / KA, W = TR::WORDS;  // TN tiles of W words = 256 words per step
+  extern __shared__ __align__(16) float sm3[];
+  const int lane = threadIdx.x & 63, wave = wave_id(), KS = blockDim.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int tn0 = blockIdx.x * TN, tiles_n = N / 16, tiles_k = K / 16;
+  const int tk0 = blockIdx.y * tk_per_wg, tk1 = min(tk0 + tk_per_wg, tiles_k);
+  const typename T32::Win wn = T32::window(8 * (4 * (j & 7) + g) + 4 * (j >> 3));
+  const int tok = MF ? (j < M ? j : 0) : 0;
+  const bool live = MF ? j < M : true;
+  const uint16_t *xr = xh + (size_t)tok * K + 2 * g;
+  const size_t tstride = (size_t)tiles_n * W;  // words between K tiles
+  const uint32_t *base = trellis + (size_t)tn0 * W + 4 * lane;
+  uint32_t *stage = (uint32_t *)sm3 + wave * 256;  // this wave's step
+  float *red = sm3 + KS * 256;
+
+  struct Raw {
+    u4 w;
+    uint32_t xa, xb;
+  };
+  const int nsteps = tk1 - tk0 > wave ? (tk1 - tk0 - wave + KS - 1) / KS : 0;
+  auto load = [&](int i, Raw &r) {
+    const int tk = tk0 + wave + KS * min(i, nsteps - 1);
+    r.w = *(const u4 *)(base + tk * tstride);
+    r.xa = *(const uint32_t *)(xr + 16 * tk);
+    r.xb = *(const uint32_t *)(xr + 16 * tk + 8);
+  };
+  using Acc = typename std::conditional<MF, f4, float>::type;
+  Acc acc[TN];
+#pragma unroll
+  for (int t = 0; t < TN; t++) acc[t] = Acc{};
+  Raw ring[D];
+  if (nsteps > 0) {
+#pragma unroll
+    for (int d = 0; d < D - 1; d++) load(d, ring[d]);
+  }
+  for (int i0 = 0; i0 < nsteps; i0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+      const int i = i0 + d;
+      if (i >= nsteps) break;
+      load(i + D - 1, ring[(d + D - 1) % D]);
+      const Raw &r = ring[d];
+      *(u4 *)(stage + 4 * lane) = r.w;  // the wave's own buffer: its LDS operations stay in order
+#pragma unroll
+      for (int t = 0; t < TN; t++) {
+        const uint32_t w0 = stage[t * W + wn.ja], w1 = stage[t * W + wn.jb];
+        const uint32_t win = __builtin_amdgcn_alignbit(w0, w1, wn.amt);
+        const uint32_t s0 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(0), 16);
+        const uint32_t s1 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(1), 16);
+        const uint32_t s2 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(2), 16);
+        const uint32_t s3 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(3), 16);
+        const uint32_t b01 = exl3_decode2<CB>(s0, s1), b23 = exl3_decode2<CB>(s2, s3);
+        if constexpr (MF) {
+          const u2 A = live ? u2{r.xa, r.xb} : u2{0, 0};
+          acc[t] = mfma16(as_h4(A), as_h4(u2{b01, b23}), acc[t]);
+        } else {
+          acc[t] = dot2(b23, r.xb, dot2(b01, r.xa, acc[t]));
+        }
+      }
+    }
+  }
+  // partials: sum over the wave's lane groups (M = 1) and over the workgroup's waves in LDS,
+  // then one atomic add per output
+  if constexpr (MF) {
+    for (int o = threadIdx.x; o < TN * 256; o += blockDim.x) red[o] = 0.0f;
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < TN; t++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) atomicAdd(&red[(t * 4 + q) * 64 + lane], acc[t][q]);
+    __syncthreads();
+    for (int o = threadIdx.x; o < TN * 256; o += blockDim.x) {
+      const int t = o >> 8, q = (o >> 6) & 3, l = o & 63;
+      const int tk = 4 * (l >> 4) + q;
+      if (tk < M) atomicAdd(&yh[(size_t)tk * N + (tn0 + t) * 16 + (l & 15)], red[o]);
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < TN; t++) {
+      float a = acc[t];
+      a += __shfl_xor(a, 16, 64);
+      a += __shfl_xor(a, 32, 64);
+      if (g == 0) red[(wave * TN + t) * 16 + j] = a;
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < TN * 16; o += blockDim.x) {
+      float sum = 0.0f;
+      for (int v = 0; v < KS; v++) sum += red[(v * TN + (o >> 4)) * 16 + (o & 15)];
+      atomicAdd(&yh[(tn0 + (o >> 4)) * 16 + (o & 15)], sum);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void exl3_zero_kernel(float *__restrict__ p, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0.0f;
+}
+
 // ------------------------------------------------------------------- dequantize
 template <int KA, bool HALF>
 __global__ __launch_bounds__(256) void exl3_dequant_kernel(const uint32_t *__restrict__ trellis,
@@ -424,6 +533,40 @@ extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const
   int ks = 1;
   while (ks < 16 && ks < tiles_k && wgs * ks < num_cu_e() * 16) ks *= 2;
   return by_rate(bits2, [&]<int KA, bool HALF>() -> int {
+    if constexpr (!HALF && (KA == 1 || KA == 2 || KA == 4)) {
+      static const bool mm2 = getenv("ISHZ_EXL3_MM2") != nullptr;
+      if (!getenv("ISHZ_EXL3_OLD") && !mm2) {
+        constexpr int TN = 32 / KA, KS3 = 4, D = 4;
+        const int tn_blocks = N / 16 / TN;  // N % 128 == 0
+        static const int split_env = [] {
+          const char *e = getenv("ISHZ_EXL3_SPLITS");  // tuning
+          return e ? atoi(e) : 0;
+        }();
+        // K splits: about four workgroups per CU for one row, two with MFMA rows (each split adds
+        // one atomic per output and row)
+        const int splits = split_env > 0 ? split_env
+                                         : std::max(1, std::min(tiles_k / KS3, (M == 1 ? 4 : 2) * num_cu_e() / tn_blocks));
+        const int per = (tiles_k + splits - 1) / splits;
+        const size_t n = (size_t)M * N;
+        hipLaunchKernelGGL(exl3_zero_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 1024)), dim3(256), 0,
+                           S(stream), yh, n);
+        const size_t lds = (size_t)KS3 * 256 * 4 + (M == 1 ? (size_t)KS3 * TN * 16 * 4 : (size_t)TN * 256 * 4);
+        auto go = [&]<int CB>() -> int {
+          if (M == 1)
+            hipLaunchKernelGGL((exl3_mm3<KA, CB, false, D>), dim3(tn_blocks, (tiles_k + per - 1) / per),
+                               dim3(64 * KS3), lds, S(stream), (const uint16_t *)xh, M, K, (const uint32_t *)trellis,
+                               N, yh, per);
+          else
+            hipLaunchKernelGGL((exl3_mm3<KA, CB, true, D>), dim3(tn_blocks, (tiles_k + per - 1) / per),
+                               dim3(64 * KS3), lds, S(stream), (const uint16_t *)xh, M, K, (const uint32_t *)trellis,
+                               N, yh, per);
+          ISHZ_LAUNCH_CHECK("exl3 matvec launch");
+          return ISHZ_OK;
+        };
+        return codebook == 0 ? go.template operator()<0>()
+                             : codebook == 1 ? go.template operator()<1>() : go.template operator()<2>();
+      }
+    }
     if constexpr (Trellis32<KA, HALF>::FITS) {
       if (!getenv("ISHZ_EXL3_OLD")) {
         // TN = 4 column tiles per workgroup (N % 128 == 0 makes N / 16 a multiple of 8); 8 waves
