@@ -49,7 +49,7 @@ def test_dequant_random_rates(bits2, cb):
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 8, 16])
-@pytest.mark.parametrize("bits2,cb", [(4, 0), (4, 2), (3, 2), (6, 1)])
+@pytest.mark.parametrize("bits2,cb", [(4, 0), (4, 2), (3, 2), (6, 1), (2, 0), (2, 2), (8, 1), (10, 0)])
 def test_matvec(M, bits2, cb):
     K, N = 1024, 512
     t, _, _, ten = make(K, N, bits2, cb, seed=M + bits2)
