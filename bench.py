@@ -152,12 +152,16 @@ def main():
         nb = distinct * 3 * ex.expert_bytes
         return calls, nb, nb, distinct
 
-    def measure(name, builder, M, steps, warmup, extra=None):
+    def measure(name, builder, M, steps, warmup, extra=None, nk=None):
         out = builder()
         calls, wbytes, allbytes = out[0], out[1], out[2]
         sec, n = timed(calls, steps, warmup)
         r = {"name": name, "M": M, "us": round(sec * 1e6, 3), "weight_bytes": int(wbytes),
              "GBps": round(wbytes / sec / 1e9, 1), "hbm_frac": round(wbytes / sec / HBM_PEAK, 4)}
+        if nk and M >= 2:  # verify: useful FLOP = 2 M N K against the 2.5 PFLOP/s dense fp16 MFMA peak
+            flops = 2.0 * M * nk[0] * nk[1]
+            r.update({"TFLOPs": round(flops / sec / 1e12, 2), "mfma_frac": round(flops / sec / 2.5e15, 4),
+                      "bytes_per_flop": round(wbytes / flops, 4)})
         if extra:
             r.update(extra(out))
         del out, calls
@@ -184,7 +188,7 @@ def main():
         if only and name not in only:
             continue
         for M in (1, 8):
-            r, _, _ = measure(f"{name}", lambda b=b, M=M: b(M), M, fam_steps, args.warmup)
+            r, _, _ = measure(f"{name}", lambda b=b, M=M: b(M), M, fam_steps, args.warmup, nk=(NS, KS))
             r["shape"] = f"{NS}x{KS}"
             families.append(r)
     if not only or "moe" in only:
@@ -201,13 +205,14 @@ def main():
             for (N, K) in ((25600, 5120), (5120, 25600)):
                 for M in (1, 8):
                     r, _, _ = measure(f"{nm}_mlp", lambda t=t, N=N, K=K, M=M: ggml_case(t, N, K, M), M, fam_steps,
-                                      args.warmup)
+                                      args.warmup, nk=(N, K))
                     r["shape"] = f"{N}x{K}"
                     families.append(r)
         for M in (2, 4):
-            r, _, _ = measure("affine2_g64_wht128", lambda M=M: affine_case(NS, KS, M), M, fam_steps, args.warmup)
+            r, _, _ = measure("affine2_g64_wht128", lambda M=M: affine_case(NS, KS, M), M, fam_steps, args.warmup,
+                              nk=(NS, KS))
             families.append(r)
-            r, _, _ = measure("exl3_2bpw", lambda M=M: exl3_case(KS, NS, M), M, fam_steps, args.warmup)
+            r, _, _ = measure("exl3_2bpw", lambda M=M: exl3_case(KS, NS, M), M, fam_steps, args.warmup, nk=(NS, KS))
             families.append(r)
 
     # ------------------------------------------------------------------ CPU baseline
