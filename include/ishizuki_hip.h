@@ -43,7 +43,7 @@ const char *ishz_last_error(void);
 int ishz_version(void);
 
 /* GGMLType.blockSize / typeSize (Config/GGUFFile.swift:45-80) for the types this library
-   decodes; 0 for any other type. */
+   decodes; 0 for any other type (ishz_ggml_geometry covers every GGMLType). */
 int ishz_ggml_block_size(uint32_t type);
 int ishz_ggml_type_size(uint32_t type);
 
@@ -150,6 +150,53 @@ int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T, int H, con
                     const void *down, size_t expert_bytes, int I, void *y, int32_t *ids_out,
                     float *weights_out, void *workspace, size_t workspace_bytes,
                     ishz_stream_t stream);
+
+/* ---------------------------------------------------------------- GGUF container (host side)
+ * GGUFFile (Config/GGUFFile.swift:179-397): header, metadata and tensor table of a .gguf file,
+ * the tensor bytes left in a read-only memory mapping. Malformed or unsupported files give
+ * ISHZ_EINVAL with the reference's reason (ishz_last_error). Shapes are row-major (GGUF's dims
+ * reversed); tensor offsets are relative to the data section, as in TensorInfo. Pointers here
+ * are host pointers; the handle is immutable after open and may be shared between threads. */
+typedef struct ishz_gguf ishz_gguf;
+typedef struct ishz_gguf_value ishz_gguf_value;
+
+/* GGMLType raw value known (1) or not (0), and its blockSize / typeSize
+ * (Config/GGUFFile.swift:39-88); ISHZ_DECLINED for an unknown value. */
+int ishz_ggml_type_known(uint32_t type);
+int ishz_ggml_geometry(uint32_t type, int *block_size, int *type_size);
+
+int ishz_gguf_open(const char *path, ishz_gguf **out);   /* GGUFFile.init(url:) */
+void ishz_gguf_close(ishz_gguf *f);
+uint32_t ishz_gguf_version(const ishz_gguf *f);
+uint64_t ishz_gguf_data_offset(const ishz_gguf *f);       /* GGUFFile.dataOffset */
+int64_t ishz_gguf_tensor_count(const ishz_gguf *f);
+int64_t ishz_gguf_find_tensor(const ishz_gguf *f, const char *name);  /* subscript(tensor:); -1 if absent */
+/* TensorInfo: name (owned by the handle), rank, shape[4] (row-major, unused dims 0), type,
+ * offset (from the data section), byte count. */
+int ishz_gguf_tensor_info(const ishz_gguf *f, int64_t i, const char **name, int *rank, int64_t *shape,
+                          uint32_t *type, uint64_t *offset, uint64_t *nbytes);
+/* data(for:) (:289-301): the tensor's bytes inside the mapping, or NULL (ISHZ_EINVAL) when they
+ * run past the end of the file. */
+const void *ishz_gguf_tensor_data(const ishz_gguf *f, int64_t i);
+/* GGUFWeights.load's packed path (Core/GGUFWeights.swift:47-85): copy a tensor's blocks as they
+ * lie on disk into caller-owned device memory (dst_bytes >= its byte count); returns when done. */
+int ishz_gguf_tensor_upload(const ishz_gguf *f, int64_t i, void *dst, size_t dst_bytes, ishz_stream_t stream);
+
+/* Metadata: keys in file order (a repeated key keeps its last value), values as GGUFValue
+ * (:125-168). Arrays nest; scalars read through the reference's accessors (intValue,
+ * floatValue, boolValue, stringValue), ISHZ_DECLINED when a value has no such reading. */
+int64_t ishz_gguf_kv_count(const ishz_gguf *f);
+const char *ishz_gguf_kv_key(const ishz_gguf *f, int64_t i);
+int64_t ishz_gguf_find_kv(const ishz_gguf *f, const char *key);  /* subscript(_:); -1 if absent */
+const ishz_gguf_value *ishz_gguf_kv_value(const ishz_gguf *f, int64_t i);
+int ishz_gguf_value_type(const ishz_gguf_value *v);              /* GGUF value type 0..12 (9 = array) */
+int64_t ishz_gguf_value_len(const ishz_gguf_value *v);           /* array length, -1 otherwise */
+const ishz_gguf_value *ishz_gguf_value_elem(const ishz_gguf_value *v, int64_t j);
+int ishz_gguf_value_int(const ishz_gguf_value *v, int64_t *out);
+int ishz_gguf_value_float(const ishz_gguf_value *v, double *out);
+int ishz_gguf_value_bool(const ishz_gguf_value *v, int *out);
+int ishz_gguf_value_string(const ishz_gguf_value *v, const char **s, size_t *len);
+int ishz_gguf_value_raw(const ishz_gguf_value *v, uint64_t *u, int64_t *i, double *d);
 
 #ifdef __cplusplus
 }

@@ -35,6 +35,32 @@ _SIGS = {
     "ishz_moe_route": (I, [P, I, I, I, I, P, P, P]),
     "ishz_moe_workspace_size": (SZ, [I, I, I, I, I]),
     "ishz_moe_swiglu": (I, [U32, P, I, I, I, P, I, I, I, P, P, P, SZ, I, P, P, P, P, SZ, P]),
+    "ishz_ggml_type_known": (I, [U32]),
+    "ishz_ggml_geometry": (I, [U32, ctypes.POINTER(I), ctypes.POINTER(I)]),
+    "ishz_gguf_open": (I, [ctypes.c_char_p, ctypes.POINTER(P)]),
+    "ishz_gguf_close": (None, [P]),
+    "ishz_gguf_version": (U32, [P]),
+    "ishz_gguf_data_offset": (ctypes.c_uint64, [P]),
+    "ishz_gguf_tensor_count": (ctypes.c_int64, [P]),
+    "ishz_gguf_find_tensor": (ctypes.c_int64, [P, ctypes.c_char_p]),
+    "ishz_gguf_tensor_info": (I, [P, ctypes.c_int64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(I),
+                                  ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(U32),
+                                  ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
+    "ishz_gguf_tensor_data": (P, [P, ctypes.c_int64]),
+    "ishz_gguf_tensor_upload": (I, [P, ctypes.c_int64, P, SZ, P]),
+    "ishz_gguf_kv_count": (ctypes.c_int64, [P]),
+    "ishz_gguf_kv_key": (ctypes.c_char_p, [P, ctypes.c_int64]),
+    "ishz_gguf_find_kv": (ctypes.c_int64, [P, ctypes.c_char_p]),
+    "ishz_gguf_kv_value": (P, [P, ctypes.c_int64]),
+    "ishz_gguf_value_type": (I, [P]),
+    "ishz_gguf_value_len": (ctypes.c_int64, [P]),
+    "ishz_gguf_value_elem": (P, [P, ctypes.c_int64]),
+    "ishz_gguf_value_int": (I, [P, ctypes.POINTER(ctypes.c_int64)]),
+    "ishz_gguf_value_float": (I, [P, ctypes.POINTER(ctypes.c_double)]),
+    "ishz_gguf_value_bool": (I, [P, ctypes.POINTER(I)]),
+    "ishz_gguf_value_string": (I, [P, ctypes.POINTER(P), ctypes.POINTER(SZ)]),
+    "ishz_gguf_value_raw": (I, [P, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_int64),
+                                ctypes.POINTER(ctypes.c_double)]),
 }
 
 _lib = None

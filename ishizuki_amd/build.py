@@ -1,6 +1,7 @@
 """Builds libishizuki_hip.so (the C-ABI HIP library) in-tree for gfx950 with hipcc.
 
-Every .hip file under csrc/ is compiled to an object in parallel, then linked. Flags:
+Every .hip file under csrc/ is compiled with hipcc (and every .cpp, host-only, with g++) to an
+object in parallel, then linked. hipcc flags:
   --offload-arch=gfx950                         CDNA4 only
   -Xclang -target-feature -Xclang -packed-fp32-ops   no packed fp32 instructions
   -O3 -fPIC -std=c++17
@@ -21,9 +22,16 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++20",
          "-Wno-unused-command-line-argument", "-I", os.path.join(HERE, "..", "include")]
 
 
+HOST_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I", "/opt/rocm/include",
+              "-I", os.path.join(HERE, "..", "include")]
+
+
 def _compile(src):
     obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    if src.endswith(".cpp"):  # host-only code (the GGUF reader)
+        cmd = ["g++", *HOST_FLAGS, "-c", src, "-o", obj]
+    else:
+        cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode:
         sys.stderr.write(r.stdout + r.stderr)
@@ -33,7 +41,7 @@ def _compile(src):
 
 def build(verbose=True):
     os.makedirs(OBJ, exist_ok=True)
-    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB + ".tmp"
