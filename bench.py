@@ -10,7 +10,8 @@ holds kernel time, not Python launch overhead.
 
 Also printed (same JSON line, "families"): us/call and GB/s at M = 1 and 8 for every family at
 17408 x 5120 (Q4_0, Q4_K, Q6_K, IQ2_XS, affine g64 + WHT, EXL3 2 bpw), the MoE FFN, and, with
---all, every BASELINE config. cpu_baseline: the CPU oracle (dequantize-then-fp32-dot, OpenMP on
+--all, every BASELINE config and the other GGUF formats (Q2_K, IQ4_XS, IQ2_XXS, IQ2_S, IQ3_XXS,
+IQ3_S, IQ1_S, IQ1_M). cpu_baseline: the CPU oracle (dequantize-then-fp32-dot, OpenMP on
 all host cores) on a bounded row sample of the headline workload.
 """
 import argparse
@@ -183,6 +184,11 @@ def main():
         ("affine2_g64_wht128", lambda M: affine_case(NS, KS, M)),
         ("exl3_2bpw", lambda M: exl3_case(KS, NS, M)),
     ]
+    # the other GGUF formats (--all, or by name in --only)
+    for t in (ggml.Q2_K, ggml.IQ4_XS, ggml.IQ2_XXS, ggml.IQ2_S, ggml.IQ3_XXS, ggml.IQ3_S, ggml.IQ1_S, ggml.IQ1_M):
+        nm = ggml.NAMES[t].lower()
+        if args.all or nm in only:
+            plan.append((nm, lambda M, t=t: ggml_case(t, NS, KS, M)))
     fam_steps = max(50, args.steps // 2)
     for name, b in plan:
         if only and name not in only:

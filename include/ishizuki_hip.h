@@ -32,9 +32,17 @@ enum { ISHZ_DT_F32 = 0, ISHZ_DT_F16 = 1, ISHZ_DT_BF16 = 2 };
 /* GGML storage types, numbered as GGMLType's raw values (Config/GGUFFile.swift:13-43). */
 enum {
   ISHZ_GGML_Q4_0 = 2,
+  ISHZ_GGML_Q2_K = 10,
   ISHZ_GGML_Q4_K = 12,
   ISHZ_GGML_Q6_K = 14,
-  ISHZ_GGML_IQ2_XS = 17
+  ISHZ_GGML_IQ2_XXS = 16,
+  ISHZ_GGML_IQ2_XS = 17,
+  ISHZ_GGML_IQ3_XXS = 18,
+  ISHZ_GGML_IQ1_S = 19,
+  ISHZ_GGML_IQ3_S = 21,
+  ISHZ_GGML_IQ2_S = 22,
+  ISHZ_GGML_IQ4_XS = 23,
+  ISHZ_GGML_IQ1_M = 29
 };
 
 /* Reason for the calling thread's last non-OK status (static storage, never NULL). */
@@ -42,8 +50,9 @@ const char *ishz_last_error(void);
 /* ABI version of this library (major * 100 + minor). */
 int ishz_version(void);
 
-/* GGMLType.blockSize / typeSize (Config/GGUFFile.swift:45-80) for the types this library
-   decodes; 0 for any other type (ishz_ggml_geometry covers every GGMLType). */
+/* GGMLType.blockSize / typeSize (Config/GGUFFile.swift:44-80) for the types this library
+   decodes (GGMLDequant.supported, Core/GGMLDequant.swift:19-24, plus Q4_0); 0 for any other
+   type (ishz_ggml_geometry covers every GGMLType). */
 int ishz_ggml_block_size(uint32_t type);
 int ishz_ggml_type_size(uint32_t type);
 

@@ -7,6 +7,7 @@
 
 #define ISHZ_TABLE_QUAL static __device__
 #include "ggml_grids.inc"
+#include "ggml_iq.h"
 
 namespace ishz {
 
@@ -136,6 +137,87 @@ DEV void decode8(const uint8_t *p, int e, float *v) {
     const uint32_t s = (q >> 9) | (__builtin_popcount(q >> 9) & 1) << 7;
     for (int i = 0; i < 8; i++)
       v[i] = db * (float)((ent >> (8 * i)) & 0xff) * (((s >> i) & 1) ? -1.0f : 1.0f);
+  } else if constexpr (TYPE == ISHZ_GGML_Q2_K) {
+    // weights 128n + 32s + 16 lane + l: bits 2s of qs[32n + 16 lane + l], scale byte 8n + 2s + lane
+    const float d = h2f(ld2(p + 80)), dmin = h2f(ld2(p + 82));
+    const int k = 8 * e, n = k / 128, s = (k / 32) & 3, ln = (k / 16) & 1, l0 = k & 15;
+    const uint8_t sc = p[8 * n + 2 * s + ln];
+    const float dl = d * (float)(sc & 0xf), ml = dmin * (float)(sc >> 4);
+    for (int i = 0; i < 8; i++) v[i] = dl * (float)((p[16 + 32 * n + 16 * ln + l0 + i] >> (2 * s)) & 3) - ml;
+  } else if constexpr (TYPE == ISHZ_GGML_IQ4_XS) {
+    const float d = h2f(ld2(p));
+    const int ib = e / 4, j0 = (e & 1) * 8, hi = (e >> 1) & 1;
+    const int lo = (p[4 + ib / 2] >> (4 * (ib % 2))) & 0xf, hb = ((ld2(p + 2) >> (2 * ib)) & 3) << 4;
+    const float dl = d * (float)((lo | hb) - 32);
+    for (int i = 0; i < 8; i++) {
+      const uint8_t q = p[8 + 16 * ib + j0 + i];
+      v[i] = dl * (float)ishz_kvalues_iq4nl[hi ? q >> 4 : q & 0xf];
+    }
+  } else if constexpr (TYPE == ISHZ_GGML_IQ2_XXS) {
+    const float d = h2f(ld2(p));
+    const int ib = e / 4, l = e & 3;
+    const uint32_t a1 = ld2(p + 2 + 8 * ib) | ld2(p + 4 + 8 * ib) << 16;
+    const uint32_t a2 = ld2(p + 6 + 8 * ib) | ld2(p + 8 + 8 * ib) << 16;
+    const float db = d * (0.5f + (float)(a2 >> 28)) * 0.25f;
+    const uint64_t ent = ishz_iq2xxs_grid[(a1 >> (8 * l)) & 0xff];
+    const uint32_t q7 = (a2 >> (7 * l)) & 127, s = q7 | (__builtin_popcount(q7) & 1) << 7;
+    for (int i = 0; i < 8; i++)
+      v[i] = db * (float)((ent >> (8 * i)) & 0xff) * (((s >> i) & 1) ? -1.0f : 1.0f);
+  } else if constexpr (TYPE == ISHZ_GGML_IQ2_S) {
+    const float d = h2f(ld2(p));
+    const int ib = e / 4, l = e & 3;
+    const uint8_t sc = p[74 + ib];
+    const float db = d * (0.5f + (float)(l < 2 ? (sc & 0xf) : (sc >> 4))) * 0.25f;
+    const int idx = p[2 + 4 * ib + l] | ((p[66 + ib] << (8 - 2 * l)) & 0x300);
+    const uint64_t ent = ishz_iq2s_grid[idx];
+    const uint8_t s = p[34 + 4 * ib + l];
+    for (int i = 0; i < 8; i++)
+      v[i] = db * (float)((ent >> (8 * i)) & 0xff) * (((s >> i) & 1) ? -1.0f : 1.0f);
+  } else if constexpr (TYPE == ISHZ_GGML_IQ3_XXS) {
+    const float d = h2f(ld2(p));
+    const int ib = e / 4, l = e & 3;
+    const uint32_t aux = ld2(p + 66 + 4 * ib) | ld2(p + 68 + 4 * ib) << 16;
+    const float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+    const uint32_t q7 = (aux >> (7 * l)) & 127, s = q7 | (__builtin_popcount(q7) & 1) << 7;
+    const uint32_t g1 = ishz_iq3xxs_grid[p[2 + 8 * ib + 2 * l]], g2 = ishz_iq3xxs_grid[p[3 + 8 * ib + 2 * l]];
+    for (int i = 0; i < 8; i++) {
+      const uint32_t gv = i < 4 ? (g1 >> (8 * i)) & 0xff : (g2 >> (8 * (i - 4))) & 0xff;
+      v[i] = db * (float)gv * (((s >> i) & 1) ? -1.0f : 1.0f);
+    }
+  } else if constexpr (TYPE == ISHZ_GGML_IQ3_S) {
+    const float d = h2f(ld2(p));
+    const int ib = e / 4, l = e & 3;
+    const uint8_t sc = p[106 + ib / 2];
+    const float db = d * (float)(1 + 2 * ((ib & 1) ? (sc >> 4) : (sc & 0xf)));
+    const int qh = p[66 + ib];
+    const uint8_t *qs = p + 2 + 8 * ib;
+    const uint32_t g1 = ishz_iq3s_grid[qs[2 * l] | ((qh << (8 - 2 * l)) & 256)];
+    const uint32_t g2 = ishz_iq3s_grid[qs[2 * l + 1] | ((qh << (7 - 2 * l)) & 256)];
+    const uint8_t s = p[74 + 4 * ib + l];
+    for (int i = 0; i < 8; i++) {
+      const uint32_t gv = i < 4 ? (g1 >> (8 * i)) & 0xff : (g2 >> (8 * (i - 4))) & 0xff;
+      v[i] = db * (float)gv * (((s >> i) & 1) ? -1.0f : 1.0f);
+    }
+  } else if constexpr (TYPE == ISHZ_GGML_IQ1_S) {
+    const float d = h2f(ld2(p));
+    const int ib = e / 4, l = e & 3;
+    const uint32_t qh = ld2(p + 34 + 2 * ib);
+    const float dl = d * (float)(2 * ((qh >> 12) & 7) + 1);
+    const float delta = (qh & 0x8000) ? -0.125f : 0.125f;
+    const uint64_t ent = ishz_iq1s_grid[p[2 + 4 * ib + l] | (((qh >> (3 * l)) & 7) << 8)];
+    for (int i = 0; i < 8; i++) v[i] = dl * ((float)(int8_t)((ent >> (8 * i)) & 0xff) + delta);
+  } else if constexpr (TYPE == ISHZ_GGML_IQ1_M) {
+    const uint32_t s0 = ld2(p + 48), s1 = ld2(p + 50), s2 = ld2(p + 52), s3 = ld2(p + 54);
+    const float d = h2f((s0 >> 12) | ((s1 >> 8) & 0x00f0) | ((s2 >> 4) & 0x0f00) | (s3 & 0xf000));
+    const int ib = e / 4, l = e & 3;
+    const uint32_t w = ld2(p + 48 + 2 * (ib / 2));
+    const int shift = 6 * (ib % 2) + (l < 2 ? 0 : 3);
+    const float dl = d * (float)(2 * ((w >> shift) & 7) + 1);
+    const int qb = p[32 + 2 * ib + (l >> 1)];
+    const int idx = p[4 * ib + l] | (((l & 1) ? (qb >> 4) : qb) & 7) << 8;
+    const float delta = (qb & ((l & 1) ? 0x80 : 0x08)) ? -0.125f : 0.125f;
+    const uint64_t ent = ishz_iq1s_grid[idx];
+    for (int i = 0; i < 8; i++) v[i] = dl * ((float)(int8_t)((ent >> (8 * i)) & 0xff) + delta);
   }
 }
 #pragma clang fp contract(on)
@@ -192,21 +274,28 @@ __global__ __launch_bounds__(256) void gather_kernel(const int32_t *__restrict__
 }
 
 // ----------------------------------------------------------------------------- host
+// The types with a GPU decoder (GGMLDequant.supported, Core/GGMLDequant.swift:19-24, plus Q4_0).
+#define ISHZ_GGML_FORMATS(X)                                                                     \
+  X(ISHZ_GGML_Q4_0, FQ4_0) X(ISHZ_GGML_Q4_K, FQ4_K) X(ISHZ_GGML_Q6_K, FQ6_K) X(ISHZ_GGML_IQ2_XS, FIQ2_XS) \
+  ISHZ_GGML_QUARTER_FORMATS(X)
+#define ISHZ_GGML_QUARTER_FORMATS(X)                                                             \
+  X(ISHZ_GGML_Q2_K, FQ2_K) X(ISHZ_GGML_IQ4_XS, FIQ4_XS) X(ISHZ_GGML_IQ2_XXS, FIQ2_XXS)           \
+  X(ISHZ_GGML_IQ2_S, FIQ2_S) X(ISHZ_GGML_IQ3_XXS, FIQ3_XXS) X(ISHZ_GGML_IQ3_S, FIQ3_S)          \
+  X(ISHZ_GGML_IQ1_S, FIQ1_S) X(ISHZ_GGML_IQ1_M, FIQ1_M)
+
 static int block_size(uint32_t t) {
   switch (t) {
-  case ISHZ_GGML_Q4_0: return FQ4_0::BS;
-  case ISHZ_GGML_Q4_K: return FQ4_K::BS;
-  case ISHZ_GGML_Q6_K: return FQ6_K::BS;
-  case ISHZ_GGML_IQ2_XS: return FIQ2_XS::BS;
+#define X(T, F) case T: return F::BS;
+    ISHZ_GGML_FORMATS(X)
+#undef X
   default: return 0;
   }
 }
 static int type_size(uint32_t t) {
   switch (t) {
-  case ISHZ_GGML_Q4_0: return FQ4_0::TS;
-  case ISHZ_GGML_Q4_K: return FQ4_K::TS;
-  case ISHZ_GGML_Q6_K: return FQ6_K::TS;
-  case ISHZ_GGML_IQ2_XS: return FIQ2_XS::TS;
+#define X(T, F) case T: return F::TS;
+    ISHZ_GGML_FORMATS(X)
+#undef X
   default: return 0;
   }
 }
@@ -273,6 +362,17 @@ static int verify(const void *x, int M, int K, const void *w, int N, void *y, hi
   return launch_verify<F, 1>(x, M, K, w, N, y, st);
 }
 
+// The quarter-block formats: K is always a multiple of 256 (their block), so M = 1 is the
+// streaming GEMV and M >= 2 the streaming MFMA kernel.
+template <class F>
+static int quarter(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st) {
+  if (M == 1) {
+    const typename F::Args a{(const uint8_t *)w, (size_t)(K / F::BS) * F::TS, K, N};
+    return launch_gemv<F>(a, x, y, st);
+  }
+  return vgemm<F>(x, M, K, w, N, y, st);
+}
+
 static int check_matmul(uint32_t type, int x_dtype, int M, int lo, int hi, int K,
                         size_t blocks_bytes, int N, const void *x, const void *w, const void *y) {
   const int bs = block_size(type);
@@ -312,6 +412,9 @@ extern "C" int ishz_ggml_matvec(uint32_t type, const void *x, int x_dtype, int M
   case ISHZ_GGML_Q4_K: return verify<FQ4_K>(x, M, K, blocks, N, y, st);
   case ISHZ_GGML_Q6_K: return verify<FQ6_K>(x, M, K, blocks, N, y, st);
   case ISHZ_GGML_IQ2_XS: return verify<FIQ2_XS>(x, M, K, blocks, N, y, st);
+#define X(T, F) case T: return quarter<F>(x, M, K, blocks, N, y, st);
+    ISHZ_GGML_QUARTER_FORMATS(X)
+#undef X
   }
   return decline("unsupported GGML type");
 }
@@ -328,6 +431,9 @@ extern "C" int ishz_ggml_matmul_few(uint32_t type, const void *x, int x_dtype, i
   case ISHZ_GGML_Q4_K: return verify<FQ4_K>(x, M, K, blocks, N, y, st);
   case ISHZ_GGML_Q6_K: return verify<FQ6_K>(x, M, K, blocks, N, y, st);
   case ISHZ_GGML_IQ2_XS: return verify<FIQ2_XS>(x, M, K, blocks, N, y, st);
+#define X(T, F) case T: return quarter<F>(x, M, K, blocks, N, y, st);
+    ISHZ_GGML_QUARTER_FORMATS(X)
+#undef X
   }
   return decline("unsupported GGML type");
 }
@@ -352,10 +458,9 @@ extern "C" int ishz_ggml_dequant(uint32_t type, const void *blocks, size_t block
   if (!blocks || !out) return einval("null pointer");
   hipStream_t st = S(stream);
   switch (type) {
-  case ISHZ_GGML_Q4_0: return dequant_t<ISHZ_GGML_Q4_0, 32, 18>(blocks, count, out, out_dtype, st);
-  case ISHZ_GGML_Q4_K: return dequant_t<ISHZ_GGML_Q4_K, 256, 144>(blocks, count, out, out_dtype, st);
-  case ISHZ_GGML_Q6_K: return dequant_t<ISHZ_GGML_Q6_K, 256, 210>(blocks, count, out, out_dtype, st);
-  case ISHZ_GGML_IQ2_XS: return dequant_t<ISHZ_GGML_IQ2_XS, 256, 74>(blocks, count, out, out_dtype, st);
+#define X(T, F) case T: return dequant_t<T, F::BS, F::TS>(blocks, count, out, out_dtype, st);
+    ISHZ_GGML_FORMATS(X)
+#undef X
   }
   return decline("unsupported GGML type");
 }
@@ -384,10 +489,9 @@ extern "C" int ishz_ggml_gather(uint32_t type, const int32_t *ids, int n_ids, co
   if (!ids || !blocks || !out) return einval("null pointer");
   hipStream_t st = S(stream);
   switch (type) {
-  case ISHZ_GGML_Q4_0: return gather_t<ISHZ_GGML_Q4_0, 32, 18>(ids, n_ids, blocks, n_rows, K, out, out_dtype, st);
-  case ISHZ_GGML_Q4_K: return gather_t<ISHZ_GGML_Q4_K, 256, 144>(ids, n_ids, blocks, n_rows, K, out, out_dtype, st);
-  case ISHZ_GGML_Q6_K: return gather_t<ISHZ_GGML_Q6_K, 256, 210>(ids, n_ids, blocks, n_rows, K, out, out_dtype, st);
-  case ISHZ_GGML_IQ2_XS: return gather_t<ISHZ_GGML_IQ2_XS, 256, 74>(ids, n_ids, blocks, n_rows, K, out, out_dtype, st);
+#define X(T, F) case T: return gather_t<T, F::BS, F::TS>(ids, n_ids, blocks, n_rows, K, out, out_dtype, st);
+    ISHZ_GGML_FORMATS(X)
+#undef X
   }
   return decline("unsupported GGML type");
 }

@@ -46,6 +46,7 @@ DEV void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, int &sc, in
 // What the GEMV skeleton needs from a GGML format: row pointers, unit count and the x staging
 // (x slots in consumption order, per-group sums, i-quant tables).
 DEV void build_iq2xs_tables_perm(u4 *grid, u4 *sgn);
+DEV void build_iq2xs_tables_nat(u4 *grid, u4 *sgn);
 
 template <class D>
 struct GgmlGemv {
@@ -59,7 +60,18 @@ struct GgmlGemv {
   // (fewer, longer waves amortise the x staging every workgroup repeats).
   static int occ(const Args &) { return 2; }
   static __host__ __device__ int units(int K) { return K / D::BS * D::UPB / D::UNIT_BLOCKS; }
-  static size_t extra_lds_bytes(const Args &) { return D::GRID ? (512 + 128) * 16 : 0; }
+  static size_t extra_lds_bytes(const Args &) { return D::tab_bytes(); }
+  // LDS tables (codebooks, sign masks) the decoders index: bytes, and the builder every
+  // workgroup runs once (GEMV: pair-permuted like x; verify: natural order). IQ2_XS's here;
+  // formats with other tables replace all three.
+  static constexpr size_t tab_bytes() { return D::GRID ? (512 + 128) * 16 : 0; }
+  static DEV void gemv_tables(u4 *t) {
+    if constexpr (D::GRID) build_iq2xs_tables_perm(t, t + 512);
+  }
+  static DEV void vtables(u4 *t) {
+    if constexpr (D::VGRID) build_iq2xs_tables_nat(t, t + 512);
+  }
+  static constexpr bool XPERM = true;  // x slots staged pair-permuted (perm0213) or natural
   static DEV auto load(const Args &a, int row, int u) { return D::load_row(a.w + (size_t)row * a.rb, u); }
   // Loads for U slots (US sums) per thread are issued together before any is stored, so
   // staging costs a memory latency per U items rather than one each; the first round's loads
@@ -103,7 +115,7 @@ struct GgmlGemv {
 #pragma unroll
     for (int j = 0; j < U; j++) {
       const int i = i0 + j * (int)blockDim.x;
-      if (i < ns && (i / (16 * D::R)) * 16 + (i & 15) < units) xs[i] = perm0213(v[j]);
+      if (i < ns && (i / (16 * D::R)) * 16 + (i & 15) < units) xs[i] = D::XPERM ? perm0213(v[j]) : v[j];
     }
   }
   static DEV void store_sums(float *xsum, int units, int i0, const u4 (*v)[SLMAX]) {
@@ -141,7 +153,7 @@ struct GgmlGemv {
         store_sums(xsum, units, i0, v);
       }
     }
-    if constexpr (D::GRID) build_iq2xs_tables_perm(extra, extra + 512);
+    D::gemv_tables(extra);
     __syncthreads();
   }
 };

@@ -23,7 +23,7 @@
 //   void vdecode(r, B[8], tabs)      B operands (MFMA b of sub-unit b / (8 / VNS))
 //   void vstage(xrow, j, g, s, A, off1, X)   A words of sub-unit s (8 / VNS of them) and sums
 //   void vscale(r, g, s, sc, mn)     value of sub-unit s = sc * (C - off1) + mn * X
-//   VGRID                            LDS tables (IQ2_XS grid and signs, natural order)
+//   vtables(tabs), tab_bytes()       LDS tables the decoder reads (codebooks, sign masks)
 //   VDEPTH                           steps kept in flight (register ring)
 #pragma once
 #include <algorithm>
@@ -32,8 +32,6 @@
 #include "common.h"
 
 namespace ishz {
-
-DEV void build_iq2xs_tables_nat(u4 *grid, u4 *sgn);
 
 // What is multiplied: a "problem" P supplies, per workgroup row blockIdx.y (a group: the whole
 // matrix, or one routed expert), the token rows of x, the weight rows, and the output writer.
@@ -71,7 +69,7 @@ __global__ __launch_bounds__(64 * NW) void vgemm_kernel(P p, int K, int Kc, int 
   const uint32_t mg = vconst(0x64006400u);
 
   for (int i = threadIdx.x; i < 8; i += blockDim.x) zero[i] = u4{0, 0, 0, 0};
-  if constexpr (F::VGRID) build_iq2xs_tables_nat(tabs, tabs + 512);
+  F::vtables(tabs);
   // A row of this lane: gg = n / 4 (lane group whose k-slot it fills), token tt = n % 4.
   const int gg = n >> 2, tt = n & 3;
   const int count = p.count(gp);
@@ -208,7 +206,7 @@ static size_t vgemm_lds(int Kc, int T) {
   constexpr int MT = 4 * NQ;
   const int cs = Kc / 256;
   return (size_t)MT * (cs * 32 + 1) * 16 + 8 * 16 + (size_t)cs * 4 * F::VNS * 2 * MT * 4 +
-         (T >= NW ? 0 : (size_t)NW * T * NQ * 64 * 4) + (size_t)T * 256 * 4 + (F::VGRID ? (512 + 128) * 16 : 0);
+         (T >= NW ? 0 : (size_t)NW * T * NQ * 64 * 4) + (size_t)T * 256 * 4 + F::tab_bytes();
 }
 
 // Launch over `groups` groups of (up to) `rows` weight rows each; T tiles per workgroup.

@@ -9,9 +9,12 @@ import torch
 from . import _lib
 from ._torch import DTYPES, TORCH, ptr, require_cuda, stream
 
-Q4_0, Q4_K, Q6_K, IQ2_XS = 2, 12, 14, 17
-SUPPORTED = (Q4_0, Q4_K, Q6_K, IQ2_XS)
-NAMES = {Q4_0: "Q4_0", Q4_K: "Q4_K", Q6_K: "Q6_K", IQ2_XS: "IQ2_XS"}
+Q4_0, Q2_K, Q4_K, Q6_K = 2, 10, 12, 14
+IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ3_S, IQ2_S, IQ4_XS, IQ1_M = 16, 17, 18, 19, 21, 22, 23, 29
+NAMES = {Q4_0: "Q4_0", Q2_K: "Q2_K", Q4_K: "Q4_K", Q6_K: "Q6_K", IQ2_XXS: "IQ2_XXS", IQ2_XS: "IQ2_XS",
+         IQ3_XXS: "IQ3_XXS", IQ1_S: "IQ1_S", IQ3_S: "IQ3_S", IQ2_S: "IQ2_S", IQ4_XS: "IQ4_XS", IQ1_M: "IQ1_M"}
+# GGMLDequant.supported (Core/GGMLDequant.swift:19-24) plus Q4_0
+SUPPORTED = tuple(NAMES)
 
 matvec_batch = range(1, 17)     # GGMLKernels.matvecBatch (:146)
 matmul_few_rows = range(2, 9)   # GGMLKernels.matmulFewRows (:217)

@@ -6,10 +6,15 @@ would hold them (numpy arrays), so the same bytes feed the GPU kernels and the C
 """
 import numpy as np
 
-Q4_0, Q4_K, Q6_K, IQ2_XS = 2, 12, 14, 17
-BLOCK = {Q4_0: (32, 18), Q4_K: (256, 144), Q6_K: (256, 210), IQ2_XS: (256, 74)}
-# byte offsets of fp16 super-scales inside a block
-SCALE_AT = {Q4_0: (0,), Q4_K: (0, 2), Q6_K: (208,), IQ2_XS: (0,)}
+Q4_0, Q2_K, Q4_K, Q6_K = 2, 10, 12, 14
+IQ2_XXS, IQ2_XS, IQ3_XXS, IQ1_S, IQ3_S, IQ2_S, IQ4_XS, IQ1_M = 16, 17, 18, 19, 21, 22, 23, 29
+BLOCK = {Q4_0: (32, 18), Q2_K: (256, 84), Q4_K: (256, 144), Q6_K: (256, 210), IQ2_XXS: (256, 66),
+         IQ2_XS: (256, 74), IQ3_XXS: (256, 98), IQ1_S: (256, 50), IQ3_S: (256, 110), IQ2_S: (256, 82),
+         IQ4_XS: (256, 136), IQ1_M: (256, 56)}
+# byte offsets of fp16 super-scales inside a block (IQ1_M spreads its d over the top nibbles of
+# the four scale words at 48..55)
+SCALE_AT = {Q4_0: (0,), Q2_K: (80, 82), Q4_K: (0, 2), Q6_K: (208,), IQ2_XXS: (0,), IQ2_XS: (0,),
+            IQ3_XXS: (0,), IQ1_S: (0,), IQ3_S: (0,), IQ2_S: (0,), IQ4_XS: (0,), IQ1_M: ()}
 
 
 def rng(seed):
@@ -29,6 +34,12 @@ def ggml_blocks(type_, N, K, seed=0, scale=0.01):
     blk = r.integers(0, 256, size=(nb, ts), dtype=np.uint8)
     for off in SCALE_AT[type_]:
         blk[:, off:off + 2] = fp16_absnormal(r, nb, scale).view(np.uint8).reshape(nb, 2)
+    if type_ == IQ1_M:
+        d = fp16_absnormal(r, nb, scale).view(np.uint16).astype(np.uint16)
+        w = blk[:, 48:56].copy().view(np.uint16)  # [nb, 4]
+        for i in range(4):
+            w[:, i] = (w[:, i] & 0x0FFF) | (((d >> (4 * i)) & 0xF) << 12)
+        blk[:, 48:56] = w.view(np.uint8)
     return blk.reshape(-1)
 
 

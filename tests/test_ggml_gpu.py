@@ -14,7 +14,8 @@ from ishizuki_amd import ggml, synth
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
-TYPES = [ggml.Q4_0, ggml.Q4_K, ggml.Q6_K, ggml.IQ2_XS]
+TYPES = list(ggml.SUPPORTED)  # the four headline formats and the quarter-block ones
+QUARTER = [ggml.Q2_K, ggml.IQ4_XS, ggml.IQ2_XXS, ggml.IQ2_S, ggml.IQ3_XXS, ggml.IQ3_S, ggml.IQ1_S, ggml.IQ1_M]
 
 
 def to_bf16_bits(a):
@@ -25,8 +26,9 @@ def to_bf16_bits(a):
     return r
 
 
-@pytest.mark.parametrize("t", [12, 14, 17])
+@pytest.mark.parametrize("t", [10, 12, 14, 16, 17, 18, 19, 21, 22, 23, 29])
 def test_dequant_golden_bit_exact(golden_ggml, t):
+    """The reference's own vectors (ggml-reference.bin) for every type it decodes."""
     b, e = golden_ggml[t]
     out = ggml.dequantize(torch.from_numpy(b).to(DEV), t, (e.size,), dtype=torch.float32)
     assert bits_equal(out.cpu().numpy(), e)
@@ -112,7 +114,7 @@ def test_verify_q4_0_k_not_multiple_of_256(M):
     assert_close(y, ref, what=f"q4_0 K=416 M={M}")
 
 
-@pytest.mark.parametrize("t", [ggml.Q4_K, ggml.Q6_K, ggml.IQ2_XS])
+@pytest.mark.parametrize("t", [ggml.Q4_K, ggml.Q6_K, ggml.IQ2_XS] + QUARTER)
 def test_matmul_few_ragged(t):
     # GGMLKernelTests.matmulFew (:145-175): N = 17, a ragged tile
     for M in range(2, 9):
