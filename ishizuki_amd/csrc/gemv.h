@@ -10,7 +10,11 @@
 // A format F provides: Args (pointers and sizes), Raw (one unit's registers), LaneC (per-lane
 // constants), units(K), load(args, row, u), dot(raw, UnitX, LaneC), stage_load(...) (x loads
 // issued first, kept in an XPre) and stage(...) (fills the LDS slots and sums of x, see UnitX),
-// extra_lds_bytes(args), and R / Q (slots and sums per unit).
+// extra_lds_bytes(args), and R / Q (slots and sums per unit). A format whose rows read different
+// activation vectors (a batch of gathered experts) also provides nx(args), the number of x
+// images (LDS is sized for all of them), xsel(args, row), the image a row reads (uniform over a
+// row group), and a stage taking the first and last image the workgroup's rows read: only those
+// are staged.
 #pragma once
 #include <algorithm>
 #include <cstdlib>
@@ -55,6 +59,16 @@ DEV u2 perm0213(u2 a) {
   return r;
 }
 
+template <class F>
+__host__ __device__ constexpr bool gemv_multi_x() {
+  return requires(const typename F::Args &a) { F::nx(a); };
+}
+template <class F>
+__host__ __device__ int gemv_nx(const typename F::Args &a) {
+  if constexpr (gemv_multi_x<F>()) return F::nx(a);
+  else return 1;
+}
+
 template <class F, int LPR, int B, int D, bool RAGGED>
 __global__ __launch_bounds__(256) void gemv_kernel(typename F::Args args, const uint16_t *__restrict__ x,
                                                    uint16_t *__restrict__ y, int groups_per_wave) {
@@ -63,9 +77,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(typename F::Args args, const 
   const int K = args.K, N = args.N;
   const int units = F::units(K);
   const int ugroups = (units + 15) / 16;
+  const int nx = gemv_nx<F>(args);
   u4 *xs = (u4 *)smem;
-  float *xsum = (float *)(xs + ugroups * 16 * F::R);
-  u4 *extra = (u4 *)(xsum + ugroups * 16 * F::Q);  // format tables / scratch
+  float *xsum = (float *)(xs + nx * ugroups * 16 * F::R);
+  u4 *extra = (u4 *)(xsum + nx * ugroups * 16 * F::Q);  // format tables / scratch
 
   constexpr int RPW = 64 / LPR;
   const int lane = threadIdx.x & 63, wave = wave_id();
@@ -108,18 +123,33 @@ __global__ __launch_bounds__(256) void gemv_kernel(typename F::Args args, const 
     advance(gl, bl);
   }
 
-  F::stage(args, x, xs, xsum, extra, units, pre);  // ends with a barrier
+  int im0 = 0;  // first x image of this workgroup's rows
+  if constexpr (gemv_multi_x<F>()) {
+    const int gfirst = blockIdx.x * (blockDim.x >> 6) * groups_per_wave;
+    const int glast = min(gfirst + (int)(blockDim.x >> 6) * groups_per_wave, (N + RPW - 1) / RPW) - 1;
+    im0 = F::xsel(args, gfirst * RPW);
+    F::stage(args, x, xs, xsum, extra, units, pre, im0, F::xsel(args, min(glast * RPW + RPW - 1, N - 1)));
+  } else {
+    F::stage(args, x, xs, xsum, extra, units, pre);  // ends with a barrier
+  }
   const uint32_t mg = vconst(0x64006400u);
   const u4 *grid = extra, *sgn = extra + F::GRID_ENTRIES;
   const int lane_slot = (sub >> 4) * 16 * F::R + (sub & 15);
   const int lane_sum = (sub >> 4) * 16 * F::Q + (sub & 15);
-  auto view = [&](int bb, int i) {
+  auto view = [&](int gg, int bb, int i) {
+    int xo = 0, so = 0;  // the group's x image
+    if constexpr (gemv_multi_x<F>()) {
+      const int im = F::xsel(args, gg * RPW) - im0;
+      xo = im * ugroups * 16 * F::R;
+      so = im * ugroups * 16 * F::Q;
+    }
     if constexpr (RAGGED) {
       const int u = unit(bb, i);
-      return UnitX{xs + (u >> 4) * 16 * F::R + (u & 15), xsum + (u >> 4) * 16 * F::Q + (u & 15), mg, grid, sgn};
+      return UnitX{xs + xo + (u >> 4) * 16 * F::R + (u & 15), xsum + so + (u >> 4) * 16 * F::Q + (u & 15), mg, grid,
+                   sgn};
     } else {
       const int k = bb * B + i;
-      return UnitX{xs + lane_slot + k * LPR * F::R, xsum + lane_sum + k * LPR * F::Q, mg, grid, sgn};
+      return UnitX{xs + xo + lane_slot + k * LPR * F::R, xsum + so + lane_sum + k * LPR * F::Q, mg, grid, sgn};
     }
   };
 
@@ -128,10 +158,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(typename F::Args args, const 
 #pragma unroll
     for (int i = 0; i < B; i++) {
       if constexpr (RAGGED) {
-        const float v = F::dot(r[i], view(bb, i), lc);
+        const float v = F::dot(r[i], view(gg, bb, i), lc);
         acc += sub + (bb * B + i) * LPR < units ? v : 0.0f;
       } else if ((bb * B + i) * LPR < units) {
-        acc += F::dot(r[i], view(bb, i), lc);
+        acc += F::dot(r[i], view(gg, bb, i), lc);
       }
     }
     if (bb == nb - 1) {
@@ -164,7 +194,7 @@ static int launch_gemv_kd(const typename F::Args &a, const void *x, void *y, hip
   constexpr int RPW = 64 / LPR;
   const int units = F::units(a.K);
   const size_t ug = (size_t)(units + 15) / 16;
-  const size_t lds = ug * 16 * F::R * 16 + ug * 16 * F::Q * 4 + F::extra_lds_bytes(a);
+  const size_t lds = gemv_nx<F>(a) * (ug * 16 * F::R * 16 + ug * 16 * F::Q * 4) + F::extra_lds_bytes(a);
   if (lds > 160 * 1024) return decline("K too large for the GEMV's LDS copy of x");
   auto kern = gemv_kernel<F, LPR, B, D, RAGGED>;
   int per_cu = 0;

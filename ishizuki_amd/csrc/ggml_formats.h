@@ -134,6 +134,22 @@ struct GgmlGemv {
       }
     }
   }
+  // Every slot and sum of one x image, without a pre-issued first round.
+  static DEV void stage_image(const uint16_t *x, u4 *xs, float *xsum, int units) {
+    const int ug = (units + 15) / 16, bd = blockDim.x;
+    for (int i0 = threadIdx.x; i0 < ug * 16 * D::R; i0 += U * bd) {
+      u4 v[U];
+      load_slots(x, units, i0, v);
+      store_slots(xs, units, i0, v);
+    }
+    if constexpr (D::XSUM) {
+      for (int i0 = threadIdx.x; i0 < ug * 16 * D::Q; i0 += US * bd) {
+        u4 v[US][SLMAX];
+        load_sums(x, units, i0, v);
+        store_sums(xsum, units, i0, v);
+      }
+    }
+  }
   static DEV void stage(const Args &a, const uint16_t *x, u4 *xs, float *xsum, u4 *extra, int units,
                         const XPre &pre) {
     const int ug = (units + 15) / 16, bd = blockDim.x;

@@ -6,11 +6,13 @@
 // down(silu(gate(x)) * up(x)), the k outputs weighted and summed in fp32, narrowed once.
 // Activations between stages are fp16 as the reference's gatherQuantizedMM outputs x.dtype.
 //
-// Kernels: route (one workgroup: routing, per-expert pair lists, active-expert list); gate+up
-// (grid over active experts x 16-row tiles of I; the expert's gate and up rows are two MFMA
-// tiles of the same workgroup, tokens gathered through the pair list; SwiGLU in the epilogue);
-// down (active experts x tiles of H); combine (weighted sum per token). Only routed experts'
-// blocks are ever read.
+// Kernels: route + place (one workgroup, a wave per token: top-k by rounds of wave argmax, then
+// per-expert pair lists and the active-expert list). One or two tokens: gate+up and down as
+// gathered GEMVs over every (token, slot) pair (the streaming GEMV skeleton; SwiGLU while
+// staging down's x). More tokens: the streaming MFMA kernel over active experts x tiles (the
+// expert's gate and up rows are two tiles of the same workgroup, tokens gathered through the pair
+// list, SwiGLU in the epilogue), then down likewise. Combine: weighted fp32 sum per token. Only
+// routed experts' blocks are ever read.
 #include <algorithm>
 #include <cstdlib>
 
@@ -27,73 +29,166 @@ struct MoeRoute {
   int32_t *offs;      // [E+1] pair range of expert e in the sorted list
   int32_t *pair_tok;  // [T*k] token of sorted pair
   int32_t *inv;       // [T*k] sorted position of (t, s)
+  int32_t *ids_out;   // optional caller copies of ids / w (null: none)
+  float *w_out;
 };
 
-// Routing ranks each expert against the token's whole logit row (rank = experts with a larger
-// logit, or an equal one at a lower index): the top-k are the experts of rank < k, already in the
-// reference's order (logit descending, ties to the lower index). Softmax max and sum are wave
-// reductions; the top-k probabilities are summed in rank order for the renormalisation.
-DEV float wave_max(float v) {
-  v = fmaxf(v, ISHZ_DPP(v, 0xB1));
-  v = fmaxf(v, ISHZ_DPP(v, 0x4E));
-  v = fmaxf(v, ISHZ_DPP(v, 0x141));
-  v = fmaxf(v, ISHZ_DPP(v, 0x140));
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  return fmaxf(v, __shfl_xor(v, 32, 64));
+
+// Order-preserving unsigned key of a float: larger value, larger key (0 = retired).
+DEV uint32_t okey(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+DEV float from_okey(uint32_t k) {
+  return __builtin_bit_cast(float, (k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
+}
+// One step of an argmax over a 16-lane row: the larger key, then the lower index.
+template <int CTRL>
+DEV void argmax_step(uint32_t &k, int &i) {
+  const uint32_t k2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, CTRL, 0xf, 0xf, true);
+  const int i2 = __builtin_amdgcn_update_dpp(0, i, CTRL, 0xf, 0xf, true);
+  const bool take = k2 > k || (k2 == k && i2 < i);
+  k = take ? k2 : k;
+  i = take ? i2 : i;
+}
+template <int CTRL>
+DEV float row_max_step(float v) {
+  return fmaxf(v, ISHZ_DPP(v, CTRL));
 }
 
-// Routing: one 64-lane workgroup per token, so tokens route in parallel.
-__global__ __launch_bounds__(64) void moe_route_kernel(const float *__restrict__ logits, int T, int E,
-                                                       int k, int normalize, MoeRoute R) {
-  extern __shared__ __align__(16) float rowb[];  // the token's logits, padded to whole float4; then 64 probs
-  const int lane = threadIdx.x, t = blockIdx.x;
-  const int E4 = (E + 3) & ~3;
-  float *pb = rowb + E4;
-  const float *l = logits + (size_t)t * E;
+// LDS a routing row uses: the token's E order keys, then k winners and k probabilities.
+__host__ __device__ inline int route_row_words(int E, int k) { return E + 2 * k; }
+
+// One token's routing by a 16-lane row (MoEBlock.callAsFunction, Text/MoEBlock.swift:124-134):
+// softmax max and sum by row reductions; k rounds of a row-wide argmax (DPP only) over the
+// logits' order keys (larger logit first, ties to the lower index: the order argPartition gives
+// over the probabilities, softmax being strictly increasing), each round retiring its winner.
+// Slot s is the round-s winner, worth exp(l - max) / sum; the renormalisation divides by the
+// slots' sum taken in slot order. Lane r holds experts r, r + 16, ... : in registers when
+// NPL > 0 (E <= 16 NPL; a round is then a register scan), else in `row`'s LDS keys.
+// `row` holds route_row_words(E, k) words of LDS.
+template <int NPL>
+DEV void route_token(const float *__restrict__ l, int E, int k, int normalize, int t, uint32_t *row,
+                     const MoeRoute &R, int32_t *ids_lds) {
+  constexpr int NR = NPL > 0 ? NPL : 1;
+  const int r = threadIdx.x & 15;
+  uint32_t *key = row, *win = row + E;
+  float *pr = (float *)(row + E + k);
+  uint32_t kr[NR];
   float mx = -INFINITY;
-  for (int e = lane; e < E4; e += 64) {
-    const float v = e < E ? l[e] : -INFINITY;  // -inf never ranks above a logit
-    rowb[e] = v;
-    mx = fmaxf(mx, v);
-  }
-  mx = wave_max(mx);
-  float sum = 0.0f;
-  for (int e = lane; e < E; e += 64) sum += expf(rowb[e] - mx);
-  sum = group_sum<64>(sum);
-  __syncthreads();
-  for (int e = lane; e < E; e += 64) {
-    const float v = rowb[e];
-    int rank = 0;
-#pragma unroll 8
-    for (int f = 0; f < E4; f += 4) {
-      const f4 u = *(const f4 *)(rowb + f);
+  if constexpr (NPL > 0) {
 #pragma unroll
-      for (int c = 0; c < 4; c++) rank += (u[c] > v) | ((u[c] == v) & (f + c < e));
+    for (int j = 0; j < NPL; j++) {
+      const int e = r + 16 * j;
+      const float v = e < E ? l[e] : -INFINITY;
+      kr[j] = e < E ? okey(v) : 0u;
+      mx = fmaxf(mx, v);
     }
-    if (rank < k) {
-      R.ids[t * k + rank] = e;
-      pb[rank] = expf(v - mx) / sum;
+  } else {
+    for (int e = r; e < E; e += 16) {
+      const float v = l[e];
+      key[e] = okey(v);
+      mx = fmaxf(mx, v);
     }
   }
-  __syncthreads();
-  float tot = 0.0f;  // rank-order sum of the top-k probabilities
-  for (int s = 0; s < k; s++) tot += pb[s];
-  if (lane < k) {
-    const float p = pb[lane];
-    R.w[t * k + lane] = normalize ? p / tot : p;
+  mx = row_max_step<0xB1>(mx);   // quad_perm [1,0,3,2]
+  mx = row_max_step<0x4E>(mx);   // quad_perm [2,3,0,1]
+  mx = row_max_step<0x141>(mx);  // row_half_mirror
+  mx = row_max_step<0x140>(mx);  // row_mirror
+  float sum = 0.0f;
+  if constexpr (NPL > 0) {
+#pragma unroll
+    for (int j = 0; j < NPL; j++)
+      if (r + 16 * j < E) sum += expf(from_okey(kr[j]) - mx);
+  } else {
+    for (int e = r; e < E; e += 16) sum += expf(from_okey(key[e]) - mx);
   }
+  sum = group_sum<16>(sum);
+  for (int s = 0; s < k; s++) {
+    uint32_t bk = 0;
+    int be = 0x7fffffff;
+    if constexpr (NPL > 0) {
+#pragma unroll
+      for (int j = 0; j < NPL; j++) {  // ascending e: a tie keeps the lower index
+        const bool take = kr[j] > bk;
+        bk = take ? kr[j] : bk;
+        be = take ? r + 16 * j : be;
+      }
+    } else {
+      for (int e = r; e < E; e += 16) {
+        const uint32_t kv = key[e];
+        if (kv > bk) {
+          bk = kv;
+          be = e;
+        }
+      }
+    }
+    argmax_step<0xB1>(bk, be);
+    argmax_step<0x4E>(bk, be);
+    argmax_step<0x141>(bk, be);
+    argmax_step<0x140>(bk, be);
+    if constexpr (NPL > 0) {
+#pragma unroll
+      for (int j = 0; j < NPL; j++) kr[j] = (r + 16 * j == be) ? 0u : kr[j];  // retired
+    }
+    if (r == (be & 15)) {
+      win[s] = (uint32_t)be;
+      pr[s] = __builtin_bit_cast(float, bk);  // the winner's key, for now
+      if constexpr (NPL == 0) key[be] = 0u;   // retired (a lane only reads its own entries)
+    }
+  }
+  // probabilities in parallel, then the slot-order sum every lane forms alike (winners were
+  // written by other lanes of the row: order the wave's LDS accesses)
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  for (int s = r; s < k; s += 16) pr[s] = expf(from_okey(__builtin_bit_cast(uint32_t, pr[s])) - mx) / sum;
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  float tot = 0.0f;
+  for (int s = 0; s < k; s++) tot += pr[s];
+  for (int s = r; s < k; s += 16) {
+    const int id = (int)win[s];
+    const float w = normalize ? pr[s] / tot : pr[s];
+    R.ids[t * k + s] = id;
+    R.w[t * k + s] = w;
+    if (ids_lds) ids_lds[t * k + s] = id;
+    if (R.ids_out) R.ids_out[t * k + s] = id;
+    if (R.w_out) R.w_out[t * k + s] = w;
+  }
+}
+
+// Keys per lane held in registers for E experts (0: keys stay in LDS); MAXE is the largest E
+// kept in registers (the 1024-thread fused kernel keeps the register budget at 128).
+#define ISHZ_ROUTE_NPL(E, MAXE, CALL)             \
+  do {                                            \
+    if ((E) <= 64) CALL(4);                       \
+    else if ((E) <= 128) CALL(8);                 \
+    else if ((E) <= 256) CALL(16);                \
+    else if ((E) <= 512 && MAXE >= 512) CALL(32); \
+    else if ((E) <= 1024 && MAXE >= 1024) CALL(64); \
+    else CALL(0);                                 \
+  } while (0)
+
+// Routing alone: a 16-lane row per token, blockDim / 16 tokens per workgroup.
+__global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict__ logits, int T, int E,
+                                                        int k, int normalize, MoeRoute R) {
+  extern __shared__ uint32_t rrows[];
+  const int rw = threadIdx.x >> 4, t = blockIdx.x * (blockDim.x >> 4) + rw;
+  if (t >= T) return;
+#define ISHZ_CALL(N) route_token<N>(logits + (size_t)t * E, E, k, normalize, t, rrows + rw * route_row_words(E, k), R, nullptr)
+  ISHZ_ROUTE_NPL(E, 1024, ISHZ_CALL);
+#undef ISHZ_CALL
 }
 
 // Pair lists (one workgroup): per-expert counts in LDS, an exclusive prefix over experts by wave
 // 0, then each pair takes the next free position of its expert (the order inside an expert does
 // not affect any result: every pair's rows are computed independently).
-__global__ __launch_bounds__(1024) void moe_place_kernel(int T, int E, int k, MoeRoute R) {
-  extern __shared__ int32_t cnt[];  // E counts, then fill cursors
+DEV void place_pairs(int T, int E, int k, const MoeRoute &R, const int32_t *ids, int32_t *cnt) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int P = T * k;
   for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
   __syncthreads();
-  for (int q = threadIdx.x; q < P; q += blockDim.x) atomicAdd(&cnt[R.ids[q]], 1);
+  for (int q = threadIdx.x; q < P; q += blockDim.x) atomicAdd(&cnt[ids[q]], 1);
   __syncthreads();
   if (wave == 0) {
     int carry = 0, nact = 0;
@@ -123,10 +218,31 @@ __global__ __launch_bounds__(1024) void moe_place_kernel(int T, int E, int k, Mo
   }
   __syncthreads();
   for (int q = threadIdx.x; q < P; q += blockDim.x) {
-    const int pos = atomicAdd(&cnt[R.ids[q]], 1);
+    const int pos = atomicAdd(&cnt[ids[q]], 1);
     R.pair_tok[pos] = q / k;
     R.inv[q] = pos;
   }
+}
+
+__global__ __launch_bounds__(1024) void moe_place_kernel(int T, int E, int k, MoeRoute R) {
+  extern __shared__ int32_t cnt[];  // E counts, then fill cursors
+  place_pairs(T, E, k, R, R.ids, cnt);
+}
+
+// Routing and placement in one workgroup (up to 64 tokens routed at once, a 16-lane row each):
+// one launch instead of two when the rows, the counts and the ids fit in LDS.
+__global__ __launch_bounds__(1024) void moe_route_place_kernel(const float *__restrict__ logits, int T, int E,
+                                                               int k, int normalize, MoeRoute R) {
+  extern __shared__ uint32_t rrows[];  // [rows][route_row_words] , E counts, then the T k ids
+  const int nr = blockDim.x >> 4, rw = threadIdx.x >> 4;
+  int32_t *cnt = (int32_t *)(rrows + nr * route_row_words(E, k)), *ids = cnt + E;
+  for (int t = rw; t < T; t += nr) {
+#define ISHZ_CALL(N) route_token<N>(logits + (size_t)t * E, E, k, normalize, t, rrows + rw * route_row_words(E, k), R, ids)
+    ISHZ_ROUTE_NPL(E, 256, ISHZ_CALL);
+#undef ISHZ_CALL
+  }
+  __syncthreads();
+  place_pairs(T, E, k, R, ids, cnt);
 }
 
 DEV float r16(float v) { return (float)(_Float16)v; }
@@ -214,14 +330,17 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(const uint16_t *__restri
 }
 
 __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__restrict__ o, int H,
-                                                          int T, int k, MoeRoute R,
+                                                          int T, int k, MoeRoute R, bool sorted,
                                                           uint16_t *__restrict__ y) {
   const size_t total = (size_t)T * H;
   for (size_t q = blockIdx.x * (size_t)blockDim.x + threadIdx.x; q < total;
        q += (size_t)gridDim.x * blockDim.x) {
     const int t = (int)(q / H), n = (int)(q % H);
     float acc = 0.0f;
-    for (int s = 0; s < k; s++) acc += h2f(o[(size_t)R.inv[t * k + s] * H + n]) * R.w[t * k + s];
+    for (int s = 0; s < k; s++) {
+      const int q2 = sorted ? R.inv[t * k + s] : t * k + s;  // row of o holding pair (t, s)
+      acc += h2f(o[(size_t)q2 * H + n]) * R.w[t * k + s];
+    }
     y[q] = f2h(acc);
   }
 }
@@ -299,6 +418,94 @@ struct VMoeDown {
   }
 };
 
+// ------------------------------------------------------------------- gathered GEMV (few tokens)
+// With one or two tokens every routed (token, slot) pair is a GEMV of its own; the streaming
+// GEMV skeleton runs all of them in one launch. Pair p = t k + s (slot order) owns rows
+// p 2I .. p 2I + 2I - 1 (gate rows, then up rows) of the gate/up launch and p H .. p H + H - 1 of
+// the down launch. A row group never straddles two pairs (2I and H are multiples of 256), so the
+// expert id is wave-uniform and read with a scalar load.
+template <class F>
+struct FMoeGateUp : F {
+  struct Args {
+    const uint8_t *gate, *up;
+    size_t rb;
+    int K, N;  // K = H, N = P 2I
+    int I, k;
+    const int32_t *ids;
+  };
+  struct XPre {};
+  static int occ(const Args &) { return 2; }
+  static size_t extra_lds_bytes(const Args &) { return F::tab_bytes(); }
+  static __host__ __device__ int nx(const Args &a) { return a.N / (2 * a.I * a.k); }  // tokens
+  static DEV int xsel(const Args &a, int row) { return row / (2 * a.I * a.k); }
+  static DEV auto load(const Args &a, int row, int u) {
+    const int p = __builtin_amdgcn_readfirstlane(row) / (2 * a.I);
+    const int e = a.ids[p], j = row - p * 2 * a.I;
+    const uint8_t *w = j < a.I ? a.gate + ((size_t)e * a.I + j) * a.rb : a.up + ((size_t)e * a.I + j - a.I) * a.rb;
+    return F::load_row(w, u);
+  }
+  static DEV XPre stage_load(const Args &, const uint16_t *, int) { return {}; }
+  static DEV void stage(const Args &a, const uint16_t *x, u4 *xs, float *xsum, u4 *extra, int units, const XPre &,
+                        int im0, int im1) {
+    const int ug = (units + 15) / 16;
+    for (int t = im0; t <= im1; t++)
+      F::stage_image(x + (size_t)t * a.K, xs + (t - im0) * ug * 16 * F::R, xsum + (t - im0) * ug * 16 * F::Q, units);
+    F::gemv_tables(extra);
+    __syncthreads();
+  }
+};
+
+// down: x of pair p is h = silu(gate) * up of its gate/up rows (fp16 ops, as the reference's
+// elementwise SwiGLU on fp16 activations), formed while staging.
+template <class F>
+struct FMoeDown : F {
+  struct Args {
+    const uint8_t *down;
+    size_t rb;
+    int K, N;  // K = I, N = P H
+    int H;
+    const int32_t *ids;
+  };
+  struct XPre {};
+  static int occ(const Args &) { return 2; }
+  static size_t extra_lds_bytes(const Args &a) { return F::tab_bytes() + (size_t)nx(a) * a.K * 2; }
+  static __host__ __device__ int nx(const Args &a) { return a.N / a.H; }  // pairs
+  static DEV int xsel(const Args &a, int row) { return row / a.H; }
+  static DEV auto load(const Args &a, int row, int u) {
+    const int p = __builtin_amdgcn_readfirstlane(row) / a.H;
+    const int e = a.ids[p];
+    return F::load_row(a.down + ((size_t)e * a.H + (row - p * a.H)) * a.rb, u);
+  }
+  static DEV XPre stage_load(const Args &, const uint16_t *, int) { return {}; }
+  // x = the gate/up outputs [P][2I]; h goes to LDS after the format's tables, then is staged.
+  static DEV void stage(const Args &a, const uint16_t *gu, u4 *xs, float *xsum, u4 *extra, int units, const XPre &,
+                        int im0, int im1) {
+    const int I = a.K, P = im1 - im0 + 1, ug = (units + 15) / 16;
+    F::gemv_tables(extra);
+    uint16_t *hb = (uint16_t *)(extra + F::tab_bytes() / 16);
+    for (int c = threadIdx.x; c < P * I / 8; c += blockDim.x) {
+      const int p = im0 + c / (I / 8), i = (c % (I / 8)) * 8;
+      const u4 g8 = *(const u4 *)(gu + (size_t)p * 2 * I + i), u8 = *(const u4 *)(gu + (size_t)p * 2 * I + I + i);
+      u4 h8;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+          const float g16 = h2f(g8[q] >> (16 * hh)), u16 = h2f(u8[q] >> (16 * hh));
+          const float sg = r16(1.0f / (1.0f + __expf(-g16)));
+          w |= (uint32_t)f2h(r16(g16 * sg) * u16) << (16 * hh);
+        }
+        h8[q] = w;
+      }
+      *(u4 *)(hb + (size_t)(p - im0) * I + i) = h8;
+    }
+    __syncthreads();
+    for (int p = 0; p < P; p++) F::stage_image(hb + (size_t)p * I, xs + p * ug * 16 * F::R, xsum + p * ug * 16 * F::Q, units);
+    __syncthreads();
+  }
+};
+
 // Token quads per pass: an expert receives at most T tokens (one slot per token).
 template <class F, class P>
 static int moe_vgemm(const P &p, int T, int K, int rows, int groups, int tiles_per_wg, hipStream_t st) {
@@ -311,8 +518,19 @@ static int moe_vgemm(const P &p, int T, int K, int rows, int groups, int tiles_p
 }
 
 // ------------------------------------------------------------------- host
+// Standalone routing launch: 16 rows per workgroup, or 4 when a row's LDS is large.
+static int route_launch(const float *logits, int T, int E, int k, int normalize, const MoeRoute &R, hipStream_t st) {
+  const size_t row = (size_t)route_row_words(E, k) * 4;
+  const int rows = 16 * row <= 64 * 1024 ? 16 : 4;
+  if (rows * row > 160 * 1024) return decline("too many experts for one routing workgroup");
+  hipLaunchKernelGGL(moe_route_kernel, dim3((T + rows - 1) / rows), dim3(16 * rows), rows * row, st, logits, T, E, k,
+                     normalize, R);
+  ISHZ_LAUNCH_CHECK("moe route launch");
+  return ISHZ_OK;
+}
+
 struct MoeLayout {
-  size_t ids, w, count, active, offs, pair_tok, inv, h, o, total;
+  size_t ids, w, count, active, offs, pair_tok, inv, h, gu, o, total;
 };
 static MoeLayout moe_layout(int T, int H, int E, int I, int k) {
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
@@ -327,6 +545,7 @@ static MoeLayout moe_layout(int T, int H, int E, int I, int k) {
   L.pair_tok = off; off += al(P * 4);
   L.inv = off; off += al(P * 4);
   L.h = off; off += al(P * I * 2);
+  L.gu = off; off += al(P * 2 * I * 2);
   L.o = off; off += al(P * H * 2);
   L.total = off;
   return L;
@@ -336,7 +555,7 @@ static MoeRoute moe_route_ptrs(void *ws, const MoeLayout &L) {
   uint8_t *b = (uint8_t *)ws;
   return MoeRoute{(int32_t *)(b + L.ids), (float *)(b + L.w), (int32_t *)(b + L.count),
                   (int32_t *)(b + L.active), (int32_t *)(b + L.offs), (int32_t *)(b + L.pair_tok),
-                  (int32_t *)(b + L.inv)};
+                  (int32_t *)(b + L.inv), nullptr, nullptr};
 }
 
 static int ks_for(int tiles, int nblk) {
@@ -347,10 +566,26 @@ static int ks_for(int tiles, int nblk) {
 
 template <class F>
 static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void *gate,
-                   const void *up, const void *down, MoeRoute R, uint16_t *h, uint16_t *o, void *y,
-                   hipStream_t st) {
+                   const void *up, const void *down, MoeRoute R, uint16_t *h, uint16_t *gu, uint16_t *o,
+                   void *y, hipStream_t st) {
   const int amax = std::min(E, T * k);
   static const bool old = getenv("ISHZ_OLD_MOE") != nullptr;
+  const size_t total = (size_t)T * H;
+  // one or two tokens: every (token, slot) pair is a GEMV; two launches of the streaming GEMV
+  if (H % 256 == 0 && I % 256 == 0 && T <= 2 && !old) {
+    const int P = T * k;
+    const typename FMoeGateUp<F>::Args ga{(const uint8_t *)gate, (const uint8_t *)up, (size_t)(H / F::BS) * F::TS,
+                                          H, P * 2 * I, I, k, R.ids};
+    int rc = launch_gemv<FMoeGateUp<F>>(ga, x, gu, st);
+    if (rc) return rc;
+    const typename FMoeDown<F>::Args da{(const uint8_t *)down, (size_t)(I / F::BS) * F::TS, I, P * H, H, R.ids};
+    rc = launch_gemv<FMoeDown<F>>(da, gu, o, st);
+    if (rc) return rc;
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)std::min<size_t>((total + 255) / 256, 4096)), dim3(256), 0,
+                       st, o, H, T, k, R, false, (uint16_t *)y);
+    ISHZ_LAUNCH_CHECK("moe combine launch");
+    return ISHZ_OK;
+  }
   // streaming MFMA kernels from 3 tokens up; one or two tokens (a GEMV per expert) run faster on
   // the per-block kernels below, which start streaming without staging x
   if (H % 256 == 0 && I % 256 == 0 && T > 2 && !old) {
@@ -380,9 +615,8 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
                        st, h, I, (const uint8_t *)down, H, R, o);
     ISHZ_LAUNCH_CHECK("moe down launch");
   }
-  const size_t total = (size_t)T * H;
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)std::min<size_t>((total + 255) / 256, 4096)), dim3(256), 0,
-                     st, o, H, T, k, R, (uint16_t *)y);
+                     st, o, H, T, k, R, true, (uint16_t *)y);
   ISHZ_LAUNCH_CHECK("moe combine launch");
   return ISHZ_OK;
 }
@@ -398,13 +632,10 @@ extern "C" size_t ishz_moe_workspace_size(int T, int H, int E, int I, int topk) 
 extern "C" int ishz_moe_route(const float *logits, int T, int E, int topk, int normalize,
                               int32_t *ids, float *weights, ishz_stream_t stream) {
   if (T <= 0 || E <= 0 || topk <= 0 || topk > E || topk > 64) return decline("bad routing shape");
-  if ((size_t)(E + 3 + 64) * 4 > 64 * 1024) return decline("too many experts for one routing workgroup");
+  if ((size_t)4 * route_row_words(E, topk) * 4 > 160 * 1024) return decline("too many experts for one routing workgroup");
   if (!logits || !ids || !weights) return einval("null pointer");
-  MoeRoute R{ids, weights, nullptr, nullptr, nullptr, nullptr, nullptr};
-  hipLaunchKernelGGL(moe_route_kernel, dim3(T), dim3(64), (size_t)(E + 3 + 64) * 4, S(stream), logits, T, E, topk,
-                     normalize, R);
-  ISHZ_LAUNCH_CHECK("moe route launch");
-  return ISHZ_OK;
+  MoeRoute R{ids, weights, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+  return route_launch(logits, T, E, topk, normalize, R, S(stream));
 }
 
 extern "C" int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T, int H,
@@ -418,7 +649,8 @@ extern "C" int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T,
     return decline("MoE experts must be Q4_0, Q4_K or Q6_K");
   if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
   if (T <= 0 || E <= 0 || topk <= 0 || topk > E || E > 4096) return decline("bad routing shape");
-  if (topk > 64 || (size_t)(E + 3 + 64) * 4 > 64 * 1024) return decline("too many experts for one routing workgroup");
+  if (topk > 64 || (size_t)4 * route_row_words(E, topk) * 4 > 160 * 1024)
+    return decline("too many experts for one routing workgroup");
   if (H <= 0 || I <= 0 || H % bs || I % bs) return decline("H and I must be whole blocks");
   const size_t need = (size_t)I * (H / bs) * ishz_ggml_type_size(type);
   if (expert_bytes < need || (size_t)H * (I / bs) * ishz_ggml_type_size(type) > expert_bytes)
@@ -427,23 +659,25 @@ extern "C" int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T,
   const MoeLayout L = moe_layout(T, H, E, I, topk);
   if (!workspace || workspace_bytes < L.total) return einval("workspace too small (ishz_moe_workspace_size)");
   MoeRoute R = moe_route_ptrs(workspace, L);
+  R.ids_out = ids_out;
+  R.w_out = weights_out;
   hipStream_t st = S(stream);
-  hipLaunchKernelGGL(moe_route_kernel, dim3(T), dim3(64), (size_t)(E + 3 + 64) * 4, st, logits, T, E, topk,
-                     normalize, R);
-  ISHZ_LAUNCH_CHECK("moe route launch");
-  hipLaunchKernelGGL(moe_place_kernel, dim3(1), dim3(1024), (size_t)E * 4, st, T, E, topk, R);
-  ISHZ_LAUNCH_CHECK("moe place launch");
-  uint16_t *h = (uint16_t *)((uint8_t *)workspace + L.h), *o = (uint16_t *)((uint8_t *)workspace + L.o);
-  int rc;
-  switch (type) {
-  case ISHZ_GGML_Q4_K: rc = moe_ffn<FQ4_K>(x, T, H, E, I, topk, gate, up, down, R, h, o, y, st); break;
-  case ISHZ_GGML_Q6_K: rc = moe_ffn<FQ6_K>(x, T, H, E, I, topk, gate, up, down, R, h, o, y, st); break;
-  default: rc = moe_ffn<FQ4_0>(x, T, H, E, I, topk, gate, up, down, R, h, o, y, st); break;
+  const int nr = std::min((T + 3) / 4 * 4, 64);  // routing rows: whole waves, at most 16
+  const size_t fused_lds = ((size_t)nr * route_row_words(E, topk) + E + (size_t)T * topk) * 4;
+  if (fused_lds <= 64 * 1024) {
+    hipLaunchKernelGGL(moe_route_place_kernel, dim3(1), dim3(16 * nr), fused_lds, st, logits, T, E, topk, normalize, R);
+    ISHZ_LAUNCH_CHECK("moe route launch");
+  } else {
+    const int rc = route_launch(logits, T, E, topk, normalize, R, st);
+    if (rc) return rc;
+    hipLaunchKernelGGL(moe_place_kernel, dim3(1), dim3(1024), (size_t)E * 4, st, T, E, topk, R);
+    ISHZ_LAUNCH_CHECK("moe place launch");
   }
-  if (rc) return rc;
-  if (ids_out && hipMemcpyAsync(ids_out, R.ids, (size_t)T * topk * 4, hipMemcpyDeviceToDevice, st) != hipSuccess)
-    return fail("moe ids copy", hipGetLastError());
-  if (weights_out && hipMemcpyAsync(weights_out, R.w, (size_t)T * topk * 4, hipMemcpyDeviceToDevice, st) != hipSuccess)
-    return fail("moe weights copy", hipGetLastError());
-  return ISHZ_OK;
+  uint16_t *h = (uint16_t *)((uint8_t *)workspace + L.h), *o = (uint16_t *)((uint8_t *)workspace + L.o);
+  uint16_t *gu = (uint16_t *)((uint8_t *)workspace + L.gu);
+  switch (type) {
+  case ISHZ_GGML_Q4_K: return moe_ffn<FQ4_K>(x, T, H, E, I, topk, gate, up, down, R, h, gu, o, y, st);
+  case ISHZ_GGML_Q6_K: return moe_ffn<FQ6_K>(x, T, H, E, I, topk, gate, up, down, R, h, gu, o, y, st);
+  default: return moe_ffn<FQ4_0>(x, T, H, E, I, topk, gate, up, down, R, h, gu, o, y, st);
+  }
 }

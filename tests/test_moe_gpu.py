@@ -34,7 +34,27 @@ def test_route_matches_oracle(T):
     assert np.allclose(w.cpu().numpy(), rw, rtol=1e-6, atol=1e-7)
 
 
-@pytest.mark.parametrize("T,type_", [(1, ggml.Q4_K), (5, ggml.Q4_K), (20, ggml.Q4_K), (4, ggml.Q6_K), (3, ggml.Q4_0)])
+@pytest.mark.parametrize("T,E", [(5, 100), (20, 1000), (3, 64)])
+def test_route_ties_and_odd_expert_counts(T, E):
+    """Quantised logits (many exact ties: the lower index wins), E not a multiple of 64, and with
+    E = 1000 the two-kernel route + place path (the fused one needs 17 key rows in LDS)."""
+    r = np.random.default_rng(E + T)
+    logits = (np.round(r.standard_normal((T, E)) * 2) / 2).astype(np.float32)
+    ids, w = moe.route(torch.from_numpy(logits).to(DEV), 8)
+    rid, rw = oracle.moe_route(logits, 8)
+    assert np.array_equal(ids.cpu().numpy(), rid)
+    assert np.allclose(w.cpu().numpy(), rw, rtol=1e-6, atol=1e-7)
+    x = synth.fp16_normal((T, 256), seed=E)
+    (g, u, d), ex = experts(E, 256, 256, seed=E)
+    y, ids2, w2 = moe.swiglu(torch.from_numpy(x).to(DEV), torch.from_numpy(logits).to(DEV), ex, top_k=8,
+                             return_routing=True)
+    assert np.array_equal(ids2.cpu().numpy(), rid)
+    assert np.allclose(w2.cpu().numpy(), rw, rtol=1e-6, atol=1e-7)
+    ref = oracle.moe_swiglu(ggml.Q4_K, x.astype(np.float32), rid, rw, g, u, d, E, 256)
+    assert_close(y.float().cpu().numpy(), ref, what=f"moe ties T={T} E={E}")
+
+
+@pytest.mark.parametrize("T,type_", [(1, ggml.Q4_K), (2, ggml.Q4_K), (2, ggml.Q6_K), (1, ggml.Q4_0), (5, ggml.Q4_K), (20, ggml.Q4_K), (4, ggml.Q6_K), (3, ggml.Q4_0)])
 def test_swiglu_small(T, type_):
     E, H, I, k = 16, 512, 256, 4
     (g, u, d), ex = experts(E, H, I, type_, seed=T)
@@ -61,16 +81,18 @@ def test_swiglu_many_tokens_per_expert():
     assert_close(y.float().cpu().numpy(), ref, what="moe many tokens per expert")
 
 
-def test_swiglu_qwen_shape():
-    # Qwen MoE: 128 experts, hidden 2048, expert intermediate 768, top-8, T = 8
-    E, H, I, k, T = 128, 2048, 768, 8, 8
+@pytest.mark.parametrize("T", [1, 2, 8])
+def test_swiglu_qwen_shape(T):
+    # Qwen MoE: 128 experts, hidden 2048, expert intermediate 768, top-8; T = 1, 2 take the
+    # gathered GEMVs, T = 8 the streaming MFMA kernels
+    E, H, I, k = 128, 2048, 768, 8
     (g, u, d), ex = experts(E, H, I, seed=50)
     x = synth.fp16_normal((T, H), seed=51)
     logits = np.random.default_rng(52).standard_normal((T, E)).astype(np.float32)
     y = moe.swiglu(torch.from_numpy(x).to(DEV), torch.from_numpy(logits).to(DEV), ex, top_k=k)
     rid, rw = oracle.moe_route(logits, k)
     ref = oracle.moe_swiglu(ggml.Q4_K, x.astype(np.float32), rid, rw, g, u, d, E, I)
-    assert_close(y.float().cpu().numpy(), ref, what="moe qwen shape")
+    assert_close(y.float().cpu().numpy(), ref, what=f"moe qwen shape T={T}")
 
 
 def test_declines():
