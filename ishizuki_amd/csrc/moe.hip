@@ -564,6 +564,11 @@ static int ks_for(int tiles, int nblk) {
   return ks;
 }
 
+static bool gathered_gemv(int T, int H, int I) {
+  static const bool old = getenv("ISHZ_OLD_MOE") != nullptr;
+  return H % 256 == 0 && I % 256 == 0 && T <= 2 && !old;
+}
+
 template <class F>
 static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void *gate,
                    const void *up, const void *down, MoeRoute R, uint16_t *h, uint16_t *gu, uint16_t *o,
@@ -572,7 +577,7 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
   static const bool old = getenv("ISHZ_OLD_MOE") != nullptr;
   const size_t total = (size_t)T * H;
   // one or two tokens: every (token, slot) pair is a GEMV; two launches of the streaming GEMV
-  if (H % 256 == 0 && I % 256 == 0 && T <= 2 && !old) {
+  if (gathered_gemv(T, H, I)) {
     const int P = T * k;
     const typename FMoeGateUp<F>::Args ga{(const uint8_t *)gate, (const uint8_t *)up, (size_t)(H / F::BS) * F::TS,
                                           H, P * 2 * I, I, k, R.ids};
@@ -664,7 +669,10 @@ extern "C" int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T,
   hipStream_t st = S(stream);
   const int nr = std::min((T + 3) / 4 * 4, 64);  // routing rows: whole waves, at most 16
   const size_t fused_lds = ((size_t)nr * route_row_words(E, topk) + E + (size_t)T * topk) * 4;
-  if (fused_lds <= 64 * 1024) {
+  if (gathered_gemv(T, H, I)) {  // slot-order ids are all the gathered GEMVs need: no placement
+    const int rc = route_launch(logits, T, E, topk, normalize, R, st);
+    if (rc) return rc;
+  } else if (fused_lds <= 64 * 1024) {
     hipLaunchKernelGGL(moe_route_place_kernel, dim3(1), dim3(16 * nr), fused_lds, st, logits, T, E, topk, normalize, R);
     ISHZ_LAUNCH_CHECK("moe route launch");
   } else {
