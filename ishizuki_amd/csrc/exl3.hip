@@ -273,7 +273,7 @@ __global__ __launch_bounds__(1024) void exl3_mm2(const uint16_t *__restrict__ xh
 template <int KA, int CB, bool MF, int D>
 __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh, int M, int K,
                                                const uint32_t *__restrict__ trellis, int N,
-                                               float *__restrict__ yh, int tk_per_wg) {
+                                               float *__restrict__ yh, int tk_per_wg, int part) {
   using TR = Trellis<KA, false>;
   using T32 = Trellis32<KA, false>;
   constexpr int TN = 32 / KA, W = TR::WORDS;  // TN tiles of W words = 256 words per step
@@ -338,7 +338,7 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
     }
   }
   // partials: sum over the wave's lane groups (M = 1) and over the workgroup's waves in LDS,
-  // then one atomic add per output
+  // then one atomic add per output, or (part) a store into this split's own [M][N] slice
   if constexpr (MF) {
     for (int o = threadIdx.x; o < TN * 256; o += blockDim.x) red[o] = 0.0f;
     __syncthreads();
@@ -350,7 +350,11 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
     for (int o = threadIdx.x; o < TN * 256; o += blockDim.x) {
       const int t = o >> 8, q = (o >> 6) & 3, l = o & 63;
       const int tk = 4 * (l >> 4) + q;
-      if (tk < M) atomicAdd(&yh[(size_t)tk * N + (tn0 + t) * 16 + (l & 15)], red[o]);
+      if (tk < M) {
+        float *dst = yh + (part ? (size_t)blockIdx.y * M * N : 0) + (size_t)tk * N + (tn0 + t) * 16 + (l & 15);
+        if (part) *dst = red[o];
+        else atomicAdd(dst, red[o]);
+      }
     }
   } else {
 #pragma unroll
@@ -364,7 +368,9 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
     for (int o = threadIdx.x; o < TN * 16; o += blockDim.x) {
       float sum = 0.0f;
       for (int v = 0; v < KS; v++) sum += red[(v * TN + (o >> 4)) * 16 + (o & 15)];
-      atomicAdd(&yh[(tn0 + (o >> 4)) * 16 + (o & 15)], sum);
+      float *dst = yh + (part ? (size_t)blockIdx.y * N : 0) + (tn0 + (o >> 4)) * 16 + (o & 15);
+      if (part) *dst = sum;
+      else atomicAdd(dst, sum);
     }
   }
 }
@@ -400,21 +406,34 @@ __global__ __launch_bounds__(256) void exl3_dequant_kernel(const uint32_t *__res
 
 // ------------------------------------------------------------------- 128-point rotation
 // EXL3Kernels.rotate (EXL3.swift:102-124): per 128 block, (x * s if before) -> WHT / sqrt(128)
-// -> (* s if after), fp32, cast to the output dtype. One wave per block, two values per lane.
+// -> (* s if after), fp32, cast to the output dtype. One wave per block, two values per lane. An
+// fp32 input may be nsum back-to-back slices summed first (the matvec's K-split partials).
 __global__ __launch_bounds__(256) void exl3_rotate_kernel(const void *__restrict__ x, int in_dt,
                                                           size_t blocks, int width,
                                                           const uint16_t *__restrict__ scales,
                                                           int before, void *__restrict__ y,
-                                                          int out_dt) {
+                                                          int out_dt, int nsum) {
   const size_t blk = (size_t)blockIdx.x * 4 + wave_id();
   if (blk >= blocks) return;
   const int lane = threadIdx.x & 63;
   const size_t base = blk * 128 + 2 * lane;
   const int col = (int)((blk * 128) % width) + 2 * lane;
   float v0, v1;
-  if (in_dt == ISHZ_DT_F32) {
-    v0 = ((const float *)x)[base];
-    v1 = ((const float *)x)[base + 1];
+  if (in_dt == ISHZ_DT_F32) {  // fp32 input: the sum of nsum slices (K-split partials), in order
+    const size_t slice = blocks * 128;
+    const float *xf = (const float *)x + base;
+    v0 = 0.0f;
+    v1 = 0.0f;
+    for (int s0 = 0; s0 < nsum; s0 += 8) {  // eight slices' loads in flight, summed in order
+      float2 p[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) p[i] = s0 + i < nsum ? *(const float2 *)(xf + (s0 + i) * slice) : float2{0.0f, 0.0f};
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        v0 += p[i].x;
+        v1 += p[i].y;
+      }
+    }
   } else {
     v0 = h2f(((const uint16_t *)x)[base]);
     v1 = h2f(((const uint16_t *)x)[base + 1]);
@@ -517,49 +536,54 @@ extern "C" int ishz_exl3_rotate(const void *x, int in_dtype, int rows, int width
   if (!x || !y || !scales) return einval("null pointer");
   const size_t blocks = (size_t)rows * (width / 128);
   hipLaunchKernelGGL(exl3_rotate_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, S(stream), x,
-                     in_dtype, blocks, width, scales, before, y, out_dtype);
+                     in_dtype, blocks, width, scales, before, y, out_dtype, 1);
   ISHZ_LAUNCH_CHECK("exl3 rotate launch");
   return ISHZ_OK;
 }
 
-extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const int16_t *trellis,
-                                int N, int bits2, int codebook, float *yh, ishz_stream_t stream) {
-  int rc = check_exl3(K, N, bits2, codebook);
-  if (rc) return rc;
-  if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
-  if (M < 1 || M > 16) return decline("row count outside 1..16");
-  if (!xh || !trellis || !yh) return einval("null pointer");
+// K splits of the wide-step kernel: about four workgroups per CU for one row, two with MFMA rows
+// (tn_blocks workgroups per split), at most 64.
+static int exl3_splits(int M, int K, int tn_blocks) {
+  static const int split_env = [] {
+    const char *e = getenv("ISHZ_EXL3_SPLITS");  // tuning
+    return e ? atoi(e) : 0;
+  }();
+  const int tiles_k = K / 16;
+  if (split_env > 0) return std::min(split_env, tiles_k);
+  return std::max(1, std::min({tiles_k / 4, (M == 1 ? 4 : 2) * num_cu_e() / tn_blocks, 64}));
+}
+
+// The matvec. With `part` (a buffer of exl3_splits(..) * M * N floats) the wide-step kernel writes
+// each K split's partial product to its own slice and *nparts says how many; otherwise yh is the
+// result (zeroed, then summed into with atomics) and *nparts = 1.
+static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis, int N, int bits2, int codebook,
+                            float *yh, float *part, int *nparts, hipStream_t st) {
+  *nparts = 1;
   const int wgs = N / 16, tiles_k = K / 16;
   int ks = 1;
   while (ks < 16 && ks < tiles_k && wgs * ks < num_cu_e() * 16) ks *= 2;
   return by_rate(bits2, [&]<int KA, bool HALF>() -> int {
     if constexpr (!HALF && (KA == 1 || KA == 2 || KA == 4)) {
       static const bool mm2 = getenv("ISHZ_EXL3_MM2") != nullptr;
-      if (!getenv("ISHZ_EXL3_OLD") && !mm2) {
-        constexpr int TN = 32 / KA, KS3 = 4, D = 4;
-        const int tn_blocks = N / 16 / TN;  // N % 128 == 0
-        static const int split_env = [] {
-          const char *e = getenv("ISHZ_EXL3_SPLITS");  // tuning
-          return e ? atoi(e) : 0;
-        }();
-        // K splits: about four workgroups per CU for one row, two with MFMA rows (each split adds
-        // one atomic per output and row)
-        const int splits = split_env > 0 ? split_env
-                                         : std::max(1, std::min(tiles_k / KS3, (M == 1 ? 4 : 2) * num_cu_e() / tn_blocks));
-        const int per = (tiles_k + splits - 1) / splits;
+      constexpr int TN = 32 / KA, KS3 = 4, D = 4;  // a step covers TN column tiles: N must tile by them
+      if (!getenv("ISHZ_EXL3_OLD") && !mm2 && (N / 16) % TN == 0) {
+        const int tn_blocks = N / 16 / TN;
+        const int per = (tiles_k + exl3_splits(M, K, tn_blocks) - 1) / exl3_splits(M, K, tn_blocks);
+        const int nsplit = (tiles_k + per - 1) / per;
         const size_t n = (size_t)M * N;
-        hipLaunchKernelGGL(exl3_zero_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 1024)), dim3(256), 0,
-                           S(stream), yh, n);
+        float *out = part ? part : yh;
+        if (part) *nparts = nsplit;
+        else
+          hipLaunchKernelGGL(exl3_zero_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 1024)), dim3(256), 0,
+                             st, yh, n);
         const size_t lds = (size_t)KS3 * 256 * 4 + (M == 1 ? (size_t)KS3 * TN * 16 * 4 : (size_t)TN * 256 * 4);
         auto go = [&]<int CB>() -> int {
           if (M == 1)
-            hipLaunchKernelGGL((exl3_mm3<KA, CB, false, D>), dim3(tn_blocks, (tiles_k + per - 1) / per),
-                               dim3(64 * KS3), lds, S(stream), (const uint16_t *)xh, M, K, (const uint32_t *)trellis,
-                               N, yh, per);
+            hipLaunchKernelGGL((exl3_mm3<KA, CB, false, D>), dim3(tn_blocks, nsplit), dim3(64 * KS3), lds, st,
+                               (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per, part ? 1 : 0);
           else
-            hipLaunchKernelGGL((exl3_mm3<KA, CB, true, D>), dim3(tn_blocks, (tiles_k + per - 1) / per),
-                               dim3(64 * KS3), lds, S(stream), (const uint16_t *)xh, M, K, (const uint32_t *)trellis,
-                               N, yh, per);
+            hipLaunchKernelGGL((exl3_mm3<KA, CB, true, D>), dim3(tn_blocks, nsplit), dim3(64 * KS3), lds, st,
+                               (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per, part ? 1 : 0);
           ISHZ_LAUNCH_CHECK("exl3 matvec launch");
           return ISHZ_OK;
         };
@@ -582,10 +606,10 @@ extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const
           auto launch = [&]<int D>() {
             if (M == 1)
               hipLaunchKernelGGL((exl3_mm2<KA, HALF, CB, false, TN, D>), dim3(N / 16 / TN), dim3(64 * KS2), lds,
-                                 S(stream), (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, yh);
+                                 st, (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, yh);
             else
               hipLaunchKernelGGL((exl3_mm2<KA, HALF, CB, true, TN, D>), dim3(N / 16 / TN), dim3(64 * KS2), lds,
-                                 S(stream), (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, yh);
+                                 st, (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, yh);
           };
           if (cfg % 100 == 4) launch.template operator()<4>();
           else launch.template operator()<8>();
@@ -598,17 +622,31 @@ extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const
     }
     if (M == 1)
       hipLaunchKernelGGL((exl3_mm<KA, HALF, false>), dim3(wgs), dim3(64 * ks), (size_t)ks * 16 * 4,
-                         S(stream), (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, codebook, yh);
+                         st, (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, codebook, yh);
     else
       hipLaunchKernelGGL((exl3_mm<KA, HALF, true>), dim3(wgs), dim3(64 * ks), (size_t)ks * 256 * 4,
-                         S(stream), (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, codebook, yh);
+                         st, (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, codebook, yh);
     ISHZ_LAUNCH_CHECK("exl3 matvec launch");
     return ISHZ_OK;
   });
 }
 
+extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const int16_t *trellis,
+                                int N, int bits2, int codebook, float *yh, ishz_stream_t stream) {
+  int rc = check_exl3(K, N, bits2, codebook);
+  if (rc) return rc;
+  if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
+  if (M < 1 || M > 16) return decline("row count outside 1..16");
+  if (!xh || !trellis || !yh) return einval("null pointer");
+  int np;
+  return exl3_matvec_core(xh, M, K, trellis, N, bits2, codebook, yh, nullptr, &np, S(stream));
+}
+
+// x rotated (fp16), then the matvec's K-split partials (fp32 [splits][M][N], splits bounded by
+// the widest column step of any rate, 32 tiles).
 extern "C" size_t ishz_exl3_workspace_size(int M, int K, int N) {
-  return ((size_t)M * K * 2 + 255) / 256 * 256 + (size_t)M * N * 4;
+  const int most = std::max(1, exl3_splits(M, K, std::max(1, N / 16 / 32)));
+  return ((size_t)M * K * 2 + 255) / 256 * 256 + (size_t)most * M * N * 4;
 }
 
 extern "C" int ishz_exl3_apply(const void *x, int x_dtype, int M, int K, const int16_t *trellis,
@@ -625,6 +663,11 @@ extern "C" int ishz_exl3_apply(const void *x, int x_dtype, int M, int K, const i
   uint16_t *xh = (uint16_t *)workspace;
   float *yh = (float *)((uint8_t *)workspace + ((size_t)M * K * 2 + 255) / 256 * 256);
   if ((rc = ishz_exl3_rotate(x, ISHZ_DT_F16, M, K, suh, 1, xh, ISHZ_DT_F16, stream))) return rc;
-  if ((rc = ishz_exl3_matvec(xh, ISHZ_DT_F16, M, K, trellis, N, bits2, codebook, yh, stream))) return rc;
-  return ishz_exl3_rotate(yh, ISHZ_DT_F32, M, N, svh, 0, y, ISHZ_DT_F16, stream);
+  int np = 1;
+  if ((rc = exl3_matvec_core(xh, M, K, trellis, N, bits2, codebook, yh, yh, &np, S(stream)))) return rc;
+  const size_t blocks = (size_t)M * (N / 128);  // output rotation, summing the K-split partials
+  hipLaunchKernelGGL(exl3_rotate_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, S(stream), yh,
+                     ISHZ_DT_F32, blocks, N, svh, 0, y, ISHZ_DT_F16, np);
+  ISHZ_LAUNCH_CHECK("exl3 rotate launch");
+  return ISHZ_OK;
 }

@@ -71,7 +71,7 @@ __host__ __device__ int gemv_nx(const typename F::Args &a) {
 
 template <class F, int LPR, int B, int D, bool RAGGED>
 __global__ __launch_bounds__(256) void gemv_kernel(typename F::Args args, const uint16_t *__restrict__ x,
-                                                   uint16_t *__restrict__ y, int groups_per_wave) {
+                                                   uint16_t *__restrict__ y, int nwaves) {
   static_assert(LPR % 16 == 0, "lanes per row must be a multiple of 16");
   extern __shared__ __align__(16) uint32_t smem[];
   const int K = args.K, N = args.N;
@@ -87,7 +87,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(typename F::Args args, const 
   const int sub = lane % LPR, rg = lane / LPR;
   const int nb = (units + B * LPR - 1) / (B * LPR);  // batches per row
   const int gw = blockIdx.x * (blockDim.x >> 6) + wave;
-  const int g_end = min((gw + 1) * groups_per_wave, (N + RPW - 1) / RPW);
+  // wave gw of nwaves owns row groups [gw G / nwaves, (gw + 1) G / nwaves): every wave, and so
+  // every CU of a full round, gets the same share to within one group
+  const int G = (N + RPW - 1) / RPW;
+  auto gstart = [&](int w) { return (int)((long long)min(w, nwaves) * G / nwaves); };
+  const int g_end = gstart(gw + 1);
   const int g_last = max(g_end - 1, 0);
   const typename F::LaneC lc = F::lane(sub);
 
@@ -107,7 +111,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(typename F::Args args, const 
   // i + D - 1 is issued into the slot batch i - 1 freed. Load and consume cursors (group,
   // batch-in-row) advance in step. x's first staging loads go out before the weight batches:
   // the memory counter is in order, so staging then waits only for x.
-  const int g0 = gw * groups_per_wave;
+  const int g0 = gstart(gw);
   auto advance = [&](int &gg, int &bb) {
     if (++bb == nb) {
       bb = 0;
@@ -125,8 +129,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(typename F::Args args, const 
 
   int im0 = 0;  // first x image of this workgroup's rows
   if constexpr (gemv_multi_x<F>()) {
-    const int gfirst = blockIdx.x * (blockDim.x >> 6) * groups_per_wave;
-    const int glast = min(gfirst + (int)(blockDim.x >> 6) * groups_per_wave, (N + RPW - 1) / RPW) - 1;
+    const int gfirst = gstart(blockIdx.x * (blockDim.x >> 6));
+    const int glast = max(gstart((blockIdx.x + 1) * (blockDim.x >> 6)) - 1, gfirst);
     im0 = F::xsel(args, gfirst * RPW);
     F::stage(args, x, xs, xsum, extra, units, pre, im0, F::xsel(args, min(glast * RPW + RPW - 1, N - 1)));
   } else {
@@ -203,10 +207,9 @@ static int launch_gemv_kd(const typename F::Args &a, const void *x, void *y, hip
   const int groups = (a.N + RPW - 1) / RPW;
   const int occ = gemv_occ_override() > 0 ? gemv_occ_override() : F::occ(a);
   const int capacity = gemv_num_cu() * 4 * std::min(occ, per_cu);
-  const int per_wave = (groups + capacity - 1) / capacity;
-  const int waves = (groups + per_wave - 1) / per_wave;
+  const int waves = std::min(capacity, groups);  // one resident round, groups spread evenly
   hipLaunchKernelGGL(kern, dim3((waves + 3) / 4), dim3(256), lds, st, a, (const uint16_t *)x, (uint16_t *)y,
-                     per_wave);
+                     waves);
   ISHZ_LAUNCH_CHECK("gemv launch");
   return ISHZ_OK;
 }

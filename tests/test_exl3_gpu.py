@@ -61,6 +61,34 @@ def test_matvec(M, bits2, cb):
     assert_close(y.cpu().numpy(), ref, what=f"exl3 matvec M={M} bits2={bits2} cb={cb}")
 
 
+@pytest.mark.parametrize("M", [1, 3])
+@pytest.mark.parametrize("bits2,N", [(2, 384), (4, 384), (2, 640), (8, 128)])
+def test_matvec_n_not_a_multiple_of_the_wide_step(M, bits2, N):
+    """The wide-step kernel covers 32 / bits column tiles per step (512 columns at 1 bpw, 256 at
+    2 bpw): other N take the general kernel, and every column is computed."""
+    K = 512
+    t, _, _, ten = make(K, N, bits2, 0, seed=N + bits2 + M)
+    xh = synth.fp16_normal((M, K), seed=M)
+    ref = xh.astype(np.float32) @ oracle.exl3_dequant(t, bits2, 0)
+    y = exl3.matvec(torch.from_numpy(xh).to(DEV), ten)
+    assert y is not None
+    assert_close(y.cpu().numpy(), ref, what=f"exl3 matvec bits2={bits2} N={N} M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 8])
+@pytest.mark.parametrize("bits2,N", [(2, 640), (4, 1024)])
+def test_apply_split_partials(M, bits2, N):
+    """apply sums the matvec's K-split partial slices in the output rotation; K = 5120 gives
+    several splits."""
+    K = 5120
+    t, suh, svh, ten = make(K, N, bits2, 0, seed=M + N)
+    x = synth.fp16_normal((M, K), seed=M + 3)
+    ref = oracle.exl3_apply(x.astype(np.float32), t, suh, svh, bits2, 0)
+    y = exl3.apply(torch.from_numpy(x).to(DEV), ten)
+    assert y is not None
+    assert_close(y.float().cpu().numpy(), ref, what=f"exl3 apply split bits2={bits2} N={N} M={M}")
+
+
 @pytest.mark.parametrize("M", [1, 4, 8])
 def test_apply_matches_oracle(M):
     K, N = 5120, 1024
