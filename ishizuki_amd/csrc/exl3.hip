@@ -168,6 +168,19 @@ DEV uint32_t exl3_decode2(uint32_t sa, uint32_t sb) {
   }
 }
 
+// 3INST / MCG image of one state as the two fp16 halves whose sum is the weight (exl3_decode
+// before its final add). A GEMV lane dots them against (x, x): the halves meet x in fp32, so the
+// weight's fp16 rounding of their sum is skipped (a difference of at most half an fp16 ulp per
+// weight, inside the matmul tolerance; dequantization keeps the exact decode).
+template <int CB>
+DEV uint32_t exl3_halves(uint32_t s) {
+  static_assert(CB != 2, "MUL1 decodes to one fp16 directly");
+  const uint32_t v = CB == 1 ? s * 0xCBAC1FEDu : s * 89226354u + 64248484u;
+  return (v & 0x8fff8fffu) ^ 0x3b603b60u;
+}
+DEV uint32_t dup_lo(uint32_t p) { return __builtin_amdgcn_perm(p, p, 0x01000100u); }
+DEV uint32_t dup_hi(uint32_t p) { return __builtin_amdgcn_perm(p, p, 0x03020302u); }
+
 template <int KA, bool HALF, int CB, bool MF, int TN, int D>
 __global__ __launch_bounds__(1024) void exl3_mm2(const uint16_t *__restrict__ xh, int M, int K,
                                                 const uint32_t *__restrict__ trellis, int N,
@@ -319,6 +332,14 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
       load(i + D - 1, ring[(d + D - 1) % D]);
       const Raw &r = ring[d];
       *(u4 *)(stage + 4 * lane) = r.w;  // the wave's own buffer: its LDS operations stay in order
+      constexpr bool HALVES = !MF && CB != 2;
+      uint32_t xd[4];  // (x, x) pairs for the halves form
+      if constexpr (HALVES) {
+        xd[0] = dup_lo(r.xa);
+        xd[1] = dup_hi(r.xa);
+        xd[2] = dup_lo(r.xb);
+        xd[3] = dup_hi(r.xb);
+      }
 #pragma unroll
       for (int t = 0; t < TN; t++) {
         const uint32_t w0 = stage[t * W + wn.ja], w1 = stage[t * W + wn.jb];
@@ -327,6 +348,13 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
         const uint32_t s1 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(1), 16);
         const uint32_t s2 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(2), 16);
         const uint32_t s3 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(3), 16);
+        if constexpr (HALVES) {
+          float a = dot2(exl3_halves<CB>(s0), xd[0], acc[t]);
+          a = dot2(exl3_halves<CB>(s1), xd[1], a);
+          a = dot2(exl3_halves<CB>(s2), xd[2], a);
+          acc[t] = dot2(exl3_halves<CB>(s3), xd[3], a);
+          continue;
+        }
         const uint32_t b01 = exl3_decode2<CB>(s0, s1), b23 = exl3_decode2<CB>(s2, s3);
         if constexpr (MF) {
           const u2 A = live ? u2{r.xa, r.xb} : u2{0, 0};
