@@ -35,11 +35,107 @@ def parse():
     ap.add_argument("--all", action="store_true", help="every BASELINE config, not just 17408x5120")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of family names to run (debug)")
+    ap.add_argument("--policy", action="store_true",
+                    help="measure the row-count dispatch policy (VerifyMatmul.minimumRows, ggmlApply's "
+                         "row ranges) instead of the benchmark")
     return ap.parse_args()
+
+
+def policy():
+    """Row-count dispatch re-measured on MI355X (one JSON line).
+
+    affine (VerifyMatmul.minimumRows, Core/VerifyMatmul.swift:19-26): per weight size, us for one
+    M-row verify call vs M one-row GEMV calls; minimum_rows = fewest rows (2..8) where the verify
+    call wins. GGUF Q4_K (ggmlApply, Core/Hadamard.swift:145-178): us for one matvec call with M
+    rows (M <= 16), for ceil(M/16) 16-row calls, and for dequantize + fp16 GEMM (hipBLAS through
+    torch.matmul); crossover = fewest rows where the dense path wins. Weights are uniform random
+    codes made on the device (timing does not depend on their values)."""
+    import numpy as np
+    import torch
+
+    from ishizuki_amd import _lib
+    from ishizuki_amd._torch import ptr
+
+    L = _lib.lib()
+    dev = torch.device("cuda:0")
+    st = lambda: torch.cuda.current_stream().cuda_stream
+
+    def us(fn, reps=40):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000 / reps
+
+    out = {"metric": "row-count dispatch policy on MI355X", "affine": [], "q4_k": []}
+    g = torch.Generator(device=dev).manual_seed(5)
+    for name, N, K in (("attn k/v", 1024, 5120), ("6144-wide", 6144, 5120), ("mlp", 17408, 5120),
+                       ("output head", 248320, 5120)):
+        codes = torch.randint(-2**31, 2**31 - 1, (N, K // 16), dtype=torch.int32, device=dev, generator=g)
+        sc = (torch.rand((N, K // 64), device=dev, generator=g) * 0.02).half()
+        bi = -sc
+        x = torch.randn((8, K), device=dev, generator=g).half()
+        y = torch.empty((8, N), device=dev, dtype=torch.half)
+        call = lambda M: L.ishz_affine_matmul(ptr(x), 1, M, K, ptr(codes), ptr(sc), ptr(bi), 1, N, 2, 64, ptr(y), st())
+        one = us(lambda: call(1))
+        row = {"shape": f"{N}x{K}", "what": name, "weight_bytes": codes.numel() * 4 + sc.numel() * 4,
+               "gemv_us": round(one, 2), "verify_us": {}}
+        mr = None
+        for M in range(2, 9):
+            if call(M) != 0:  # declined: no time to report
+                row["verify_us"][M] = None
+                continue
+            t = us(lambda: call(M))
+            row["verify_us"][M] = round(t, 2)
+            if mr is None and t < M * one:
+                mr = M
+        row["minimum_rows"] = mr
+        out["affine"].append(row)
+        del codes, sc, bi
+    for name, N, K in (("attn k/v", 1024, 5120), ("mlp up", 25600, 5120), ("mlp down", 5120, 25600)):
+        nb = N * (K // 256) * 144
+        blk = torch.randint(0, 256, (nb,), dtype=torch.uint8, device=dev, generator=g)
+        blk.view(-1, 144)[:, :4] = torch.tensor([0x1f, 0x1c, 0x1f, 0x1c], dtype=torch.uint8, device=dev)  # d, dmin ~ 0.005
+        x = torch.randn((64, K), device=dev, generator=g).half()
+        y = torch.empty((64, N), device=dev, dtype=torch.half)
+        wd = torch.empty((N, K), device=dev, dtype=torch.half)
+        mv = lambda M, r0=0: L.ishz_ggml_matvec(12, ptr(x[r0:]), 1, M, K, ptr(blk), nb, N, ptr(y[r0:]), st())
+
+        def chunks(M):
+            for r0 in range(0, M, 16):
+                mv(min(16, M - r0), r0)
+
+        def dense(M):
+            L.ishz_ggml_dequant(12, ptr(blk), nb, N * K, ptr(wd), 1, st())
+            torch.matmul(x[:M], wd.t(), out=y[:M])
+
+        row = {"shape": f"{N}x{K}", "what": name, "weight_bytes": nb, "matvec_us": {}, "chunks16_us": {},
+               "dense_us": {}}
+        cross = None
+        for M in (1, 2, 4, 8, 12, 16, 24, 32, 48, 64):
+            if M <= 16:
+                row["matvec_us"][M] = round(us(lambda: mv(M)), 2)
+            tc = us(lambda: chunks(M))
+            td = us(lambda: dense(M))
+            row["chunks16_us"][M] = round(tc, 2)
+            row["dense_us"][M] = round(td, 2)
+            if cross is None and td < tc:
+                cross = M
+        row["dense_from_rows"] = cross
+        out["q4_k"].append(row)
+        del blk, wd
+    print(json.dumps(out))
 
 
 def main():
     args = parse()
+    if args.policy:
+        return policy()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the kernels shard by "
               "output rows; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)

@@ -13,14 +13,14 @@ supported_rows = range(2, 9)   # VerifyMatmul.supportedRows (:12)
 
 
 def minimum_rows(nbytes):
-    """VerifyMatmul.minimumRows (Core/VerifyMatmul.swift:19-26), a dispatch policy."""
-    if nbytes >= 100_000_000:
-        return 2
-    if nbytes >= 10_000_000:
-        return 3
-    if nbytes >= 5_000_000:
-        return 4
-    return 6
+    """VerifyMatmul.minimumRows (Core/VerifyMatmul.swift:19-26), re-measured on MI355X.
+
+    The reference's thresholds (2 rows from 100 MB, 3 from 10 MB, 4 from 5 MB, else 6) are where
+    its verify kernel beats MLX's per-row path on an M1 Max. Here the alternative is M one-row
+    GEMV calls, and one M-row verify call is faster from M = 2 at every size measured (1.6 MB
+    attention k/v to the 397 MB vocabulary head, `python bench.py --policy`), so the minimum is 2.
+    """
+    return 2
 
 
 def hadamard_rotate(x, block, signs=None, inverse=False):

@@ -707,7 +707,9 @@ static int affine_vgemm_launch(const void *x, int M, int K, const uint32_t *code
   using F = FAffine<GS, BF16S>;
   constexpr int D = 4;
   const int ntiles = (N + 15) / 16;
-  const int T = (ntiles + num_cu_aff() - 1) / num_cu_aff();  // tiles per workgroup: one round of CUs
+  // tiles per workgroup: one round of CUs, at most 16 / NQ (the waves' per-tile partials live in
+  // LDS: a very wide output, such as a vocabulary head, takes several rounds instead)
+  const int T = std::min((ntiles + num_cu_aff() - 1) / num_cu_aff(), std::max(1, 16 / NQ));
   const int wgs = (ntiles + T - 1) / T;
   constexpr int NW = 8;  // waves per workgroup: two per SIMD, so one issues while the other waits
   const size_t fixed = 128 * 16 + (size_t)NW * T * NQ * 64 * 4;

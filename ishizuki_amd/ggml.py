@@ -84,3 +84,31 @@ def gather(ids, blocks, type_, input_dim, dtype=torch.bfloat16, rows=None):
     rc = _lib.lib().ishz_ggml_gather(type_, ptr(ids), ids.numel(), ptr(blocks), nbytes, rows,
                                      input_dim, ptr(out), DTYPES.get(dtype, -1), stream())
     return out if _lib.check(rc, "ggml_gather") else None
+
+
+def dense_from_rows(nbytes):
+    """Fewest rows at which dequantize + fp16 GEMM beats 16-row streaming passes (measured on
+    MI355X with Q4_K, `python bench.py --policy`: 32 rows for a 2.9 MB attention projection, 48
+    for the 74 MB MLP projections)."""
+    return 32 if nbytes < 10_000_000 else 48
+
+
+def apply(h, blocks, type_, output_dim):
+    """PackedLinear.ggmlApply (Core/Hadamard.swift:145-178) with the row policy re-measured on
+    MI355X: up to 16 rows is one matvec call (the reference splits 5..16 rows into matmulFew calls
+    of 8; here the matvec's MFMA path already decodes each weight once for all 16); more rows are
+    16-row calls until the dense path pays, then the weight is expanded once and multiplied."""
+    shape = h.shape
+    x = h.reshape(-1, shape[-1])
+    rows, K = x.shape
+    if rows <= 16:
+        y = matvec(x, blocks, type_, output_dim)
+    elif rows < dense_from_rows(blocks.numel()):
+        parts = [matvec(x[r:r + 16], blocks, type_, output_dim) for r in range(0, rows, 16)]
+        y = None if any(p is None for p in parts) else torch.cat(parts, 0)
+    else:
+        w = dequantize(blocks, type_, (output_dim, K), dtype=x.dtype)
+        y = None if w is None else x @ w.t()
+    if y is None:
+        return None
+    return y.reshape(*shape[:-1], output_dim)

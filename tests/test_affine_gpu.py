@@ -62,6 +62,17 @@ def test_affine_matmul(M, group):
     assert_close(y.float().cpu().numpy(), ref, what=f"affine M={M} g={group}")
 
 
+@pytest.mark.parametrize("M", [5, 8, 16])
+def test_affine_verify_very_wide_output(M):
+    """40000 output rows (2500 tiles, more than 16 / NQ per CU): the verify kernel runs in several
+    rounds of workgroups rather than declining (the vocabulary-head shape)."""
+    N, K = 40000, 256
+    (x, w, s, b), _, ref = affine_case(N, K, M, 64, seed=M + 100)
+    y = affine.quantized_matmul(x, w, s, b, group_size=64)
+    assert y is not None
+    assert_close(y.float().cpu().numpy(), ref, what=f"affine wide N={N} M={M}")
+
+
 @pytest.mark.parametrize("M", [1, 2, 8])
 @pytest.mark.parametrize("signs_seed", [None, 7])
 def test_affine_rotated_linear(M, signs_seed):

@@ -139,3 +139,16 @@ def test_declines_return_none():
     assert ggml.matvec(x, blk, ggml.Q4_K, 4) is None
     assert ggml.matvec(x[:1].float(), blk, ggml.Q4_K, 4) is None
     assert ggml.matvec(x[:1], blk, ggml.Q4_K, 5) is None   # short buffer
+
+
+@pytest.mark.parametrize("rows", [3, 16, 20, 40])
+def test_apply_row_policy(rows):
+    """PackedLinear.ggmlApply's row policy: one call to 16 rows, 16-row calls, then dequantize +
+    GEMM (40 rows of a small matrix). Same tolerance as the matvec."""
+    N, K = 256, 1024
+    blk = synth.ggml_blocks(ggml.Q4_K, N, K, seed=rows)
+    x = synth.fp16_normal((rows, K), seed=rows + 1)
+    ref = oracle.ggml_matmul(ggml.Q4_K, x.astype(np.float32), blk, N)
+    y = ggml.apply(torch.from_numpy(x).to(DEV), torch.from_numpy(blk).to(DEV), ggml.Q4_K, N)
+    assert y is not None and y.shape == (rows, N)
+    assert_close(y.float().cpu().numpy(), ref, what=f"ggml apply rows={rows}")
