@@ -506,10 +506,16 @@ struct FMoeDown : F {
   }
 };
 
-// Token quads per pass: an expert receives at most T tokens (one slot per token).
+// Quads per pass sized for about twice an expert's expected load (T k / E tokens) plus two;
+// an expert with more tokens takes further passes.
 template <class F, class P>
-static int moe_vgemm(const P &p, int T, int K, int rows, int groups, int tiles_per_wg, hipStream_t st) {
-  switch (std::min(4, (T + 3) / 4)) {
+static int moe_vgemm(const P &p, int T, int E, int k, int K, int rows, int groups, int tiles_per_wg, hipStream_t st) {
+  static const int nq_env = [] {
+    const char *e = getenv("ISHZ_MOE_NQ");  // tuning: token quads per pass
+    return e ? atoi(e) : 0;
+  }();
+  const int want = (2 * T * k / std::max(E, 1) + 2 + 3) / 4;
+  switch (nq_env > 0 ? nq_env : std::max(1, std::min({4, (T + 3) / 4, want}))) {
     case 1: return launch_vgemm_p<F, P, 1>(p, K, rows, groups, tiles_per_wg, st);
     case 2: return launch_vgemm_p<F, P, 2>(p, K, rows, groups, tiles_per_wg, st);
     case 3: return launch_vgemm_p<F, P, 3>(p, K, rows, groups, tiles_per_wg, st);
@@ -605,10 +611,10 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
     };
     const VMoeGateUp gu{(const uint16_t *)x, (const uint8_t *)gate, (const uint8_t *)up,
                         (size_t)(H / F::BS) * F::TS, H, I, R, h};
-    int rc = moe_vgemm<F>(gu, T, H, tiles_gu * 16, amax, pick(tiles_gu, 1), st);
+    int rc = moe_vgemm<F>(gu, T, E, k, H, tiles_gu * 16, amax, pick(tiles_gu, 1), st);
     if (rc) return rc;
     const VMoeDown dn{h, (const uint8_t *)down, (size_t)(I / F::BS) * F::TS, I, H, R, o};
-    rc = moe_vgemm<F>(dn, T, I, H, amax, pick(tiles_dn, 0), st);
+    rc = moe_vgemm<F>(dn, T, E, k, I, H, amax, pick(tiles_dn, 0), st);
     if (rc) return rc;
   } else {
     int ks = ks_for((I / 16) * amax, H / F::BS);
