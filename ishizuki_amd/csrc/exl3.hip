@@ -368,13 +368,19 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
   // partials: sum over the wave's lane groups (M = 1) and over the workgroup's waves in LDS,
   // then one atomic add per output, or (part) a store into this split's own [M][N] slice
   if constexpr (MF) {
-    for (int o = threadIdx.x; o < TN * 256; o += blockDim.x) red[o] = 0.0f;
-    __syncthreads();
+    // the waves add their tiles into LDS one after another (fixed order, no atomics)
+    for (int v = 0; v < KS; v++) {
+      if (wave == v) {
 #pragma unroll
-    for (int t = 0; t < TN; t++)
+        for (int t = 0; t < TN; t++)
 #pragma unroll
-      for (int q = 0; q < 4; q++) atomicAdd(&red[(t * 4 + q) * 64 + lane], acc[t][q]);
-    __syncthreads();
+          for (int q = 0; q < 4; q++) {
+            float &r = red[(t * 4 + q) * 64 + lane];
+            r = v == 0 ? acc[t][q] : r + acc[t][q];
+          }
+      }
+      __syncthreads();
+    }
     for (int o = threadIdx.x; o < TN * 256; o += blockDim.x) {
       const int t = o >> 8, q = (o >> 6) & 3, l = o & 63;
       const int tk = 4 * (l >> 4) + q;
