@@ -570,9 +570,12 @@ static int ks_for(int tiles, int nblk) {
   return ks;
 }
 
-static bool gathered_gemv(int T, int H, int I) {
+// One or two tokens take the gathered GEMVs when down's LDS (every pair's staged h and x image,
+// about 2 I + 2.9 I bytes per pair) fits; otherwise the per-block kernels.
+static bool gathered_gemv(int T, int H, int I, int k) {
   static const bool old = getenv("ISHZ_OLD_MOE") != nullptr;
-  return H % 256 == 0 && I % 256 == 0 && T <= 2 && !old;
+  const size_t per_pair = (size_t)2 * I + ((size_t)I / 64 + 15) / 16 * 16 * (8 * 16 + 4 * 4);
+  return H % 256 == 0 && I % 256 == 0 && T <= 2 && !old && (size_t)T * k * per_pair <= 144 * 1024;
 }
 
 template <class F>
@@ -583,7 +586,7 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
   static const bool old = getenv("ISHZ_OLD_MOE") != nullptr;
   const size_t total = (size_t)T * H;
   // one or two tokens: every (token, slot) pair is a GEMV; two launches of the streaming GEMV
-  if (gathered_gemv(T, H, I)) {
+  if (gathered_gemv(T, H, I, k)) {
     const int P = T * k;
     const typename FMoeGateUp<F>::Args ga{(const uint8_t *)gate, (const uint8_t *)up, (size_t)(H / F::BS) * F::TS,
                                           H, P * 2 * I, I, k, R.ids};
@@ -675,7 +678,7 @@ extern "C" int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T,
   hipStream_t st = S(stream);
   const int nr = std::min((T + 3) / 4 * 4, 64);  // routing rows: whole waves, at most 16
   const size_t fused_lds = ((size_t)nr * route_row_words(E, topk) + E + (size_t)T * topk) * 4;
-  if (gathered_gemv(T, H, I)) {  // slot-order ids are all the gathered GEMVs need: no placement
+  if (gathered_gemv(T, H, I, topk)) {  // slot-order ids are all the gathered GEMVs need: no placement
     const int rc = route_launch(logits, T, E, topk, normalize, R, st);
     if (rc) return rc;
   } else if (fused_lds <= 64 * 1024) {

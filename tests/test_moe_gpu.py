@@ -95,6 +95,20 @@ def test_swiglu_qwen_shape(T):
     assert_close(y.float().cpu().numpy(), ref, what=f"moe qwen shape T={T}")
 
 
+@pytest.mark.parametrize("T,k", [(2, 32), (1, 64)])
+def test_swiglu_large_topk_few_tokens(T, k):
+    """Many slots for one or two tokens: past the gathered GEMVs' LDS the per-block kernels run."""
+    E, H, I = 64, 512, 768
+    (g, u, d), ex = experts(E, H, I, seed=k)
+    x = synth.fp16_normal((T, H), seed=k + 1)
+    logits = np.random.default_rng(k + 2).standard_normal((T, E)).astype(np.float32)
+    y = moe.swiglu(torch.from_numpy(x).to(DEV), torch.from_numpy(logits).to(DEV), ex, top_k=k)
+    assert y is not None
+    rid, rw = oracle.moe_route(logits, k)
+    ref = oracle.moe_swiglu(ggml.Q4_K, x.astype(np.float32), rid, rw, g, u, d, E, I)
+    assert_close(y.float().cpu().numpy(), ref, what=f"moe T={T} k={k}")
+
+
 def test_declines():
     _, ex = experts(4, 256, 256, seed=1)
     x = torch.zeros((2, 256), dtype=torch.float32, device=DEV)
