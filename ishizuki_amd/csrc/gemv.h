@@ -257,9 +257,16 @@ static int launch_gemv_l(const typename F::Args &a, const void *x, void *y, hipS
   }
 }
 
+int gemv_lpr_override();  // ISHZ_GEMV_LPR (tuning)
+
 template <class F>
 static int launch_gemv(const typename F::Args &a, const void *x, void *y, hipStream_t st) {
   const int units = F::units(a.K);
+  switch (gemv_lpr_override()) {
+    case 16: return launch_gemv_l<F, 16>(a, x, y, st);
+    case 32: return launch_gemv_l<F, 32>(a, x, y, st);
+    case 64: return launch_gemv_l<F, 64>(a, x, y, st);
+  }
   if (units <= 160) return launch_gemv_l<F, 16>(a, x, y, st);
   if (units <= 384) return launch_gemv_l<F, 32>(a, x, y, st);
   return launch_gemv_l<F, 64>(a, x, y, st);

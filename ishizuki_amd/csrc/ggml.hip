@@ -326,6 +326,10 @@ int gemv_depth_override() {
   static const int v = env_int("ISHZ_GEMV_D");
   return v;
 }
+int gemv_lpr_override() {
+  static const int v = env_int("ISHZ_GEMV_LPR");
+  return v;
+}
 int gemv_occ_override() {
   static const int v = env_int("ISHZ_GEMV_OCC");
   return v;
