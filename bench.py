@@ -226,6 +226,22 @@ def main():
             for c, sc, bi in sets]
         return calls, nb, nb + 2 * (K + N)
 
+    def affine_nbit_case(N, K, M, bits, seed=6):
+        """Plain (unrotated) 4- or 8-bit MLX affine pack, g64: ishz_affine_matmul."""
+        codes, s, b = synth.affine_pack_bits(N, K, bits, group=64, seed=seed)
+        c0 = torch.from_numpy(codes.view(np.int32)).to(dev)
+        s0, b0 = torch.from_numpy(s).to(dev), torch.from_numpy(b).to(dev)
+        nb = c0.numel() * 4 + s0.numel() * 2 + b0.numel() * 2
+        sets = [(c0, s0, b0)] + [(c0.clone(), s0.clone(), b0.clone()) for _ in range(copies_of(nb) - 1)]
+        x = torch.from_numpy(synth.fp16_normal((M, K), seed=seed + 1)).to(dev)
+        y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        L = affine._lib.lib()
+        from ishizuki_amd._torch import ptr
+        calls = [lambda c=c, sc=sc, bi=bi: L.ishz_affine_matmul(
+            ptr(x), 1, M, K, ptr(c), ptr(sc), ptr(bi), 1, N, bits, 64, ptr(y), torch.cuda.current_stream().cuda_stream)
+            for c, sc, bi in sets]
+        return calls, nb, nb + 2 * M * (K + N)
+
     def exl3_case(K, N, M, bits2=4, seed=3):
         t, suh, svh = synth.exl3_pack(K, N, bits2=bits2, seed=seed)
         t0 = torch.from_numpy(t).to(dev)
@@ -299,6 +315,11 @@ def main():
         ("affine2_g64_wht128", lambda M: affine_case(NS, KS, M)),
         ("exl3_2bpw", lambda M: exl3_case(KS, NS, M)),
     ]
+    # 4- and 8-bit MLX affine packs (--all, or by name in --only)
+    for bits in (4, 8):
+        nm = f"affine{bits}_g64"
+        if args.all or nm in only:
+            plan.append((nm, lambda M, bits=bits: affine_nbit_case(NS, KS, M, bits)))
     # the other GGUF formats (--all, or by name in --only)
     for t in (ggml.Q2_K, ggml.IQ4_XS, ggml.IQ2_XXS, ggml.IQ2_S, ggml.IQ3_XXS, ggml.IQ3_S, ggml.IQ1_S, ggml.IQ1_M):
         nm = ggml.NAMES[t].lower()

@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <cstdlib>
 
+#include "affine_nbit.h"
 #include "common.h"
 #include "gemv.h"
 
@@ -762,13 +763,28 @@ static int check_affine(const void *x, int x_dtype, int M, int K, const void *co
                         const void *scales, const void *biases, int scale_dtype, int N, int bits,
                         int group, const void *y) {
   if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
-  if (bits != 2) return decline("only 2-bit packs are decoded in-kernel");
+  if (bits != 2 && bits != 4 && bits != 8) return decline("packs of 2, 4 or 8 bits are decoded in-kernel");
   if (group != 64 && group != 128) return decline("group size must be 64 or 128");
   if (scale_dtype != ISHZ_DT_F16 && scale_dtype != ISHZ_DT_BF16) return decline("scales must be fp16 or bf16");
   if (M < 1 || M > 16) return decline("row count outside 1..16");
   if (K <= 0 || K % 128 || N <= 0) return decline("K must be a positive multiple of 128");
   if (!x || !codes || !scales || !biases || !y) return einval("null pointer");
   return ISHZ_OK;
+}
+
+// 4- and 8-bit packs (x already rotated when the layer rotates).
+static int affine_nbit_dispatch(const void *x, int M, int K, const uint32_t *codes, const void *scales,
+                                const void *biases, int bf16s, int N, int bits, int group, void *y, hipStream_t st) {
+#define ISHZ_NB(B, G)                                                                              \
+  return bf16s ? affine_nbit<B, G, true>(x, M, K, codes, scales, biases, N, y, st)              \
+               : affine_nbit<B, G, false>(x, M, K, codes, scales, biases, N, y, st)
+  if (bits == 4) {
+    if (group == 64) ISHZ_NB(4, 64);
+    ISHZ_NB(4, 128);
+  }
+  if (group == 64) ISHZ_NB(8, 64);
+  ISHZ_NB(8, 128);
+#undef ISHZ_NB
 }
 
 static int affine_dispatch(const void *x, int M, int K, const float *signs, int block,
@@ -810,6 +826,9 @@ extern "C" int ishz_affine_matmul(const void *x, int x_dtype, int M, int K, cons
                                   int bits, int group, void *y, ishz_stream_t stream) {
   int rc = check_affine(x, x_dtype, M, K, codes, scales, biases, scale_dtype, N, bits, group, y);
   if (rc) return rc;
+  if (bits != 2)
+    return affine_nbit_dispatch(x, M, K, codes, scales, biases, scale_dtype == ISHZ_DT_BF16, N, bits, group, y,
+                                S(stream));
   return affine_dispatch(x, M, K, nullptr, 0, codes, scales, biases, scale_dtype == ISHZ_DT_BF16, N,
                          group, y, S(stream));
 }
@@ -831,6 +850,14 @@ extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, cons
   if (block > 0 && (!pow2(block) || block > 4096 || K % block)) return decline("bad Hadamard block");
   const int bf16s = scale_dtype == ISHZ_DT_BF16;
   hipStream_t st = S(stream);
+  if (bits != 2) {  // 4- and 8-bit packs: rotate x once into the workspace, then the matmul
+    if (block == 0) return affine_nbit_dispatch(x, M, K, codes, scales, biases, bf16s, N, bits, group, y, st);
+    if (!workspace || workspace_bytes < ishz_affine_workspace_size(M, K))
+      return einval("workspace too small (ishz_affine_workspace_size)");
+    rc = ishz_hadamard(x, ISHZ_DT_F16, M, K, block, signs, 0, workspace, stream);
+    if (rc) return rc;
+    return affine_nbit_dispatch(workspace, M, K, codes, scales, biases, bf16s, N, bits, group, y, st);
+  }
   if (M == 1 && block > 0 && block <= 128 && workspace && workspace_bytes >= ishz_affine_workspace_size(1, K) &&
       !getenv("ISHZ_M1_MFMA")) {
     const FAffine<64, false>::Args a{codes, nullptr, nullptr, signs, block, K, N, nullptr};

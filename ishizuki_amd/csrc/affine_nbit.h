@@ -1,0 +1,177 @@
+// MLX affine packs of 4 or 8 bits per weight (VerifyMatmul.applyAny's other fast-path widths,
+// Core/VerifyMatmul.swift:83-89; pack layout Quantize/WeightedAffineQuantizer.swift:142-153):
+// w[n][k] = s[n][k/gs] * q + b[n][k/gs], q the bits-wide field k of the row's little-endian u32
+// stream, so a word holds 8 (4-bit) or 4 (8-bit) consecutive codes.
+//
+// One format serves both skeletons: a "unit" / verify quarter is 64 weights of one group (group
+// size 64 or 128), 32 or 64 bytes of codes plus the group's scale and bias. Codes are masked in
+// place with the fp16 exponent of 1024 (`v_and_or_b32`), so a word yields exact fp16 1024 + q in
+// pairs; the offset and the bias come back through the sum of x over the unit:
+//   sum_k w_k x_k = s * (sum (1024 + q_k) x_k - 1024 X) + b * X.
+// Pair orders: 4-bit word >> 4j masked with 0x000F000F gives codes (j, j + 4); 8-bit word (>> 8)
+// masked with 0x00FF00FF gives (0, 2) and (1, 3). x is staged in the same pair order.
+#pragma once
+#include "ggml_formats.h"
+#include "vgemm.h"
+
+namespace ishz {
+
+// (x0, x4, x1, x5, x2, x6, x3, x7): the pair order of 4-bit codes masked from one word.
+DEV u4 perm04(u4 a) {
+  return u4{(a.x & 0xffffu) | (a.z << 16), (a.x >> 16) | (a.z & 0xffff0000u), (a.y & 0xffffu) | (a.w << 16),
+            (a.y >> 16) | (a.w & 0xffff0000u)};
+}
+
+// The problem the streaming MFMA kernel runs for these packs (one group: the whole matrix).
+struct VAffineN {
+  const uint16_t *x;
+  const uint32_t *codes;
+  const uint16_t *scales, *biases;
+  int M, K, N;
+  uint16_t *y;
+  struct Group {};
+  DEV bool group(int, Group &) const { return true; }
+  DEV int count(const Group &) const { return M; }
+  DEV int rows(const Group &) const { return N; }
+  DEV const uint16_t *xrow(const Group &, int tk) const { return x + (size_t)tk * K; }
+  DEV const uint8_t *wrow(const Group &, int) const { return nullptr; }  // the format reads through vload_p
+  DEV void finish(const Group &, int c0, int m, int tb, int te, const float *out) const {
+    for (int o = threadIdx.x; o < (te - tb) * 256; o += blockDim.x) {
+      const int tk = (o >> 4) & 15, row = (tb + (o >> 8)) * 16 + (o & 15);
+      if (tk < m && row < N) y[(size_t)(c0 + tk) * N + row] = f2h(out[o]);
+    }
+  }
+};
+
+template <int BITS, int GS, bool BF16S>
+struct FAffineN : GgmlGemv<FAffineN<BITS, GS, BF16S>> {
+  static_assert(BITS == 4 || BITS == 8, "4- or 8-bit packs");
+  using Base = GgmlGemv<FAffineN<BITS, GS, BF16S>>;
+  struct Args {
+    const uint32_t *codes;
+    const uint16_t *scales, *biases;
+    int K, N;
+  };
+  static constexpr int WPU = 64 * BITS / 32;  // code words per 64-weight unit
+  static constexpr int BS = 64, UPB = 1, UNIT_BLOCKS = 1;
+  static constexpr int MAXB = 2, PREFB = 2, DEPTH = BITS == 4 ? 3 : 2;
+  static constexpr int R = 8, Q = 2, SUM_LEN = 32;
+  static constexpr bool XSUM = true, GRID = false, VGRID = false, XPERM = BITS == 8;
+  static DEV u4 xperm(u4 v) { return BITS == 4 ? perm04(v) : perm0213(v); }
+  static __host__ __device__ int units(int K) { return K / 64; }
+  static int occ(const Args &) { return 2; }
+  static size_t extra_lds_bytes(const Args &) { return 0; }
+  static DEV int slot_k(int u, int r) { return 64 * u + 8 * r; }
+  static DEV int sum_k(int u, int q) { return 64 * u + 32 * q; }
+  struct Raw {
+    u4 q[WPU / 4];
+    uint32_t s, b;
+  };
+  static DEV float ld_s(uint32_t v) { return BF16S ? __builtin_bit_cast(float, v << 16) : h2f(v); }
+  // Unit u of row `row`: its codes and its group's scale and bias.
+  static DEV Raw load_unit(const uint32_t *codes, const uint16_t *scales, const uint16_t *biases, int K, int row,
+                           int u) {
+    Raw r;
+    const u4 *c = (const u4 *)(codes + (size_t)row * (K * BITS / 32) + (size_t)u * WPU);
+#pragma unroll
+    for (int i = 0; i < WPU / 4; i++) r.q[i] = c[i];
+    const size_t gi = (size_t)row * (K / GS) + (size_t)u * 64 / GS;
+    r.s = scales[gi];
+    r.b = biases[gi];
+    return r;
+  }
+  static DEV Raw load(const Args &a, int row, int u) { return load_unit(a.codes, a.scales, a.biases, a.K, row, u); }
+  struct LaneC {};
+  static DEV LaneC lane(int) { return {}; }
+  // Eight B-operand / dot words of 8 codes each, in the x pair order.
+  static DEV void decode(const Raw &r, u4 *B, uint32_t mg) {
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      if constexpr (BITS == 4) {
+        const uint32_t w = r.q[t >> 2][t & 3];
+        B[t] = u4{and_or(w, 0x000F000Fu, mg), and_or(w >> 4, 0x000F000Fu, mg), and_or(w >> 8, 0x000F000Fu, mg),
+                  and_or(w >> 12, 0x000F000Fu, mg)};
+      } else {
+        const uint32_t w0 = r.q[(2 * t) >> 2][(2 * t) & 3], w1 = r.q[(2 * t + 1) >> 2][(2 * t + 1) & 3];
+        B[t] = u4{and_or(w0, 0x00FF00FFu, mg), and_or(w0 >> 8, 0x00FF00FFu, mg), and_or(w1, 0x00FF00FFu, mg),
+                  and_or(w1 >> 8, 0x00FF00FFu, mg)};
+      }
+    }
+  }
+  static DEV float dot(const Raw &r, const UnitX &s, const LaneC &) {
+    u4 B[8];
+    decode(r, B, s.mg);
+    float S = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      const u4 X = s.slot(t);
+      S = dot2(B[t].x, X.x, S);
+      S = dot2(B[t].y, X.y, S);
+      S = dot2(B[t].z, X.z, S);
+      S = dot2(B[t].w, X.w, S);
+    }
+    const float X = s.sum(0) + s.sum(1);
+    return ld_s(r.s) * (S - 1024.0f * X) + ld_s(r.b) * X;
+  }
+  typedef typename Base::XPre XPre;
+  static DEV XPre stage_load(const Args &, const uint16_t *x, int units) {
+    XPre p;
+    Base::load_slots(x, units, threadIdx.x, p.v);
+    Base::load_sums(x, units, threadIdx.x, p.sv);
+    return p;
+  }
+  static DEV void stage(const Args &, const uint16_t *x, u4 *xs, float *xsum, u4 *extra, int units, const XPre &pre) {
+    Base::stage_body(x, xs, xsum, extra, units, pre);
+  }
+
+  // Streaming MFMA verify: quarter g of step j is unit 4j + g of the chunk; one scale group per
+  // quarter (VNS = 1, eight MFMAs).
+  static constexpr int VNS = 1, VSTEP_BYTES = 0, VDEPTH = BITS == 4 ? 3 : 2;
+  typedef Raw VRaw;
+  static DEV VRaw vload_p(const VAffineN &p, const VAffineN::Group &, int row, int kc0, int j, int g) {
+    return load_unit(p.codes, p.scales, p.biases, p.K, row, kc0 / 64 + 4 * j + g);
+  }
+  static DEV void vdecode(const VRaw &r, u4 *B, uint32_t mg, const u4 *, const u4 *) { decode(r, B, mg); }
+  static DEV void vstage(const uint16_t *x, int j, int g, int, u4 *A, float &off1, float &X) {
+    const uint16_t *p = x + 256 * j + 64 * g;
+    X = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+      const u4 v = *(const u4 *)(p + 8 * b);
+#pragma unroll
+      for (int e = 0; e < 4; e++) X = dot2(v[e], 0x3C003C00u, X);
+      A[b] = xperm(v);
+    }
+    off1 = 1024.0f * X;
+  }
+  static DEV void vscale(const VRaw &r, int, int, float &sc, float &mn) {
+    sc = ld_s(r.s);
+    mn = ld_s(r.b);
+  }
+};
+
+// y[M][N] = x . W^T for a 4- or 8-bit pack: the streaming GEMV at M = 1, the streaming MFMA
+// kernel for M = 2..16 (K a multiple of 256 there; declined otherwise).
+template <int BITS, int GS, bool BF16S>
+static int affine_nbit(const void *x, int M, int K, const uint32_t *codes, const void *scales, const void *biases,
+                       int N, void *y, hipStream_t st) {
+  using F = FAffineN<BITS, GS, BF16S>;
+  if (K % 64) return decline("K must be a multiple of 64");
+  if (M == 1) {
+    const typename F::Args a{codes, (const uint16_t *)scales, (const uint16_t *)biases, K, N};
+    return launch_gemv<F>(a, x, y, st);
+  }
+  if (K % 256) return decline("verify rows need K a multiple of 256 for 4- and 8-bit packs");
+  const VAffineN p{(const uint16_t *)x, codes, (const uint16_t *)scales, (const uint16_t *)biases, M, K, N,
+                   (uint16_t *)y};
+  const int ntiles = (N + 15) / 16;
+  const int T = (ntiles + gemv_num_cu() - 1) / gemv_num_cu();
+  switch ((M + 3) / 4) {
+    case 1: return launch_vgemm_p<F, VAffineN, 1>(p, K, N, 1, T, st);
+    case 2: return launch_vgemm_p<F, VAffineN, 2>(p, K, N, 1, T, st);
+    case 3: return launch_vgemm_p<F, VAffineN, 3>(p, K, N, 1, T, st);
+    default: return launch_vgemm_p<F, VAffineN, 4>(p, K, N, 1, T, st);
+  }
+}
+
+}  // namespace ishz

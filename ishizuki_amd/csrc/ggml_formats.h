@@ -72,6 +72,7 @@ struct GgmlGemv {
     if constexpr (D::VGRID) build_iq2xs_tables_nat(t, t + 512);
   }
   static constexpr bool XPERM = true;  // x slots staged pair-permuted (perm0213) or natural
+  static DEV u4 xperm(u4 v) { return D::XPERM ? perm0213(v) : v; }  // a format may replace it
   static DEV auto load(const Args &a, int row, int u) { return D::load_row(a.w + (size_t)row * a.rb, u); }
   // Loads for U slots (US sums) per thread are issued together before any is stored, so
   // staging costs a memory latency per U items rather than one each; the first round's loads
@@ -115,7 +116,7 @@ struct GgmlGemv {
 #pragma unroll
     for (int j = 0; j < U; j++) {
       const int i = i0 + j * (int)blockDim.x;
-      if (i < ns && (i / (16 * D::R)) * 16 + (i & 15) < units) xs[i] = D::XPERM ? perm0213(v[j]) : v[j];
+      if (i < ns && (i / (16 * D::R)) * 16 + (i & 15) < units) xs[i] = D::xperm(v[j]);
     }
   }
   static DEV void store_sums(float *xsum, int units, int i0, const u4 (*v)[SLMAX]) {
@@ -150,8 +151,12 @@ struct GgmlGemv {
       }
     }
   }
-  static DEV void stage(const Args &a, const uint16_t *x, u4 *xs, float *xsum, u4 *extra, int units,
+  static DEV void stage(const Args &, const uint16_t *x, u4 *xs, float *xsum, u4 *extra, int units,
                         const XPre &pre) {
+    stage_body(x, xs, xsum, extra, units, pre);
+  }
+  // The staging itself (formats with their own Args call it from their stage).
+  static DEV void stage_body(const uint16_t *x, u4 *xs, float *xsum, u4 *extra, int units, const XPre &pre) {
     const int ug = (units + 15) / 16, bd = blockDim.x;
     const int ns = ug * 16 * D::R;
     store_slots(xs, units, threadIdx.x, pre.v);  // first round: loads issued by stage_load

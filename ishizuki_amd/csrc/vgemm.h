@@ -19,7 +19,8 @@
 //
 // A format F provides:
 //   VNS                              sub-units per quarter
-//   VRaw vload(row, j, g)            the quarter's codes and the row's step header
+//   VRaw vload(row, j, g)            the quarter's codes and the row's step header (or
+//   VRaw vload_p(p, group, row, kc0, j, g)   for packs held in several arrays)
 //   void vdecode(r, B[8], tabs)      B operands (MFMA b of sub-unit b / (8 / VNS))
 //   void vstage(xrow, j, g, s, A, off1, X)   A words of sub-unit s (8 / VNS of them) and sums
 //   void vscale(r, g, s, sc, mn)     value of sub-unit s = sc * (C - off1) + mn * X
@@ -120,7 +121,10 @@ __global__ __launch_bounds__(64 * NW) void vgemm_kernel(P p, int K, int Kc, int 
         int tl, j;
         where(min(k, cnt - 1), tl, j);
         const int row = min((tb + tl) * 16 + n, N - 1);
-        r = F::vload(p.wrow(gp, row) + (size_t)(kc0 / 256) * F::VSTEP_BYTES, j, G);
+        if constexpr (requires { F::vload_p(p, gp, row, kc0, j, G); })
+          r = F::vload_p(p, gp, row, kc0, j, G);  // formats whose rows are not one byte run
+        else
+          r = F::vload(p.wrow(gp, row) + (size_t)(kc0 / 256) * F::VSTEP_BYTES, j, G);
       };
       Raw ring[D];
       if (cnt > 0) {

@@ -64,6 +64,22 @@ def affine_pack(N, K, group=64, bits=2, seed=0, scale=0.02, probs=(0.3, 0.4, 0.3
     return codes, s, b
 
 
+def affine_pack_bits(N, K, bits, group=64, seed=0, scale=0.02):
+    """MLX affine pack of `bits` in {4, 8}: uniform random codes (value k at bits (k % (32/bits)) *
+    bits of word k / (32/bits)), scales |N|*scale and biases -s * 2^(bits-1) (fp16), so weights
+    are centred on zero."""
+    assert bits in (4, 8)
+    r = rng(seed)
+    per = 32 // bits
+    q = r.integers(0, 1 << bits, size=(N, K // per, per), dtype=np.uint64)
+    codes = np.zeros((N, K // per), np.uint64)
+    for i in range(per):
+        codes |= q[:, :, i] << np.uint64(bits * i)
+    s = fp16_absnormal(r, N * (K // group), scale).reshape(N, K // group)
+    b = (-s.astype(np.float32) * (1 << (bits - 1))).astype(np.float16)
+    return codes.astype(np.uint32), s, b
+
+
 def exl3_pack(K, N, bits2=4, seed=0, scale=0.02):
     """EXL3 tensor: trellis int16 [K/16, N/16, 8*bits2] of uniform random bits, and suh/svh
     scales fp16 |N(0,1)|*scale."""

@@ -62,6 +62,54 @@ def test_affine_matmul(M, group):
     assert_close(y.float().cpu().numpy(), ref, what=f"affine M={M} g={group}")
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 16])
+@pytest.mark.parametrize("group,bf16", [(64, False), (128, True)])
+def test_affine_wide_bits(bits, M, group, bf16):
+    """4- and 8-bit packs (VerifyMatmul.applyAny's other fast-path widths): the GEMV at M = 1,
+    the streaming MFMA kernel above."""
+    N, K = 1000, 1024
+    codes, s, b = synth.affine_pack_bits(N, K, bits, group=group, seed=bits + M)
+    x = synth.fp16_normal((M, K), seed=M + 40)
+    ref = oracle.affine_matmul(x.astype(np.float32), codes, s.view(np.uint16), b.view(np.uint16), N, bits, group)
+    sd, bd = torch.from_numpy(s).to(DEV), torch.from_numpy(b).to(DEV)
+    if bf16:  # bf16 scales and biases (the values rounded to bf16; the reference uses them as given)
+        sd, bd = sd.to(torch.bfloat16), bd.to(torch.bfloat16)
+        ref = _ref_bf16(x, codes, sd, bd, N, K, bits, group)
+    y = affine.quantized_matmul(torch.from_numpy(x).to(DEV), torch.from_numpy(codes.view(np.int32)).to(DEV), sd, bd,
+                                group_size=group, bits=bits)
+    assert y is not None
+    assert_close(y.float().cpu().numpy(), ref, what=f"affine bits={bits} M={M} g={group} bf16={bf16}")
+
+
+def _ref_bf16(x, codes, sd, bd, N, K, bits, group):
+    """Reference with bf16 scales: dequantize through the oracle with unit scale / zero bias, then
+    apply the bf16 values (exact in fp32)."""
+    per = 32 // bits
+    q = np.stack([(codes[:, k // per] >> np.uint32(bits * (k % per))) & np.uint32((1 << bits) - 1)
+                  for k in range(K)], 1).astype(np.float32)
+    s = np.repeat(sd.float().cpu().numpy(), group, 1)
+    b = np.repeat(bd.float().cpu().numpy(), group, 1)
+    w = (s * q + b).astype(np.float32)
+    return x.astype(np.float32) @ w.T
+
+
+@pytest.mark.parametrize("bits,M", [(4, 1), (4, 8), (8, 3)])
+def test_affine_wide_bits_rotated_linear(bits, M):
+    """PackedLinear's rotated forward with a 4- or 8-bit pack: x rotated once, then the matmul."""
+    N, K = 300, 1024
+    codes, s, b = synth.affine_pack_bits(N, K, bits, group=64, seed=bits * 3 + M)
+    x = synth.fp16_normal((M, K), seed=M + 50)
+    signs = synth.hadamard_signs(K, seed=7)
+    xr = oracle.hadamard(x.astype(np.float32), 128, signs).astype(np.float16).astype(np.float32)
+    ref = oracle.affine_matmul(xr, codes, s.view(np.uint16), b.view(np.uint16), N, bits, 64)
+    y = affine.linear(torch.from_numpy(x).to(DEV), torch.from_numpy(codes.view(np.int32)).to(DEV),
+                      torch.from_numpy(s).to(DEV), torch.from_numpy(b).to(DEV), signs=torch.from_numpy(signs),
+                      block=128, group_size=64, bits=bits)
+    assert y is not None
+    assert_close(y.float().cpu().numpy(), ref, what=f"affine linear bits={bits} M={M}")
+
+
 @pytest.mark.parametrize("M", [5, 8, 16])
 def test_affine_verify_very_wide_output(M):
     """40000 output rows (2500 tiles, more than 16 / NQ per CU): the verify kernel runs in several

@@ -133,6 +133,22 @@ def test_affine_closed_form():
     assert np.array_equal(np.abs(w[q != 1]), sf[q != 1]) and np.all(w[q == 1] == 0)
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+def test_affine_closed_form_wide(bits):
+    """4- and 8-bit packs: field k of the row's u32 stream, restated with numpy bit ops."""
+    from ishizuki_amd import synth
+    N, K, g = 5, 256, 128
+    codes, s, b = synth.affine_pack_bits(N, K, bits, group=g, seed=bits)
+    w = oracle.affine_dequant(codes, s.view(np.uint16), b.view(np.uint16), N, K, bits, g)
+    per = 32 // bits
+    q = np.stack([(codes[:, k // per] >> np.uint32(bits * (k % per))) & np.uint32((1 << bits) - 1)
+                  for k in range(K)], 1).astype(np.float32)
+    sf = np.repeat(s.astype(np.float32), g, 1)
+    bf = np.repeat(b.astype(np.float32), g, 1)
+    assert np.array_equal(w, (sf * q + bf).astype(np.float32))
+    assert q.max() == (1 << bits) - 1 and q.min() == 0
+
+
 def test_matmul_fused_agrees_with_expanded():
     from ishizuki_amd import synth
     for t, K in ((2, 512), (12, 512), (14, 512), (17, 512)):
