@@ -282,6 +282,33 @@ def main():
         nb = distinct * 3 * ex.expert_bytes
         return calls, nb, nb, distinct
 
+    def moe_affine_case(T, E=128, H=2048, I=768, k=8, bits=4, seed=8):
+        """The MoE FFN over MLX affine stacked experts (4-bit g64), weights made on the device."""
+        g = torch.Generator(device=dev).manual_seed(seed)
+
+        def pack(rows, K):
+            c = torch.randint(-2**31, 2**31 - 1, (E, rows, K * bits // 32), dtype=torch.int32, device=dev, generator=g)
+            sc = (torch.rand((E, rows, K // 64), device=dev, generator=g) * 0.01).half()
+            return c, sc, (-sc.float() * (1 << (bits - 1))).half()
+        packs = (pack(I, H), pack(I, H), pack(H, I))
+        per_expert = sum(p[0].numel() * 4 + p[1].numel() * 2 + p[2].numel() * 2 for p in packs) // E
+        copies = [packs] + [tuple(tuple(t.clone() for t in p) for p in packs)
+                            for _ in range(copies_of(per_expert * E) - 1)]
+        x = torch.from_numpy(synth.fp16_normal((T, H), seed=seed + 3)).to(dev)
+        logits_np = np.random.default_rng(seed + 5).standard_normal((T, E)).astype(np.float32)
+        logits = torch.from_numpy(logits_np).to(dev)
+        distinct = len(np.unique(np.argsort(-logits_np, axis=1, kind="stable")[:, :k]))
+        y = torch.empty((T, H), dtype=torch.float16, device=dev)
+        L = moe._lib.lib()
+        from ishizuki_amd._torch import ptr
+        wsb = L.ishz_moe_workspace_size(T, H, E, I, k)
+        wsp = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        calls = [lambda c=c: L.ishz_moe_swiglu_affine(
+            ptr(x), 1, T, H, ptr(logits), E, k, 1, *(ptr(t) for p in c for t in p), 1, bits, 64, I, ptr(y), None, None,
+            ptr(wsp), wsb, torch.cuda.current_stream().cuda_stream) for c in copies]
+        nb = distinct * per_expert
+        return calls, nb, nb, distinct
+
     def measure(name, builder, M, steps, warmup, extra=None, nk=None):
         out = builder()
         calls, wbytes, allbytes = out[0], out[1], out[2]
@@ -337,6 +364,11 @@ def main():
         for T in (1, 8, 64):
             r, _, _ = measure("moe_q4k_e128_h2048_i768_top8", lambda T=T: moe_case(T), T, fam_steps, args.warmup,
                               extra=lambda o: {"distinct_experts": int(o[3])})
+            families.append(r)
+    if args.all or "moe_affine4" in only:
+        for T in (1, 8, 64):
+            r, _, _ = measure("moe_affine4_g64_e128_h2048_i768_top8", lambda T=T: moe_affine_case(T), T, fam_steps,
+                              args.warmup, extra=lambda o: {"distinct_experts": int(o[3])})
             families.append(r)
     if args.all:
         for M in (1,):

@@ -156,6 +156,19 @@ int ishz_moe_route(const float *logits, int T, int E, int topk, int normalize, i
    gatherQuantizedMM over affine experts; GGUF experts are a composition of its routing with the
    GGML kernels.) */
 size_t ishz_moe_workspace_size(int T, int H, int E, int I, int topk);
+
+/* The same FFN over MLX affine stacked experts, the reference's own expert format
+   (StackedExperts, Text/MoEBlock.swift:22-50, multiplied through gatherQuantizedMM at :45-49):
+   gate and up packs hold E experts of [I][H] weights, down E experts of [H][I]; codes u32
+   [E][rows][K * bits / 32], scales / biases [E][rows][K / group] in scale_dtype. bits 4 or 8,
+   group 64 or 128, H and I multiples of 256. Routing, workspace and outputs as ishz_moe_swiglu. */
+int ishz_moe_swiglu_affine(const void *x, int x_dtype, int T, int H, const float *logits, int E,
+                           int topk, int normalize, const uint32_t *gate_codes, const void *gate_scales,
+                           const void *gate_biases, const uint32_t *up_codes, const void *up_scales,
+                           const void *up_biases, const uint32_t *down_codes, const void *down_scales,
+                           const void *down_biases, int scale_dtype, int bits, int group, int I,
+                           void *y, int32_t *ids_out, float *weights_out, void *workspace,
+                           size_t workspace_bytes, ishz_stream_t stream);
 int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T, int H, const float *logits,
                     int E, int topk, int normalize, const void *gate, const void *up,
                     const void *down, size_t expert_bytes, int I, void *y, int32_t *ids_out,

@@ -22,6 +22,12 @@ DEV u4 perm04(u4 a) {
             (a.y >> 16) | (a.w & 0xffff0000u)};
 }
 
+// One weight row of an affine pack: its code words and its groups' scales and biases.
+struct AffRow {
+  const uint32_t *codes;
+  const uint16_t *scales, *biases;
+};
+
 // The problem the streaming MFMA kernel runs for these packs (one group: the whole matrix).
 struct VAffineN {
   const uint16_t *x;
@@ -29,6 +35,10 @@ struct VAffineN {
   const uint16_t *scales, *biases;
   int M, K, N;
   uint16_t *y;
+  int wpr, gpr;  // code words and scale groups per row
+  DEV AffRow arow(int row) const {
+    return {codes + (size_t)row * wpr, scales + (size_t)row * gpr, biases + (size_t)row * gpr};
+  }
   struct Group {};
   DEV bool group(int, Group &) const { return true; }
   DEV int count(const Group &) const { return M; }
@@ -68,19 +78,20 @@ struct FAffineN : GgmlGemv<FAffineN<BITS, GS, BF16S>> {
     uint32_t s, b;
   };
   static DEV float ld_s(uint32_t v) { return BF16S ? __builtin_bit_cast(float, v << 16) : h2f(v); }
-  // Unit u of row `row`: its codes and its group's scale and bias.
-  static DEV Raw load_unit(const uint32_t *codes, const uint16_t *scales, const uint16_t *biases, int K, int row,
-                           int u) {
+  // Unit u of a row: its codes and its group's scale and bias.
+  static DEV Raw load_unit(const AffRow &w, int u) {
     Raw r;
-    const u4 *c = (const u4 *)(codes + (size_t)row * (K * BITS / 32) + (size_t)u * WPU);
+    const u4 *c = (const u4 *)(w.codes + (size_t)u * WPU);
 #pragma unroll
     for (int i = 0; i < WPU / 4; i++) r.q[i] = c[i];
-    const size_t gi = (size_t)row * (K / GS) + (size_t)u * 64 / GS;
-    r.s = scales[gi];
-    r.b = biases[gi];
+    r.s = w.scales[u * 64 / GS];
+    r.b = w.biases[u * 64 / GS];
     return r;
   }
-  static DEV Raw load(const Args &a, int row, int u) { return load_unit(a.codes, a.scales, a.biases, a.K, row, u); }
+  static DEV Raw load(const Args &a, int row, int u) {
+    const size_t gpr = a.K / GS;
+    return load_unit({a.codes + (size_t)row * (a.K * BITS / 32), a.scales + row * gpr, a.biases + row * gpr}, u);
+  }
   struct LaneC {};
   static DEV LaneC lane(int) { return {}; }
   // Eight B-operand / dot words of 8 codes each, in the x pair order.
@@ -128,8 +139,13 @@ struct FAffineN : GgmlGemv<FAffineN<BITS, GS, BF16S>> {
   // quarter (VNS = 1, eight MFMAs).
   static constexpr int VNS = 1, VSTEP_BYTES = 0, VDEPTH = BITS == 4 ? 3 : 2;
   typedef Raw VRaw;
-  static DEV VRaw vload_p(const VAffineN &p, const VAffineN::Group &, int row, int kc0, int j, int g) {
-    return load_unit(p.codes, p.scales, p.biases, p.K, row, kc0 / 64 + 4 * j + g);
+  // Any problem whose rows are affine rows: P::arow(group, row) or, with one group, P::arow(row).
+  template <class P>
+  static DEV VRaw vload_p(const P &p, const typename P::Group &gp, int row, int kc0, int j, int g) {
+    if constexpr (requires { p.arow(gp, row); })
+      return load_unit(p.arow(gp, row), kc0 / 64 + 4 * j + g);
+    else
+      return load_unit(p.arow(row), kc0 / 64 + 4 * j + g);
   }
   static DEV void vdecode(const VRaw &r, u4 *B, uint32_t mg, const u4 *, const u4 *) { decode(r, B, mg); }
   static DEV void vstage(const uint16_t *x, int j, int g, int, u4 *A, float &off1, float &X) {
@@ -163,7 +179,7 @@ static int affine_nbit(const void *x, int M, int K, const uint32_t *codes, const
   }
   if (K % 256) return decline("verify rows need K a multiple of 256 for 4- and 8-bit packs");
   const VAffineN p{(const uint16_t *)x, codes, (const uint16_t *)scales, (const uint16_t *)biases, M, K, N,
-                   (uint16_t *)y};
+                   (uint16_t *)y, K * BITS / 32, K / GS};
   const int ntiles = (N + 15) / 16;
   const int T = (ntiles + gemv_num_cu() - 1) / gemv_num_cu();
   switch ((M + 3) / 4) {

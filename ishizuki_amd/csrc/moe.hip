@@ -16,6 +16,7 @@
 #include <algorithm>
 #include <cstdlib>
 
+#include "affine_nbit.h"
 #include "ggml_formats.h"
 #include "vgemm.h"
 
@@ -635,6 +636,76 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
   return ISHZ_OK;
 }
 
+// Routing, and the pair lists when `place` (the streaming MFMA projections need them; the
+// gathered GEMVs read the slot-order ids only): one launch when it fits one workgroup's LDS.
+static int moe_route_all(const float *logits, int T, int E, int topk, int normalize, const MoeRoute &R, bool place,
+                         hipStream_t st) {
+  const int nr = std::min((T + 3) / 4 * 4, 64);  // routing rows: whole waves, at most 16
+  const size_t fused_lds = ((size_t)nr * route_row_words(E, topk) + E + (size_t)T * topk) * 4;
+  if (!place) return route_launch(logits, T, E, topk, normalize, R, st);
+  if (fused_lds <= 64 * 1024) {
+    hipLaunchKernelGGL(moe_route_place_kernel, dim3(1), dim3(16 * nr), fused_lds, st, logits, T, E, topk, normalize, R);
+    ISHZ_LAUNCH_CHECK("moe route launch");
+    return ISHZ_OK;
+  }
+  const int rc = route_launch(logits, T, E, topk, normalize, R, st);
+  if (rc) return rc;
+  hipLaunchKernelGGL(moe_place_kernel, dim3(1), dim3(1024), (size_t)E * 4, st, T, E, topk, R);
+  ISHZ_LAUNCH_CHECK("moe place launch");
+  return ISHZ_OK;
+}
+
+// ------------------------------------------------------------------- affine experts
+// StackedExperts (Text/MoEBlock.swift:22-50): every expert's gate, up and down as one MLX affine
+// pack each ([E][I][H], [E][I][H], [E][H][I] weights; scales and biases per group). The same
+// projections as the GGUF problems above, their rows read as affine rows.
+struct AffPack {
+  const uint32_t *codes;
+  const uint16_t *scales, *biases;
+  int wpr, gpr;  // code words and groups per weight row
+  DEV AffRow row(size_t r) const { return {codes + r * wpr, scales + r * gpr, biases + r * gpr}; }
+};
+struct VMoeGateUpA : VMoeGateUp {
+  AffPack g, u;
+  DEV AffRow arow(const Group &gp, int row) const {
+    const int tile = row >> 4, i = min((tile >> 1) * 16 + (row & 15), I - 1);
+    return ((tile & 1) ? u : g).row((size_t)gp.e * I + i);
+  }
+};
+struct VMoeDownA : VMoeDown {
+  AffPack d;
+  DEV AffRow arow(const Group &gp, int row) const { return d.row((size_t)gp.e * H + row); }
+};
+
+template <class F>
+static int moe_ffn_affine(const void *x, int T, int H, int E, int I, int k, const AffPack &gate, const AffPack &up,
+                          const AffPack &down, MoeRoute R, uint16_t *h, uint16_t *o, void *y, hipStream_t st) {
+  const int amax = std::min(E, T * k);
+  const int tiles_gu = 2 * ((I + 15) / 16), tiles_dn = (H + 15) / 16;
+  const int act = std::min(amax, 128);
+  auto pick = [&](int tiles, int even) {
+    int t = std::max(1, std::min(32, tiles * act / (gemv_num_cu() * 2)));
+    if (even) t = std::max(2, t & ~1);
+    return t;
+  };
+  VMoeGateUpA gu{};
+  static_cast<VMoeGateUp &>(gu) = VMoeGateUp{(const uint16_t *)x, nullptr, nullptr, 0, H, I, R, h};
+  gu.g = gate;
+  gu.u = up;
+  int rc = moe_vgemm<F>(gu, T, E, k, H, tiles_gu * 16, amax, pick(tiles_gu, 1), st);
+  if (rc) return rc;
+  VMoeDownA dn{};
+  static_cast<VMoeDown &>(dn) = VMoeDown{h, nullptr, 0, I, H, R, o};
+  dn.d = down;
+  rc = moe_vgemm<F>(dn, T, E, k, I, H, amax, pick(tiles_dn, 0), st);
+  if (rc) return rc;
+  const size_t total = (size_t)T * H;
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)std::min<size_t>((total + 255) / 256, 4096)), dim3(256), 0,
+                     st, o, H, T, k, R, true, (uint16_t *)y);
+  ISHZ_LAUNCH_CHECK("moe combine launch");
+  return ISHZ_OK;
+}
+
 }  // namespace ishz
 
 using namespace ishz;
@@ -676,20 +747,8 @@ extern "C" int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T,
   R.ids_out = ids_out;
   R.w_out = weights_out;
   hipStream_t st = S(stream);
-  const int nr = std::min((T + 3) / 4 * 4, 64);  // routing rows: whole waves, at most 16
-  const size_t fused_lds = ((size_t)nr * route_row_words(E, topk) + E + (size_t)T * topk) * 4;
-  if (gathered_gemv(T, H, I, topk)) {  // slot-order ids are all the gathered GEMVs need: no placement
-    const int rc = route_launch(logits, T, E, topk, normalize, R, st);
-    if (rc) return rc;
-  } else if (fused_lds <= 64 * 1024) {
-    hipLaunchKernelGGL(moe_route_place_kernel, dim3(1), dim3(16 * nr), fused_lds, st, logits, T, E, topk, normalize, R);
-    ISHZ_LAUNCH_CHECK("moe route launch");
-  } else {
-    const int rc = route_launch(logits, T, E, topk, normalize, R, st);
-    if (rc) return rc;
-    hipLaunchKernelGGL(moe_place_kernel, dim3(1), dim3(1024), (size_t)E * 4, st, T, E, topk, R);
-    ISHZ_LAUNCH_CHECK("moe place launch");
-  }
+  const int rc = moe_route_all(logits, T, E, topk, normalize, R, !gathered_gemv(T, H, I, topk), st);
+  if (rc) return rc;
   uint16_t *h = (uint16_t *)((uint8_t *)workspace + L.h), *o = (uint16_t *)((uint8_t *)workspace + L.o);
   uint16_t *gu = (uint16_t *)((uint8_t *)workspace + L.gu);
   switch (type) {
@@ -697,4 +756,48 @@ extern "C" int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T,
   case ISHZ_GGML_Q6_K: return moe_ffn<FQ6_K>(x, T, H, E, I, topk, gate, up, down, R, h, gu, o, y, st);
   default: return moe_ffn<FQ4_0>(x, T, H, E, I, topk, gate, up, down, R, h, gu, o, y, st);
   }
+}
+
+extern "C" int ishz_moe_swiglu_affine(const void *x, int x_dtype, int T, int H, const float *logits, int E,
+                                      int topk, int normalize, const uint32_t *gate_codes,
+                                      const void *gate_scales, const void *gate_biases,
+                                      const uint32_t *up_codes, const void *up_scales, const void *up_biases,
+                                      const uint32_t *down_codes, const void *down_scales,
+                                      const void *down_biases, int scale_dtype, int bits, int group, int I,
+                                      void *y, int32_t *ids_out, float *weights_out, void *workspace,
+                                      size_t workspace_bytes, ishz_stream_t stream) {
+  if (bits != 4 && bits != 8) return decline("affine experts of 4 or 8 bits are decoded in-kernel");
+  if (group != 64 && group != 128) return decline("group size must be 64 or 128");
+  if (scale_dtype != ISHZ_DT_F16 && scale_dtype != ISHZ_DT_BF16) return decline("scales must be fp16 or bf16");
+  if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
+  if (T <= 0 || E <= 0 || topk <= 0 || topk > E || E > 4096) return decline("bad routing shape");
+  if (topk > 64 || (size_t)4 * route_row_words(E, topk) * 4 > 160 * 1024)
+    return decline("too many experts for one routing workgroup");
+  if (H <= 0 || I <= 0 || H % 256 || I % 256) return decline("H and I must be multiples of 256");
+  if (!x || !logits || !gate_codes || !gate_scales || !gate_biases || !up_codes || !up_scales || !up_biases ||
+      !down_codes || !down_scales || !down_biases || !y)
+    return einval("null pointer");
+  const MoeLayout L = moe_layout(T, H, E, I, topk);
+  if (!workspace || workspace_bytes < L.total) return einval("workspace too small (ishz_moe_workspace_size)");
+  MoeRoute R = moe_route_ptrs(workspace, L);
+  R.ids_out = ids_out;
+  R.w_out = weights_out;
+  hipStream_t st = S(stream);
+  int rc = moe_route_all(logits, T, E, topk, normalize, R, true, st);
+  if (rc) return rc;
+  uint16_t *h = (uint16_t *)((uint8_t *)workspace + L.h), *o = (uint16_t *)((uint8_t *)workspace + L.o);
+  const AffPack gp{gate_codes, (const uint16_t *)gate_scales, (const uint16_t *)gate_biases, H * bits / 32, H / group};
+  const AffPack upk{up_codes, (const uint16_t *)up_scales, (const uint16_t *)up_biases, H * bits / 32, H / group};
+  const AffPack dp{down_codes, (const uint16_t *)down_scales, (const uint16_t *)down_biases, I * bits / 32, I / group};
+  const bool bf = scale_dtype == ISHZ_DT_BF16;
+#define ISHZ_MA(B, G)                                                                                        \
+  return bf ? moe_ffn_affine<FAffineN<B, G, true>>(x, T, H, E, I, topk, gp, upk, dp, R, h, o, y, st)       \
+            : moe_ffn_affine<FAffineN<B, G, false>>(x, T, H, E, I, topk, gp, upk, dp, R, h, o, y, st)
+  if (bits == 4) {
+    if (group == 64) ISHZ_MA(4, 64);
+    ISHZ_MA(4, 128);
+  }
+  if (group == 64) ISHZ_MA(8, 64);
+  ISHZ_MA(8, 128);
+#undef ISHZ_MA
 }

@@ -1,8 +1,9 @@
 """MoE expert-gathered quantized FFN on MI355X.
 
 Mirrors MoEBlock.callAsFunction / ResidentExperts.swiglu (Sources/IshizukiKit/Text/MoEBlock.swift:
-124-171) for GGML-block experts over libishizuki_hip: routing, gate+up with SwiGLU, down, weighted
-sum. Only the routed experts' blocks are read.
+124-171) over libishizuki_hip, for GGML-block experts and for MLX affine stacked experts
+(StackedExperts, :22-50; 4- or 8-bit packs): routing, gate+up with SwiGLU, down, weighted sum.
+Only the routed experts' weights are read.
 """
 import torch
 
@@ -48,5 +49,39 @@ def swiglu(x, logits, experts, top_k=8, normalize=True, return_routing=False):
                            int(normalize), ptr(ex.gate), ptr(ex.up), ptr(ex.down), ex.expert_bytes, ex.I,
                            ptr(y), ptr(ids), ptr(w), ptr(ws), ws.numel(), stream())
     if not _lib.check(rc, "moe_swiglu"):
+        return None
+    return (y, ids, w) if return_routing else y
+
+
+class AffineExperts:
+    """StackedExperts (Text/MoEBlock.swift:22-50) for gate, up ([E, I, H]) and down ([E, H, I]): each
+    an MLX affine pack (codes int32 [E, rows, K * bits / 32], scales / biases fp16 or bf16
+    [E, rows, K / group])."""
+
+    def __init__(self, gate, up, down, bits, group, experts, hidden, intermediate):
+        self.gate = tuple(t.contiguous() for t in gate)
+        self.up = tuple(t.contiguous() for t in up)
+        self.down = tuple(t.contiguous() for t in down)
+        self.bits, self.group, self.E, self.H, self.I = bits, group, experts, hidden, intermediate
+
+
+def swiglu_affine(x, logits, experts, top_k=8, normalize=True, return_routing=False):
+    """The MoE FFN over affine stacked experts; None if declined."""
+    require_cuda(x, logits)
+    x = x.contiguous()
+    logits = logits.float().contiguous()
+    T, H = x.shape
+    ex = experts
+    L = _lib.lib()
+    ws = torch.empty(L.ishz_moe_workspace_size(T, H, ex.E, ex.I, top_k), dtype=torch.uint8, device=x.device)
+    y = torch.empty((T, H), dtype=x.dtype, device=x.device)
+    ids = torch.empty((T, top_k), dtype=torch.int32, device=x.device)
+    w = torch.empty((T, top_k), dtype=torch.float32, device=x.device)
+    (gc, gs, gb), (uc, us, ub), (dc, ds, db) = ex.gate, ex.up, ex.down
+    rc = L.ishz_moe_swiglu_affine(ptr(x), DTYPES.get(x.dtype, -1), T, H, ptr(logits), ex.E, top_k, int(normalize),
+                                  ptr(gc), ptr(gs), ptr(gb), ptr(uc), ptr(us), ptr(ub), ptr(dc), ptr(ds), ptr(db),
+                                  DTYPES.get(gs.dtype, -1), ex.bits, ex.group, ex.I, ptr(y), ptr(ids), ptr(w),
+                                  ptr(ws), ws.numel(), stream())
+    if not _lib.check(rc, "moe_swiglu_affine"):
         return None
     return (y, ids, w) if return_routing else y

@@ -113,3 +113,53 @@ def test_declines():
     _, ex = experts(4, 256, 256, seed=1)
     x = torch.zeros((2, 256), dtype=torch.float32, device=DEV)
     assert moe.swiglu(x, torch.zeros((2, 4), device=DEV), ex, top_k=2) is None   # fp32 x
+
+
+def affine_experts(E, H, I, bits, group, seed, scale):
+    def pack(rows, K, s):
+        c, sc, b = synth.affine_pack_bits(E * rows, K, bits, group=group, seed=s, scale=scale)
+        return c, sc, b
+    packs = [pack(I, H, seed), pack(I, H, seed + 1), pack(H, I, seed + 2)]
+    dev = lambda a: torch.from_numpy(a).to(DEV)
+    tens = [(dev(c.view(np.int32)), dev(sc), dev(b)) for c, sc, b in packs]
+    return packs, moe.AffineExperts(tens[0], tens[1], tens[2], bits, group, E, H, I)
+
+
+def affine_moe_reference(x, rid, rw, packs, E, H, I, bits, group):
+    """The oracle's MoE formula (ishzo_moe_swiglu: fp16 projection outputs, fp16 SwiGLU ops, fp32
+    weighted sum in slot order, narrowed once) over affine weights from the oracle's dequantizer."""
+    r16 = lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+    (gc, gs, gb), (uc, us, ub), (dc, ds, db) = packs
+    deq = lambda c, s, b, rows, K: oracle.affine_dequant(c, s.view(np.uint16), b.view(np.uint16), E * rows, K, bits,
+                                                         group).reshape(E, rows, K)
+    Wg, Wu, Wd = deq(gc, gs, gb, I, H), deq(uc, us, ub, I, H), deq(dc, ds, db, H, I)
+    T, k = rid.shape
+    y = np.zeros((T, H), np.float32)
+    for t in range(T):
+        acc = np.zeros(H, np.float32)
+        for s in range(k):
+            e = rid[t, s]
+            g = r16(Wg[e] @ x[t]); u = r16(Wu[e] @ x[t])
+            sg = r16(1.0 / (1.0 + np.exp(-g)))
+            h = r16(r16(g * sg) * u)
+            o = r16(Wd[e] @ h)
+            acc = (acc + o * np.float32(rw[t, s])).astype(np.float32)
+        y[t] = r16(acc)
+    return y
+
+
+@pytest.mark.parametrize("bits,group,T", [(4, 64, 1), (4, 128, 5), (8, 64, 3), (4, 64, 20)])
+def test_swiglu_affine_experts(bits, group, T):
+    """StackedExperts as MLX affine packs (the reference's expert format), 4 and 8 bits."""
+    E, H, I, k = 16, 512, 256, 4
+    packs, ex = affine_experts(E, H, I, bits, group, seed=bits * 10 + T, scale=0.01 if bits == 4 else 0.0008)
+    x = synth.fp16_normal((T, H), seed=T + 70)
+    logits = np.random.default_rng(T + 71).standard_normal((T, E)).astype(np.float32)
+    y, ids, w = moe.swiglu_affine(torch.from_numpy(x).to(DEV), torch.from_numpy(logits).to(DEV), ex, top_k=k,
+                                  return_routing=True)
+    assert y is not None
+    rid, rw = oracle.moe_route(logits, k)
+    assert np.array_equal(ids.cpu().numpy(), rid)
+    ref = affine_moe_reference(x.astype(np.float32), rid, rw, packs, E, H, I, bits, group)
+    assert np.isfinite(ref).all()
+    assert_close(y.float().cpu().numpy(), ref, what=f"moe affine bits={bits} g={group} T={T}")
