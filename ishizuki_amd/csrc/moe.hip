@@ -677,10 +677,54 @@ struct VMoeDownA : VMoeDown {
   DEV AffRow arow(const Group &gp, int row) const { return d.row((size_t)gp.e * H + row); }
 };
 
+// One or two tokens: the gathered GEMVs with affine rows.
+template <class F>
+struct FMoeGateUpA : FMoeGateUp<F> {
+  struct Args : FMoeGateUp<F>::Args {
+    AffPack g, u;
+  };
+  static DEV auto load(const Args &a, int row, int u) {
+    const int p = __builtin_amdgcn_readfirstlane(row) / (2 * a.I);
+    const int e = a.ids[p], j = row - p * 2 * a.I;
+    return F::load_unit(j < a.I ? a.g.row((size_t)e * a.I + j) : a.u.row((size_t)e * a.I + j - a.I), u);
+  }
+};
+template <class F>
+struct FMoeDownA : FMoeDown<F> {
+  struct Args : FMoeDown<F>::Args {
+    AffPack d;
+  };
+  static DEV auto load(const Args &a, int row, int u) {
+    const int p = __builtin_amdgcn_readfirstlane(row) / a.H;
+    return F::load_unit(a.d.row((size_t)a.ids[p] * a.H + (row - p * a.H)), u);
+  }
+};
+
 template <class F>
 static int moe_ffn_affine(const void *x, int T, int H, int E, int I, int k, const AffPack &gate, const AffPack &up,
-                          const AffPack &down, MoeRoute R, uint16_t *h, uint16_t *o, void *y, hipStream_t st) {
+                          const AffPack &down, MoeRoute R, uint16_t *h, uint16_t *gu, uint16_t *o, void *y,
+                          hipStream_t st) {
   const int amax = std::min(E, T * k);
+  const size_t total = (size_t)T * H;
+  if (gathered_gemv(T, H, I, k)) {  // as moe_ffn: every (token, slot) pair a GEMV, two launches
+    const int P = T * k;
+    typename FMoeGateUpA<F>::Args ga{};
+    static_cast<typename FMoeGateUp<F>::Args &>(ga) =
+        typename FMoeGateUp<F>::Args{nullptr, nullptr, 0, H, P * 2 * I, I, k, R.ids};
+    ga.g = gate;
+    ga.u = up;
+    int rc = launch_gemv<FMoeGateUpA<F>>(ga, x, gu, st);
+    if (rc) return rc;
+    typename FMoeDownA<F>::Args da{};
+    static_cast<typename FMoeDown<F>::Args &>(da) = typename FMoeDown<F>::Args{nullptr, 0, I, P * H, H, R.ids};
+    da.d = down;
+    rc = launch_gemv<FMoeDownA<F>>(da, gu, o, st);
+    if (rc) return rc;
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)std::min<size_t>((total + 255) / 256, 4096)), dim3(256), 0,
+                       st, o, H, T, k, R, false, (uint16_t *)y);
+    ISHZ_LAUNCH_CHECK("moe combine launch");
+    return ISHZ_OK;
+  }
   const int tiles_gu = 2 * ((I + 15) / 16), tiles_dn = (H + 15) / 16;
   const int act = std::min(amax, 128);
   auto pick = [&](int tiles, int even) {
@@ -688,18 +732,17 @@ static int moe_ffn_affine(const void *x, int T, int H, int E, int I, int k, cons
     if (even) t = std::max(2, t & ~1);
     return t;
   };
-  VMoeGateUpA gu{};
-  static_cast<VMoeGateUp &>(gu) = VMoeGateUp{(const uint16_t *)x, nullptr, nullptr, 0, H, I, R, h};
-  gu.g = gate;
-  gu.u = up;
-  int rc = moe_vgemm<F>(gu, T, E, k, H, tiles_gu * 16, amax, pick(tiles_gu, 1), st);
+  VMoeGateUpA pgu{};
+  static_cast<VMoeGateUp &>(pgu) = VMoeGateUp{(const uint16_t *)x, nullptr, nullptr, 0, H, I, R, h};
+  pgu.g = gate;
+  pgu.u = up;
+  int rc = moe_vgemm<F>(pgu, T, E, k, H, tiles_gu * 16, amax, pick(tiles_gu, 1), st);
   if (rc) return rc;
   VMoeDownA dn{};
   static_cast<VMoeDown &>(dn) = VMoeDown{h, nullptr, 0, I, H, R, o};
   dn.d = down;
   rc = moe_vgemm<F>(dn, T, E, k, I, H, amax, pick(tiles_dn, 0), st);
   if (rc) return rc;
-  const size_t total = (size_t)T * H;
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)std::min<size_t>((total + 255) / 256, 4096)), dim3(256), 0,
                      st, o, H, T, k, R, true, (uint16_t *)y);
   ISHZ_LAUNCH_CHECK("moe combine launch");
@@ -783,16 +826,17 @@ extern "C" int ishz_moe_swiglu_affine(const void *x, int x_dtype, int T, int H, 
   R.ids_out = ids_out;
   R.w_out = weights_out;
   hipStream_t st = S(stream);
-  int rc = moe_route_all(logits, T, E, topk, normalize, R, true, st);
+  int rc = moe_route_all(logits, T, E, topk, normalize, R, !gathered_gemv(T, H, I, topk), st);
   if (rc) return rc;
   uint16_t *h = (uint16_t *)((uint8_t *)workspace + L.h), *o = (uint16_t *)((uint8_t *)workspace + L.o);
+  uint16_t *gu = (uint16_t *)((uint8_t *)workspace + L.gu);
   const AffPack gp{gate_codes, (const uint16_t *)gate_scales, (const uint16_t *)gate_biases, H * bits / 32, H / group};
   const AffPack upk{up_codes, (const uint16_t *)up_scales, (const uint16_t *)up_biases, H * bits / 32, H / group};
   const AffPack dp{down_codes, (const uint16_t *)down_scales, (const uint16_t *)down_biases, I * bits / 32, I / group};
   const bool bf = scale_dtype == ISHZ_DT_BF16;
 #define ISHZ_MA(B, G)                                                                                        \
-  return bf ? moe_ffn_affine<FAffineN<B, G, true>>(x, T, H, E, I, topk, gp, upk, dp, R, h, o, y, st)       \
-            : moe_ffn_affine<FAffineN<B, G, false>>(x, T, H, E, I, topk, gp, upk, dp, R, h, o, y, st)
+  return bf ? moe_ffn_affine<FAffineN<B, G, true>>(x, T, H, E, I, topk, gp, upk, dp, R, h, gu, o, y, st)   \
+            : moe_ffn_affine<FAffineN<B, G, false>>(x, T, H, E, I, topk, gp, upk, dp, R, h, gu, o, y, st)
   if (bits == 4) {
     if (group == 64) ISHZ_MA(4, 64);
     ISHZ_MA(4, 128);

@@ -148,7 +148,7 @@ def affine_moe_reference(x, rid, rw, packs, E, H, I, bits, group):
     return y
 
 
-@pytest.mark.parametrize("bits,group,T", [(4, 64, 1), (4, 128, 5), (8, 64, 3), (4, 64, 20)])
+@pytest.mark.parametrize("bits,group,T", [(4, 64, 1), (8, 128, 2), (4, 128, 5), (8, 64, 3), (4, 64, 20)])
 def test_swiglu_affine_experts(bits, group, T):
     """StackedExperts as MLX affine packs (the reference's expert format), 4 and 8 bits."""
     E, H, I, k = 16, 512, 256, 4
