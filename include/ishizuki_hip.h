@@ -50,6 +50,12 @@ const char *ishz_last_error(void);
 /* ABI version of this library (major * 100 + minor). */
 int ishz_version(void);
 
+/* Measurement utility, no counterpart in the reference: a plain streaming read of `bytes`
+ * (a multiple of 16) on `stream`, for timing the practical read ceiling of a weight matrix's
+ * size beside the quantized matmuls. `sink` is a 4-byte device buffer it practically never
+ * writes. */
+int ishz_stream_read(const void *p, size_t bytes, void *sink, ishz_stream_t stream);
+
 /* GGMLType.blockSize / typeSize (Config/GGUFFile.swift:44-80) for the types this library
    decodes (GGMLDequant.supported, Core/GGMLDequant.swift:19-24, plus Q4_0); 0 for any other
    type (ishz_ggml_geometry covers every GGMLType). */

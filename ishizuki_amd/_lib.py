@@ -17,6 +17,7 @@ P, I, U32, SZ, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, ctypes.c_size
 _SIGS = {
     "ishz_last_error": (ctypes.c_char_p, []),
     "ishz_version": (I, []),
+    "ishz_stream_read": (I, [P, SZ, P, P]),
     "ishz_ggml_block_size": (I, [U32]),
     "ishz_ggml_type_size": (I, [U32]),
     "ishz_ggml_matvec": (I, [U32, P, I, I, I, P, SZ, I, P, P]),

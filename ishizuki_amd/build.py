@@ -4,7 +4,7 @@ Every .hip file under csrc/ is compiled with hipcc (and every .cpp, host-only, w
 object in parallel, then linked. hipcc flags:
   --offload-arch=gfx950                         CDNA4 only
   -Xclang -target-feature -Xclang -packed-fp32-ops   no packed fp32 instructions
-  -O3 -fPIC -std=c++17
+  -O3 -fPIC -std=c++20 (g++ -std=c++17 for the host-only GGUF reader)
 """
 import concurrent.futures
 import glob

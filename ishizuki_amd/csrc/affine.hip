@@ -134,7 +134,6 @@ struct FAffine {
     const float *signs;
     int block;  // Hadamard block (0: x is not rotated)
     int K, N;
-    const u4 *img;  // x already staged by affine_prestage_kernel (the LDS image), or null
   };
   struct Raw {
     u4 q;
@@ -142,12 +141,15 @@ struct FAffine {
   };
   struct LaneC {};
   static constexpr int R = 8, Q = 2, MAXB = 5, PREFB = 2, DEPTH = 2, GRID_ENTRIES = 0;
+  // 512 threads: eight waves share one staged (and rotated) x, so at most two 512-element
+  // rotation passes per wave at K = 5120.
+  static constexpr int WG = 512;
   static __host__ __device__ int units(int K) { return K / 64; }
   // 16-byte words of the staged x: slots, then the two sums per unit.
   static __host__ __device__ int img_words(int K) { return (units(K) + 15) / 16 * (16 * R + 4 * Q); }
-  // Resident waves per SIMD the grid is sized for: with a prestaged x, many short waves balance
-  // the SIMDs best; staging in-kernel favours fewer, longer waves.
-  static int occ(const Args &a) { return a.img ? 4 : 2; }
+  // Resident waves per SIMD the grid is sized for: with a plain x copy, many short waves balance
+  // the SIMDs best; rotating x while staging favours fewer, longer waves.
+  static int occ(const Args &a) { return a.block > 0 ? 2 : 4; }
   // Blocks above 128 are rotated in an LDS copy of x (one fp32 per element).
   static size_t extra_lds_bytes(const Args &a) { return a.block > 128 ? (size_t)a.K * 4 : 0; }
   static DEV LaneC lane(int) { return {}; }
@@ -324,26 +326,11 @@ struct FAffine {
 
   static DEV XPre stage_load(const Args &a, const uint16_t *x, int) {
     XPre p{};
-    if (a.img) {
-      const int n = img_words(a.K);
-#pragma unroll
-      for (int j = 0; j < PF; j++) p.xv[j] = a.img[min((int)threadIdx.x + j * (int)blockDim.x, n - 1)];
-      return p;
-    }
     if (a.block > 128) return p;
     return load_group(a, x, threadIdx.x >> 6, blockDim.x >> 6);
   }
   static DEV void stage(const Args &a, const uint16_t *x, u4 *xs, float *xsum, u4 *extra, int, const XPre &pre) {
     const int lane = threadIdx.x & 63, wave = wave_id(), nw = blockDim.x >> 6;
-    if (a.img) {  // xs and xsum are contiguous, laid out as the image
-      const int n = img_words(a.K), bd = blockDim.x;
-#pragma unroll
-      for (int j = 0; j < PF; j++)
-        if ((int)threadIdx.x + j * bd < n) xs[threadIdx.x + j * bd] = pre.xv[j];
-      for (int i = threadIdx.x + PF * bd; i < n; i += bd) xs[i] = a.img[i];
-      __syncthreads();
-      return;
-    }
     if (a.block > 128) {
       uint16_t *xh = (uint16_t *)xs;
       float *xr = (float *)extra;
@@ -692,12 +679,12 @@ __global__ __launch_bounds__(64) void affine_prestage_kernel(FAffine<64, false>:
 template <int GS>
 static int affine_gemv(const void *x, const float *signs, int block, const uint32_t *codes,
                        const void *scales, const void *biases, int bf16s, int K, int N, void *y,
-                       hipStream_t st, const u4 *img = nullptr) {
+                       hipStream_t st) {
   if (bf16s) {
-    const typename FAffine<GS, true>::Args a{codes, (const uint16_t *)scales, (const uint16_t *)biases, signs, block, K, N, img};
+    const typename FAffine<GS, true>::Args a{codes, (const uint16_t *)scales, (const uint16_t *)biases, signs, block, K, N};
     return launch_gemv<FAffine<GS, true>>(a, x, y, st);
   }
-  const typename FAffine<GS, false>::Args a{codes, (const uint16_t *)scales, (const uint16_t *)biases, signs, block, K, N, img};
+  const typename FAffine<GS, false>::Args a{codes, (const uint16_t *)scales, (const uint16_t *)biases, signs, block, K, N};
   return launch_gemv<FAffine<GS, false>>(a, x, y, st);
 }
 
@@ -834,7 +821,8 @@ extern "C" int ishz_affine_matmul(const void *x, int x_dtype, int M, int K, cons
 }
 
 // Room for the rotated activations (fp16, general path) or every row's staged x image (what the
-// GEMV and verify workgroups copy; a null or smaller workspace stages x in every workgroup).
+// verify workgroups copy; a null or smaller workspace stages x in every workgroup). One row needs
+// none: the GEMV rotates and stages x in each workgroup.
 extern "C" size_t ishz_affine_workspace_size(int M, int K) {
   if (K <= 0 || M <= 0) return 0;
   return std::max((size_t)M * K * 2, (size_t)M * FAffine<64, false>::img_words(K) * 16);
@@ -858,16 +846,6 @@ extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, cons
     if (rc) return rc;
     return affine_nbit_dispatch(workspace, M, K, codes, scales, biases, bf16s, N, bits, group, y, st);
   }
-  if (M == 1 && block > 0 && block <= 128 && workspace && workspace_bytes >= ishz_affine_workspace_size(1, K) &&
-      !getenv("ISHZ_M1_MFMA")) {
-    const FAffine<64, false>::Args a{codes, nullptr, nullptr, signs, block, K, N, nullptr};
-    const int npass = (K + 511) / 512;
-    hipLaunchKernelGGL(affine_prestage_kernel, dim3(npass), dim3(64), 0, st, a, (const uint16_t *)x, (u4 *)workspace);
-    ISHZ_LAUNCH_CHECK("affine prestage launch");
-    const u4 *img = (const u4 *)workspace;
-    return group == 64 ? affine_gemv<64>(x, signs, block, codes, scales, biases, bf16s, K, N, y, st, img)
-                       : affine_gemv<128>(x, signs, block, codes, scales, biases, bf16s, K, N, y, st, img);
-  }
   if (block == 0 || (M == 1 && !getenv("ISHZ_M1_MFMA")))
     return affine_dispatch(x, M, K, signs, block, codes, scales, biases, bf16s, N, group, y, st);
   if (block <= 128 && K % 256 == 0 && !getenv("ISHZ_OLD_VERIFY")) {
@@ -875,7 +853,7 @@ extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, cons
     // fused into each workgroup's staging
     const u4 *img = nullptr;
     if (workspace && workspace_bytes >= ishz_affine_workspace_size(M, K)) {
-      const FAffine<64, false>::Args a{codes, nullptr, nullptr, signs, block, K, N, nullptr};
+      const FAffine<64, false>::Args a{codes, nullptr, nullptr, signs, block, K, N};
       hipLaunchKernelGGL(affine_prestage_kernel, dim3((K + 511) / 512, M), dim3(64), 0, st, a, (const uint16_t *)x,
                          (u4 *)workspace);
       ISHZ_LAUNCH_CHECK("affine prestage launch");

@@ -69,8 +69,16 @@ __host__ __device__ int gemv_nx(const typename F::Args &a) {
   else return 1;
 }
 
+// Threads per workgroup: F::WG where the format sets it (the workgroup shares one staged copy of
+// x, so a larger one stages fewer copies, each with more waves), else 256.
+template <class F>
+__host__ __device__ constexpr int gemv_threads() {
+  if constexpr (requires { F::WG; }) return F::WG;
+  else return 256;
+}
+
 template <class F, int LPR, int B, int D, bool RAGGED>
-__global__ __launch_bounds__(256) void gemv_kernel(typename F::Args args, const uint16_t *__restrict__ x,
+__global__ __launch_bounds__(gemv_threads<F>()) void gemv_kernel(typename F::Args args, const uint16_t *__restrict__ x,
                                                    uint16_t *__restrict__ y, int nwaves) {
   static_assert(LPR % 16 == 0, "lanes per row must be a multiple of 16");
   extern __shared__ __align__(16) uint32_t smem[];
@@ -201,14 +209,15 @@ static int launch_gemv_kd(const typename F::Args &a, const void *x, void *y, hip
   const size_t lds = gemv_nx<F>(a) * (ug * 16 * F::R * 16 + ug * 16 * F::Q * 4) + F::extra_lds_bytes(a);
   if (lds > 160 * 1024) return decline("K too large for the GEMV's LDS copy of x");
   auto kern = gemv_kernel<F, LPR, B, D, RAGGED>;
-  int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds) != hipSuccess || per_cu < 1)
+  constexpr int NT = gemv_threads<F>(), WPG = NT / 64;
+  int per_cu = 0;  // workgroups per CU, so per_cu * WPG / 4 waves per SIMD
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, NT, lds) != hipSuccess || per_cu < 1)
     per_cu = 1;
   const int groups = (a.N + RPW - 1) / RPW;
   const int occ = gemv_occ_override() > 0 ? gemv_occ_override() : F::occ(a);
-  const int capacity = gemv_num_cu() * 4 * std::min(occ, per_cu);
+  const int capacity = gemv_num_cu() * 4 * std::min(occ, std::max(per_cu * WPG / 4, 1));
   const int waves = std::min(capacity, groups);  // one resident round, groups spread evenly
-  hipLaunchKernelGGL(kern, dim3((waves + 3) / 4), dim3(256), lds, st, a, (const uint16_t *)x, (uint16_t *)y,
+  hipLaunchKernelGGL(kern, dim3((waves + WPG - 1) / WPG), dim3(NT), lds, st, a, (const uint16_t *)x, (uint16_t *)y,
                      waves);
   ISHZ_LAUNCH_CHECK("gemv launch");
   return ISHZ_OK;
