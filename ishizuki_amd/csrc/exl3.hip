@@ -277,16 +277,42 @@ __global__ __launch_bounds__(1024) void exl3_mm2(const uint16_t *__restrict__ xh
   }
 }
 
+// The 128-point Walsh-Hadamard transform of one block held as two values per lane (lane l holds
+// entries 2l, 2l + 1), in Sylvester order, scaled by 1 / sqrt(128): the in-lane pair first, then
+// one cross-lane exchange per bit of the lane index. The rotation kernel and the matvec's fused
+// input rotation both use it, so their results are bit-identical.
+DEV void wht128_pair(float &v0, float &v1, int lane) {
+  float a = v0 + v1, b = v0 - v1;
+  v0 = a;
+  v1 = b;
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const float p0 = __shfl_xor(v0, m, 64), p1 = __shfl_xor(v1, m, 64);
+    const bool hi = (lane & m) != 0;
+    v0 = hi ? p0 - v0 : v0 + p0;
+    v1 = hi ? p1 - v1 : v1 + p1;
+  }
+  const float r = 0.08838834764831845f;  // 1 / sqrt(128)
+  v0 *= r;
+  v1 *= r;
+}
+
 // Wide-step matvec / verify for the integer rates of 1, 2 and 4 bits: a wave's step is TN = 32/KA
 // adjacent column tiles of one K tile (1 KB contiguous), fetched with one 128-bit load per lane
 // and spread through LDS, so each wave keeps kilobytes in flight instead of the few hundred
 // bytes that per-lane word loads give. Lanes decode as in exl3_mm2 (32-bit windows, pairwise
 // codebook). The K tiles split over workgroups (blockIdx.y) and over a workgroup's waves; partial
 // outputs are summed into yh with atomic adds (yh zeroed first), in no fixed order.
-template <int KA, int CB, bool MF, int D>
+//
+// ROT (M = 1): xh is the unrotated x and suh its input scales; each workgroup rotates the 128-point
+// blocks that cover its K tiles into LDS (after its first weight loads are issued) and reads x
+// there, in place of a separate rotation launch.
+template <int KA, int CB, bool MF, int D, bool ROT = false>
 __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh, int M, int K,
                                                const uint32_t *__restrict__ trellis, int N,
-                                               float *__restrict__ yh, int tk_per_wg, int part) {
+                                               float *__restrict__ yh, int tk_per_wg, int part,
+                                               const uint16_t *__restrict__ suh = nullptr) {
+  static_assert(!(ROT && MF), "the fused input rotation is the one-row kernel's");
   using TR = Trellis<KA, false>;
   using T32 = Trellis32<KA, false>;
   constexpr int TN = 32 / KA, W = TR::WORDS;  // TN tiles of W words = 256 words per step
@@ -312,8 +338,10 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
   auto load = [&](int i, Raw &r) {
     const int tk = tk0 + wave + KS * min(i, nsteps - 1);
     r.w = *(const u4 *)(base + tk * tstride);
-    r.xa = *(const uint32_t *)(xr + 16 * tk);
-    r.xb = *(const uint32_t *)(xr + 16 * tk + 8);
+    if constexpr (!ROT) {
+      r.xa = *(const uint32_t *)(xr + 16 * tk);
+      r.xb = *(const uint32_t *)(xr + 16 * tk + 8);
+    }
   };
   using Acc = typename std::conditional<MF, f4, float>::type;
   Acc acc[TN];
@@ -324,13 +352,34 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
 #pragma unroll
     for (int d = 0; d < D - 1; d++) load(d, ring[d]);
   }
+  // ROT: x of this workgroup's K range, rotated, at xl[k - kb0] (fp16, as the rotation kernel
+  // rounds it); every wave takes whole 128-blocks
+  const int kb0 = (tk0 * 16) & ~127;
+  const uint16_t *xl = (const uint16_t *)(red + KS * TN * 16);
+  if constexpr (ROT) {
+    uint16_t *xw = (uint16_t *)(red + KS * TN * 16);
+    const int kb1 = min((tk1 * 16 + 127) & ~127, K);
+    for (int b = kb0 + 128 * wave; b < kb1; b += 128 * KS) {
+      const int c = b + 2 * lane;
+      float v0 = h2f(xh[c]) * h2f(suh[c]), v1 = h2f(xh[c + 1]) * h2f(suh[c + 1]);
+      wht128_pair(v0, v1, lane);
+      xw[c - kb0] = f2h(v0);
+      xw[c - kb0 + 1] = f2h(v1);
+    }
+    __syncthreads();
+  }
   for (int i0 = 0; i0 < nsteps; i0 += D) {
 #pragma unroll
     for (int d = 0; d < D; d++) {
       const int i = i0 + d;
       if (i >= nsteps) break;
       load(i + D - 1, ring[(d + D - 1) % D]);
-      const Raw &r = ring[d];
+      Raw &r = ring[d];
+      if constexpr (ROT) {
+        const int xo = 16 * (tk0 + wave + KS * i) - kb0 + 2 * g;
+        r.xa = *(const uint32_t *)(xl + xo);
+        r.xb = *(const uint32_t *)(xl + xo + 8);
+      }
       *(u4 *)(stage + 4 * lane) = r.w;  // the wave's own buffer: its LDS operations stay in order
       constexpr bool HALVES = !MF && CB != 2;
       uint32_t xd[4];  // (x, x) pairs for the halves form
@@ -476,19 +525,7 @@ __global__ __launch_bounds__(256) void exl3_rotate_kernel(const void *__restrict
     v0 *= h2f(scales[col]);
     v1 *= h2f(scales[col + 1]);
   }
-  float a = v0 + v1, b = v0 - v1;
-  v0 = a;
-  v1 = b;
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    const float p0 = __shfl_xor(v0, m, 64), p1 = __shfl_xor(v1, m, 64);
-    const bool hi = (lane & m) != 0;
-    v0 = hi ? p0 - v0 : v0 + p0;
-    v1 = hi ? p1 - v1 : v1 + p1;
-  }
-  const float r = 0.08838834764831845f;  // 1 / sqrt(128)
-  v0 *= r;
-  v1 *= r;
+  wht128_pair(v0, v1, lane);
   if (!before) {
     v0 *= h2f(scales[col]);
     v1 *= h2f(scales[col + 1]);
@@ -590,8 +627,10 @@ static int exl3_splits(int M, int K, int tn_blocks) {
 // The matvec. With `part` (a buffer of exl3_splits(..) * M * N floats) the wide-step kernel writes
 // each K split's partial product to its own slice and *nparts says how many; otherwise yh is the
 // result (zeroed, then summed into with atomics) and *nparts = 1.
+// With `suh` (M = 1, exl3_fused_rotation(..) true) xh is the unrotated x and the wide-step kernel
+// rotates it itself.
 static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis, int N, int bits2, int codebook,
-                            float *yh, float *part, int *nparts, hipStream_t st) {
+                            float *yh, float *part, int *nparts, hipStream_t st, const uint16_t *suh = nullptr) {
   *nparts = 1;
   const int wgs = N / 16, tiles_k = K / 16;
   int ks = 1;
@@ -610,9 +649,13 @@ static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis
         else
           hipLaunchKernelGGL(exl3_zero_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 1024)), dim3(256), 0,
                              st, yh, n);
-        const size_t lds = (size_t)KS3 * 256 * 4 + (M == 1 ? (size_t)KS3 * TN * 16 * 4 : (size_t)TN * 256 * 4);
+        const size_t lds = (size_t)KS3 * 256 * 4 + (M == 1 ? (size_t)KS3 * TN * 16 * 4 : (size_t)TN * 256 * 4) +
+                           (suh ? (size_t)(per * 16 + 256) * 2 : 0);  // ROT: the rotated K range of x
         auto go = [&]<int CB>() -> int {
-          if (M == 1)
+          if (M == 1 && suh)
+            hipLaunchKernelGGL((exl3_mm3<KA, CB, false, D, true>), dim3(tn_blocks, nsplit), dim3(64 * KS3), lds, st,
+                               (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per, part ? 1 : 0, suh);
+          else if (M == 1)
             hipLaunchKernelGGL((exl3_mm3<KA, CB, false, D>), dim3(tn_blocks, nsplit), dim3(64 * KS3), lds, st,
                                (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per, part ? 1 : 0);
           else
@@ -625,6 +668,7 @@ static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis
                              : codebook == 1 ? go.template operator()<1>() : go.template operator()<2>();
       }
     }
+    if (suh) return einval("the fused input rotation needs the wide-step kernel");
     if constexpr (Trellis32<KA, HALF>::FITS) {
       if (!getenv("ISHZ_EXL3_OLD")) {
         // TN = 4 column tiles per workgroup (N % 128 == 0 makes N / 16 a multiple of 8); 8 waves
@@ -676,6 +720,13 @@ extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const
   return exl3_matvec_core(xh, M, K, trellis, N, bits2, codebook, yh, nullptr, &np, S(stream));
 }
 
+// Whether exl3_matvec_core takes the wide-step kernel for one row, which can rotate x itself.
+static bool exl3_fused_rotation(int M, int N, int bits2) {
+  static const bool off = getenv("ISHZ_EXL3_OLD") || getenv("ISHZ_EXL3_MM2");
+  const int KA = bits2 / 2;
+  return M == 1 && !off && (bits2 == 2 || bits2 == 4 || bits2 == 8) && (N / 16) % (32 / KA) == 0;
+}
+
 // x rotated (fp16), then the matvec's K-split partials (fp32 [splits][M][N], splits bounded by
 // the widest column step of any rate, 32 tiles).
 extern "C" size_t ishz_exl3_workspace_size(int M, int K, int N) {
@@ -696,9 +747,13 @@ extern "C" int ishz_exl3_apply(const void *x, int x_dtype, int M, int K, const i
     return einval("workspace too small (ishz_exl3_workspace_size)");
   uint16_t *xh = (uint16_t *)workspace;
   float *yh = (float *)((uint8_t *)workspace + ((size_t)M * K * 2 + 255) / 256 * 256);
-  if ((rc = ishz_exl3_rotate(x, ISHZ_DT_F16, M, K, suh, 1, xh, ISHZ_DT_F16, stream))) return rc;
   int np = 1;
-  if ((rc = exl3_matvec_core(xh, M, K, trellis, N, bits2, codebook, yh, yh, &np, S(stream)))) return rc;
+  if (exl3_fused_rotation(M, N, bits2)) {  // one row: the matvec rotates its own K range of x
+    if ((rc = exl3_matvec_core(x, M, K, trellis, N, bits2, codebook, yh, yh, &np, S(stream), suh))) return rc;
+  } else {
+    if ((rc = ishz_exl3_rotate(x, ISHZ_DT_F16, M, K, suh, 1, xh, ISHZ_DT_F16, stream))) return rc;
+    if ((rc = exl3_matvec_core(xh, M, K, trellis, N, bits2, codebook, yh, yh, &np, S(stream)))) return rc;
+  }
   const size_t blocks = (size_t)M * (N / 128);  // output rotation, summing the K-split partials
   hipLaunchKernelGGL(exl3_rotate_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, S(stream), yh,
                      ISHZ_DT_F32, blocks, N, svh, 0, y, ISHZ_DT_F16, np);

@@ -99,6 +99,20 @@ def test_apply_matches_oracle(M):
     assert_close(y.float().cpu().numpy(), ref, what=f"exl3 apply M={M}")
 
 
+@pytest.mark.parametrize("K", [128, 1152, 5120])
+@pytest.mark.parametrize("bits2,cb", [(2, 0), (4, 1), (8, 2), (4, 0)])
+def test_apply_fused_input_rotation(K, bits2, cb):
+    """M = 1 with N a whole number of wide steps: the matvec rotates x itself (every workgroup its
+    own 128-blocks, K ranges that start and end inside a block at K = 1152), no rotation launch."""
+    N = 512
+    t, suh, svh, ten = make(K, N, bits2, cb, seed=K + bits2 + cb)
+    x = synth.fp16_normal((1, K), seed=K + 7)
+    ref = oracle.exl3_apply(x.astype(np.float32), t, suh, svh, bits2, cb)
+    y = exl3.apply(torch.from_numpy(x).to(DEV), ten)
+    assert y is not None
+    assert_close(y.float().cpu().numpy(), ref, what=f"exl3 apply fused rotation K={K} bits2={bits2} cb={cb}")
+
+
 @pytest.mark.parametrize("name,cb", [("qwen3", 0), ("qwen38", 2)])
 def test_projection_reproduces_checkpoint(golden_exl3, name, cb):
     # EXL3Tests.projectionMatchesCheckpoint (:74-98): rel-L2 < 0.12 against the fp16 checkpoint.
