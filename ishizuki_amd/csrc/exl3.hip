@@ -304,15 +304,14 @@ DEV void wht128_pair(float &v0, float &v1, int lane) {
 // codebook). The K tiles split over workgroups (blockIdx.y) and over a workgroup's waves; partial
 // outputs are summed into yh with atomic adds (yh zeroed first), in no fixed order.
 //
-// ROT (M = 1): xh is the unrotated x and suh its input scales; each workgroup rotates the 128-point
-// blocks that cover its K tiles into LDS (after its first weight loads are issued) and reads x
-// there, in place of a separate rotation launch.
+// ROT: xh is the unrotated x and suh its input scales; each workgroup rotates the 128-point blocks
+// that cover its K tiles, for every row, into LDS (after its first weight loads are issued) and
+// reads x there, in place of a separate rotation launch.
 template <int KA, int CB, bool MF, int D, bool ROT = false>
 __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh, int M, int K,
                                                const uint32_t *__restrict__ trellis, int N,
                                                float *__restrict__ yh, int tk_per_wg, int part,
                                                const uint16_t *__restrict__ suh = nullptr) {
-  static_assert(!(ROT && MF), "the fused input rotation is the one-row kernel's");
   using TR = Trellis<KA, false>;
   using T32 = Trellis32<KA, false>;
   constexpr int TN = 32 / KA, W = TR::WORDS;  // TN tiles of W words = 256 words per step
@@ -354,17 +353,21 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
   }
   // ROT: x of this workgroup's K range, rotated, at xl[k - kb0] (fp16, as the rotation kernel
   // rounds it); every wave takes whole 128-blocks
-  const int kb0 = (tk0 * 16) & ~127;
-  const uint16_t *xl = (const uint16_t *)(red + KS * TN * 16);
+  // (row m at xl[m * XS + k - kb0], XS = tk_per_wg * 16 + 256 halves: the K range rounded out to
+  // whole blocks); every wave takes whole (row, block) pairs
+  const int kb0 = (tk0 * 16) & ~127, XS = tk_per_wg * 16 + 256;
+  const uint16_t *xl = (const uint16_t *)(red + (MF ? TN * 256 : KS * TN * 16));
   if constexpr (ROT) {
-    uint16_t *xw = (uint16_t *)(red + KS * TN * 16);
-    const int kb1 = min((tk1 * 16 + 127) & ~127, K);
-    for (int b = kb0 + 128 * wave; b < kb1; b += 128 * KS) {
+    uint16_t *xw = (uint16_t *)(red + (MF ? TN * 256 : KS * TN * 16));
+    const int nblk = (min((tk1 * 16 + 127) & ~127, K) - kb0) / 128;
+    for (int q = wave; q < M * nblk; q += KS) {
+      const int m = q / nblk, b = kb0 + 128 * (q % nblk);
       const int c = b + 2 * lane;
-      float v0 = h2f(xh[c]) * h2f(suh[c]), v1 = h2f(xh[c + 1]) * h2f(suh[c + 1]);
+      const uint16_t *xm = xh + (size_t)m * K;
+      float v0 = h2f(xm[c]) * h2f(suh[c]), v1 = h2f(xm[c + 1]) * h2f(suh[c + 1]);
       wht128_pair(v0, v1, lane);
-      xw[c - kb0] = f2h(v0);
-      xw[c - kb0 + 1] = f2h(v1);
+      xw[m * XS + c - kb0] = f2h(v0);
+      xw[m * XS + c - kb0 + 1] = f2h(v1);
     }
     __syncthreads();
   }
@@ -376,7 +379,7 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
       load(i + D - 1, ring[(d + D - 1) % D]);
       Raw &r = ring[d];
       if constexpr (ROT) {
-        const int xo = 16 * (tk0 + wave + KS * i) - kb0 + 2 * g;
+        const int xo = tok * XS + 16 * (tk0 + wave + KS * i) - kb0 + 2 * g;
         r.xa = *(const uint32_t *)(xl + xo);
         r.xb = *(const uint32_t *)(xl + xo + 8);
       }
@@ -627,7 +630,7 @@ static int exl3_splits(int M, int K, int tn_blocks) {
 // The matvec. With `part` (a buffer of exl3_splits(..) * M * N floats) the wide-step kernel writes
 // each K split's partial product to its own slice and *nparts says how many; otherwise yh is the
 // result (zeroed, then summed into with atomics) and *nparts = 1.
-// With `suh` (M = 1, exl3_fused_rotation(..) true) xh is the unrotated x and the wide-step kernel
+// With `suh` (exl3_fused_rotation(..) true) xh is the unrotated x and the wide-step kernel
 // rotates it itself.
 static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis, int N, int bits2, int codebook,
                             float *yh, float *part, int *nparts, hipStream_t st, const uint16_t *suh = nullptr) {
@@ -640,6 +643,7 @@ static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis
       static const bool mm2 = getenv("ISHZ_EXL3_MM2") != nullptr;
       constexpr int TN = 32 / KA, KS3 = 4, D = 4;  // a step covers TN column tiles: N must tile by them
       if (!getenv("ISHZ_EXL3_OLD") && !mm2 && (N / 16) % TN == 0) {
+        if (suh && M != 1) return einval("the fused input rotation is for one row");
         const int tn_blocks = N / 16 / TN;
         const int per = (tiles_k + exl3_splits(M, K, tn_blocks) - 1) / exl3_splits(M, K, tn_blocks);
         const int nsplit = (tiles_k + per - 1) / per;
@@ -650,7 +654,7 @@ static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis
           hipLaunchKernelGGL(exl3_zero_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 1024)), dim3(256), 0,
                              st, yh, n);
         const size_t lds = (size_t)KS3 * 256 * 4 + (M == 1 ? (size_t)KS3 * TN * 16 * 4 : (size_t)TN * 256 * 4) +
-                           (suh ? (size_t)(per * 16 + 256) * 2 : 0);  // ROT: the rotated K range of x
+                           (suh ? (size_t)M * (per * 16 + 256) * 2 : 0);  // ROT: the rotated K range of x
         auto go = [&]<int CB>() -> int {
           if (M == 1 && suh)
             hipLaunchKernelGGL((exl3_mm3<KA, CB, false, D, true>), dim3(tn_blocks, nsplit), dim3(64 * KS3), lds, st,
@@ -720,11 +724,18 @@ extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const
   return exl3_matvec_core(xh, M, K, trellis, N, bits2, codebook, yh, nullptr, &np, S(stream));
 }
 
-// Whether exl3_matvec_core takes the wide-step kernel for one row, which can rotate x itself.
-static bool exl3_fused_rotation(int M, int N, int bits2) {
+// Whether exl3_matvec_core takes the wide-step kernel, which can rotate x itself, and the
+// workgroup's rotated slice of x fits beside the kernel's own LDS. One row only: with 8 rows each
+// workgroup rotates ~8x the blocks before its first MFMA, which measured slower (17408x5120 at
+// 2 bpw: 37.8 us against 34.7 us for the separate rotation launch).
+static bool exl3_fused_rotation(int M, int K, int N, int bits2) {
   static const bool off = getenv("ISHZ_EXL3_OLD") || getenv("ISHZ_EXL3_MM2");
   const int KA = bits2 / 2;
-  return M == 1 && !off && (bits2 == 2 || bits2 == 4 || bits2 == 8) && (N / 16) % (32 / KA) == 0;
+  if (M != 1 || off || !(bits2 == 2 || bits2 == 4 || bits2 == 8) || (N / 16) % (32 / KA)) return false;
+  const int TN = 32 / KA, tiles_k = K / 16, splits = exl3_splits(M, K, N / 16 / TN);
+  const size_t per = (tiles_k + splits - 1) / splits;
+  const size_t own = 4 * 256 * 4 + (M == 1 ? (size_t)4 * TN * 16 * 4 : (size_t)TN * 256 * 4);
+  return own + (size_t)M * (per * 16 + 256) * 2 <= 120 * 1024;
 }
 
 // x rotated (fp16), then the matvec's K-split partials (fp32 [splits][M][N], splits bounded by
@@ -748,7 +759,7 @@ extern "C" int ishz_exl3_apply(const void *x, int x_dtype, int M, int K, const i
   uint16_t *xh = (uint16_t *)workspace;
   float *yh = (float *)((uint8_t *)workspace + ((size_t)M * K * 2 + 255) / 256 * 256);
   int np = 1;
-  if (exl3_fused_rotation(M, N, bits2)) {  // one row: the matvec rotates its own K range of x
+  if (exl3_fused_rotation(M, K, N, bits2)) {  // the matvec rotates its own K range of x
     if ((rc = exl3_matvec_core(x, M, K, trellis, N, bits2, codebook, yh, yh, &np, S(stream), suh))) return rc;
   } else {
     if ((rc = ishz_exl3_rotate(x, ISHZ_DT_F16, M, K, suh, 1, xh, ISHZ_DT_F16, stream))) return rc;

@@ -99,18 +99,20 @@ def test_apply_matches_oracle(M):
     assert_close(y.float().cpu().numpy(), ref, what=f"exl3 apply M={M}")
 
 
+@pytest.mark.parametrize("M", [1, 3, 16])
 @pytest.mark.parametrize("K", [128, 1152, 5120])
 @pytest.mark.parametrize("bits2,cb", [(2, 0), (4, 1), (8, 2), (4, 0)])
-def test_apply_fused_input_rotation(K, bits2, cb):
-    """M = 1 with N a whole number of wide steps: the matvec rotates x itself (every workgroup its
-    own 128-blocks, K ranges that start and end inside a block at K = 1152), no rotation launch."""
+def test_apply_fused_input_rotation(M, K, bits2, cb):
+    """N a whole number of wide steps: at M = 1 the matvec rotates x itself (every workgroup the
+    128-blocks of its K range; K ranges that start and end inside a block at K = 1152), no
+    rotation launch; M = 3 and 16 take the rotation kernel into the workspace at the same shapes."""
     N = 512
     t, suh, svh, ten = make(K, N, bits2, cb, seed=K + bits2 + cb)
-    x = synth.fp16_normal((1, K), seed=K + 7)
+    x = synth.fp16_normal((M, K), seed=K + 7 + M)
     ref = oracle.exl3_apply(x.astype(np.float32), t, suh, svh, bits2, cb)
     y = exl3.apply(torch.from_numpy(x).to(DEV), ten)
     assert y is not None
-    assert_close(y.float().cpu().numpy(), ref, what=f"exl3 apply fused rotation K={K} bits2={bits2} cb={cb}")
+    assert_close(y.float().cpu().numpy(), ref, what=f"exl3 apply fused rotation M={M} K={K} bits2={bits2} cb={cb}")
 
 
 @pytest.mark.parametrize("name,cb", [("qwen3", 0), ("qwen38", 2)])
