@@ -626,6 +626,16 @@ struct FQ6_K : GgmlGemv<FQ6_K> {
 // index, 7-bit sign index), scales u8[8] at 66. Entry l of group ib (weights 32ib + 8l + j) is
 // d*(0.5+nibble)*0.25 * grid[q&511][j] * sign(ksigns[q>>9], j), nibble = scales[ib] lo for
 // l < 2, hi otherwise.
+// IQ2_XS sign masks of one ksigns index (7 bits; the eighth sign is their parity) in the GEMV's
+// pair order (x0,x2 | x1,x3 | x4,x6 | x5,x7), sign bits at 15 and 31 of each word, computed in
+// registers instead of read from an LDS table. Word w is s * (2^a + 2^b): the two shifted copies
+// of the 8-bit s occupy disjoint bits, so the product is their OR, and bits 15 and 31 are signs
+// (0, 2), (1, 3), (4, 6), (5, 7); the caller keeps only those bits (mask 0x80008000).
+DEV u4 iq2xs_sign_words(uint32_t idx) {
+  const uint32_t s = idx | (__builtin_popcount(idx) & 1u) << 7;
+  return u4{s * 0x20008000u, s * 0x10004000u, s * 0x02000800u, s * 0x01000400u};
+}
+
 struct FIQ2_XS : GgmlGemv<FIQ2_XS> {
   static constexpr uint32_t TYPE = ISHZ_GGML_IQ2_XS;
   static constexpr int BS = 256, TS = 74, UPB = 4;  // unit: two groups, 16 B of qs, 64 weights
@@ -654,12 +664,13 @@ struct FIQ2_XS : GgmlGemv<FIQ2_XS> {
 #pragma unroll
     for (int l = 0; l < 8; l++) {
       const uint32_t q = (QS[l >> 1] >> (16 * (l & 1))) & 0xffffu;
-      const u4 G = s.grid[q & 511], M = s.sgn[q >> 9];
+      const u4 G = s.grid[q & 511], M = iq2xs_sign_words(q >> 9);
       const u4 X = s.slot(l);
-      float e = dot2(G.x ^ M.x, X.x, 0.0f);
-      e = dot2(G.y ^ M.y, X.y, e);
-      e = dot2(G.z ^ M.z, X.z, e);
-      e = dot2(G.w ^ M.w, X.w, e);
+      constexpr uint32_t SB = 0x80008000u;
+      float e = dot2(G.x ^ (M.x & SB), X.x, 0.0f);
+      e = dot2(G.y ^ (M.y & SB), X.y, e);
+      e = dot2(G.z ^ (M.z & SB), X.z, e);
+      e = dot2(G.w ^ (M.w & SB), X.w, e);
       const uint32_t nib = (r.sc >> (8 * (l >> 2) + 4 * ((l >> 1) & 1))) & 15;
       acc += (d * (0.5f + (float)nib) * 0.25f) * e;
     }
