@@ -58,6 +58,15 @@ DEV void tab_signs(u4 *dst) {
   }
 }
 
+// The same masks computed in registers (no LDS read): word w is s * (2^(15-2w) + 2^(30-2w)),
+// whose two shifted copies of the 8-bit pattern occupy disjoint bits, so bits 15 and 31 hold signs
+// 2w and 2w + 1; everything else is masked off.
+DEV u4 sign_words(uint32_t s) {
+  constexpr uint32_t SB = 0x80008000u;
+  return u4{s * 0x40008000u & SB, s * 0x10002000u & SB, s * 0x04000800u & SB, s * 0x01000200u & SB};
+}
+DEV uint32_t ksigns_pattern(uint32_t idx) { return idx | (__builtin_popcount(idx) & 1u) << 7; }
+
 // ------------------------------------------------------------------------- shared base
 template <class D>
 struct GgmlQuarter : GgmlGemv<D> {
@@ -255,7 +264,7 @@ struct FIQ2_XXS : GgmlQuarter<FIQ2_XXS> {
     for (int h = 0; h < 2; h++)
 #pragma unroll
       for (int l = 0; l < 4; l++)
-        B[4 * h + l] = t[byte_of(r.q[2 * h], l)] ^ t[256 + __builtin_amdgcn_ubfe(r.q[2 * h + 1], 7 * l, 7)];
+        B[4 * h + l] = t[byte_of(r.q[2 * h], l)] ^ sign_words(ksigns_pattern(__builtin_amdgcn_ubfe(r.q[2 * h + 1], 7 * l, 7)));
   }
   static DEV void vscale(const VRaw &r, int, int s, float &sc, float &mn) {
     sc = h2f(r.d) * (0.5f + (float)(r.q[2 * s + 1] >> 28)) * 0.25f;
@@ -293,7 +302,7 @@ struct FIQ2_S : GgmlQuarter<FIQ2_S> {
 #pragma unroll
       for (int l = 0; l < 4; l++) {
         const uint32_t idx = byte_of(r.qs[h], l) | ((qh << (8 - 2 * l)) & 0x300u);
-        B[4 * h + l] = t[idx] ^ t[1024 + byte_of(r.sg[h], l)];
+        B[4 * h + l] = t[idx] ^ sign_words(byte_of(r.sg[h], l));
       }
     }
   }
@@ -336,7 +345,7 @@ struct FIQ3_XXS : GgmlQuarter<FIQ3_XXS> {
       for (int l = 0; l < 4; l++) {
         const uint32_t w = r.q[2 * h + (l >> 1)];
         const u2 g1 = grid[byte_of(w, 2 * (l & 1))], g2 = grid[byte_of(w, 2 * (l & 1) + 1)];
-        B[4 * h + l] = u4{g1.x, g1.y, g2.x, g2.y} ^ t[__builtin_amdgcn_ubfe(r.aux[h], 7 * l, 7)];
+        B[4 * h + l] = u4{g1.x, g1.y, g2.x, g2.y} ^ sign_words(ksigns_pattern(__builtin_amdgcn_ubfe(r.aux[h], 7 * l, 7)));
       }
   }
   static DEV void vscale(const VRaw &r, int, int s, float &sc, float &mn) {
@@ -381,7 +390,7 @@ struct FIQ3_S : GgmlQuarter<FIQ3_S> {
         const uint32_t i1 = byte_of(w, 2 * (l & 1)) | ((qh << (8 - 2 * l)) & 256u);
         const uint32_t i2 = byte_of(w, 2 * (l & 1) + 1) | ((qh << (7 - 2 * l)) & 256u);
         const u2 g1 = grid[i1], g2 = grid[i2];
-        B[4 * h + l] = u4{g1.x, g1.y, g2.x, g2.y} ^ t[byte_of(r.sg[h], l)];
+        B[4 * h + l] = u4{g1.x, g1.y, g2.x, g2.y} ^ sign_words(byte_of(r.sg[h], l));
       }
     }
   }
