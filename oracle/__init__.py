@@ -38,6 +38,7 @@ def lib():
             "ishzo_half_to_float": (F, [ctypes.c_uint16]),
             "ishzo_float_to_half": (ctypes.c_uint16, [F]),
             "ishzo_dequant": (I, [U, P, SZ, SZ, P]),
+            "ishzo_dequant_rows": (I, [U, P, I, I, P, I]),
             "ishzo_ggml_matmul": (I, [U, P, I, I, P, I, P, I]),
             "ishzo_ggml_matmul_fused": (I, [U, P, I, I, P, I, P, I]),
             "ishzo_affine_dequant": (I, [P, P, P, I, I, I, I, P]),
@@ -80,6 +81,16 @@ def dequant(type_, blocks, count):
     rc = lib().ishzo_dequant(type_, _p(b), b.size, count, _p(out))
     if rc:
         raise ValueError({-1: "unsupported type", -2: "count is not whole blocks", -3: "short buffer"}[rc])
+    return out
+
+
+def dequant_rows(type_, blocks, N, K, threads=0):
+    """W [N][K] from its GGML blocks, rows decoded in parallel (ishzo_dequant per row)."""
+    b = _c(blocks, np.uint8)
+    out = np.empty((N, K), np.float32)
+    rc = lib().ishzo_dequant_rows(type_, _p(b), N, K, _p(out), threads)
+    if rc:
+        raise ValueError(f"oracle dequant failed {rc}")
     return out
 
 

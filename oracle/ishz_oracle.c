@@ -386,6 +386,22 @@ static float dot_f32(const float *a, const float *b, int K) {
   return ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
 }
 
+/* Rows of a [N][K] GGML matrix dequantized in parallel (ishzo_dequant per row). */
+int ishzo_dequant_rows(uint32_t type, const uint8_t *blocks, int N, int K, float *out, int threads) {
+  int bs = ishzo_block_size(type), ts = ishzo_type_size(type);
+  if (!bs) return -1;
+  if (K % bs) return -2;
+  size_t rb = (size_t)(K / bs) * (size_t)ts;
+  set_threads(threads);
+  int rc = 0;
+#pragma omp parallel for schedule(static)
+  for (int n = 0; n < N; n++) {
+    int r = ishzo_dequant(type, blocks + (size_t)n * rb, rb, (size_t)K, out + (size_t)n * K);
+    if (r) rc = r;
+  }
+  return rc;
+}
+
 /* Dequantize-then-dot, the reference's CPU definition (GGMLKernelTests.swift:111-140 checks
    the matvec against the expanded weight exactly this way). */
 int ishzo_ggml_matmul(uint32_t type, const float *x, int M, int K, const uint8_t *blocks, int N,
@@ -446,16 +462,19 @@ int ishzo_affine_dequant(const uint32_t *codes, const uint16_t *scales, const ui
   size_t wpr = (size_t)K * bits / 32;
   int gpr = K / group;
   uint32_t mask = (1u << bits) - 1;
+#pragma omp parallel for schedule(static)
   for (int n = 0; n < N; n++) {
     const uint32_t *row = codes + (size_t)n * wpr;
-    for (int k = 0; k < K; k++) {
-      size_t bit = (size_t)k * bits;
-      uint64_t pair = row[bit / 32];
-      if (bit / 32 + 1 < wpr) pair |= (uint64_t)row[bit / 32 + 1] << 32;
-      uint32_t q = (uint32_t)(pair >> (bit % 32)) & mask;
-      float s = ishzo_half_to_float(scales[(size_t)n * gpr + k / group]);
-      float b = ishzo_half_to_float(biases[(size_t)n * gpr + k / group]);
-      out[(size_t)n * K + k] = s * (float)q + b;
+    for (int g = 0; g < gpr; g++) {
+      float s = ishzo_half_to_float(scales[(size_t)n * gpr + g]);
+      float b = ishzo_half_to_float(biases[(size_t)n * gpr + g]);
+      for (int k = g * group; k < (g + 1) * group; k++) {
+        size_t bit = (size_t)k * bits;
+        uint64_t pair = row[bit / 32];
+        if (bit / 32 + 1 < wpr) pair |= (uint64_t)row[bit / 32 + 1] << 32;
+        uint32_t q = (uint32_t)(pair >> (bit % 32)) & mask;
+        out[(size_t)n * K + k] = s * (float)q + b;
+      }
     }
   }
   return 0;
@@ -548,6 +567,7 @@ int ishzo_exl3_dequant(const int16_t *trellis, int K, int N, int bits2, int cb, 
   int words16 = 8 * bits2; /* 16*bits int16 per tile */
   int tk_n = K / 16, tn_n = N / 16;
   static const int rmap[4] = {0, 1, 8, 9};
+#pragma omp parallel for schedule(static)
   for (int tk = 0; tk < tk_n; tk++)
     for (int tn = 0; tn < tn_n; tn++) {
       const uint16_t *t16 = (const uint16_t *)trellis + ((size_t)tk * tn_n + tn) * words16;
@@ -579,13 +599,20 @@ int ishzo_exl3_apply(const float *x, int M, int K, const int16_t *trellis, const
     ishzo_hadamard(x, M, K, 128, suh, 0, xh);
     for (size_t i = 0; i < (size_t)M * K; i++) xh[i] = round16(xh[i]);
     set_threads(threads);
-#pragma omp parallel for schedule(static)
-    for (int n = 0; n < N; n++)
-      for (int m = 0; m < M; m++) {
-        float acc = 0.0f;
-        for (int k = 0; k < K; k++) acc += xh[(size_t)m * K + k] * w[(size_t)k * N + n];
-        yh[(size_t)m * N + n] = acc;
+#pragma omp parallel
+    {
+      float *col = (float *)malloc((size_t)K * sizeof(float));
+#pragma omp for schedule(static)
+      for (int n = 0; n < N; n++) {
+        for (int k = 0; k < K; k++) col[k] = w[(size_t)k * N + n];
+        for (int m = 0; m < M; m++) {
+          float acc = 0.0f;
+          for (int k = 0; k < K; k++) acc += xh[(size_t)m * K + k] * col[k];
+          yh[(size_t)m * N + n] = acc;
+        }
       }
+      free(col);
+    }
     ishzo_hadamard(yh, M, N, 128, svh, 1, y);
     for (size_t i = 0; i < (size_t)M * N; i++) y[i] = round16(y[i]);
   }

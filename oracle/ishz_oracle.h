@@ -40,6 +40,9 @@ uint16_t ishzo_float_to_half(float f);  /* round to nearest even */
 /* 0 ok, -1 unsupported type, -2 count not whole blocks, -3 short buffer. */
 int ishzo_dequant(uint32_t type, const uint8_t *bytes, size_t nbytes, size_t count, float *out);
 
+/* Rows of W [N][K] dequantized in parallel (same values as ishzo_dequant of the whole matrix). */
+int ishzo_dequant_rows(uint32_t type, const uint8_t *blocks, int N, int K, float *out, int threads);
+
 /* y[m][n] = sum_k x[m][k] * W[n][k], W = dequant(blocks) row-major [N][K]; fp32 accumulate.
    threads <= 0 means all cores. Returns ishzo_dequant's status. */
 int ishzo_ggml_matmul(uint32_t type, const float *x, int M, int K, const uint8_t *blocks,

@@ -13,6 +13,13 @@ import oracle
 from conftest import assert_close
 from ishizuki_amd import affine, synth
 
+
+def affine_bound(xf, codes, s, b, N, K, bits, group):
+    """|x| @ |W|.T for the per-element criterion (W from the oracle's affine dequantizer)."""
+    W = oracle.affine_dequant(codes, np.asarray(s).view(np.uint16), np.asarray(b).view(np.uint16), N, K, bits, group)
+    return np.abs(np.asarray(xf, np.float32)) @ np.abs(W).T
+
+
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
@@ -49,17 +56,17 @@ def affine_case(N, K, M, group, seed, block=0, signs_seed=None):
     ref = oracle.affine_matmul(xf, codes, s.view(np.uint16), b.view(np.uint16), N, 2, group)
     dev = lambda a: torch.from_numpy(a).to(DEV)
     args = (dev(x), dev(codes.view(np.int32)), dev(s), dev(b))
-    return args, signs, ref
+    return args, signs, (ref, affine_bound(xf, codes, s, b, N, K, 2, group))
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 8, 16])
 @pytest.mark.parametrize("group", [64, 128])
 def test_affine_matmul(M, group):
     N, K = 1000, 2048
-    (x, w, s, b), _, ref = affine_case(N, K, M, group, seed=M)
+    (x, w, s, b), _, (ref, bd) = affine_case(N, K, M, group, seed=M)
     y = affine.quantized_matmul(x, w, s, b, group_size=group)
     assert y is not None
-    assert_close(y.float().cpu().numpy(), ref, what=f"affine M={M} g={group}")
+    assert_close(y.float().cpu().numpy(), ref, bound=bd, what=f"affine M={M} g={group}")
 
 
 @pytest.mark.parametrize("bits", [4, 8])
@@ -72,6 +79,7 @@ def test_affine_wide_bits(bits, M, group, bf16):
     codes, s, b = synth.affine_pack_bits(N, K, bits, group=group, seed=bits + M)
     x = synth.fp16_normal((M, K), seed=M + 40)
     ref = oracle.affine_matmul(x.astype(np.float32), codes, s.view(np.uint16), b.view(np.uint16), N, bits, group)
+    bound = affine_bound(x, codes, s, b, N, K, bits, group)
     sd, bd = torch.from_numpy(s).to(DEV), torch.from_numpy(b).to(DEV)
     if bf16:  # bf16 scales and biases (the values rounded to bf16; the reference uses them as given)
         sd, bd = sd.to(torch.bfloat16), bd.to(torch.bfloat16)
@@ -79,7 +87,7 @@ def test_affine_wide_bits(bits, M, group, bf16):
     y = affine.quantized_matmul(torch.from_numpy(x).to(DEV), torch.from_numpy(codes.view(np.int32)).to(DEV), sd, bd,
                                 group_size=group, bits=bits)
     assert y is not None
-    assert_close(y.float().cpu().numpy(), ref, what=f"affine bits={bits} M={M} g={group} bf16={bf16}")
+    assert_close(y.float().cpu().numpy(), ref, bound=bound, what=f"affine bits={bits} M={M} g={group} bf16={bf16}")
 
 
 def _ref_bf16(x, codes, sd, bd, N, K, bits, group):
@@ -103,11 +111,12 @@ def test_affine_wide_bits_rotated_linear(bits, M):
     signs = synth.hadamard_signs(K, seed=7)
     xr = oracle.hadamard(x.astype(np.float32), 128, signs).astype(np.float16).astype(np.float32)
     ref = oracle.affine_matmul(xr, codes, s.view(np.uint16), b.view(np.uint16), N, bits, 64)
+    bound = affine_bound(xr, codes, s, b, N, K, bits, 64)
     y = affine.linear(torch.from_numpy(x).to(DEV), torch.from_numpy(codes.view(np.int32)).to(DEV),
                       torch.from_numpy(s).to(DEV), torch.from_numpy(b).to(DEV), signs=torch.from_numpy(signs),
                       block=128, group_size=64, bits=bits)
     assert y is not None
-    assert_close(y.float().cpu().numpy(), ref, what=f"affine linear bits={bits} M={M}")
+    assert_close(y.float().cpu().numpy(), ref, bound=bound, what=f"affine linear bits={bits} M={M}")
 
 
 @pytest.mark.parametrize("M", [5, 8, 16])
@@ -115,20 +124,20 @@ def test_affine_verify_very_wide_output(M):
     """40000 output rows (2500 tiles, more than 16 / NQ per CU): the verify kernel runs in several
     rounds of workgroups rather than declining (the vocabulary-head shape)."""
     N, K = 40000, 256
-    (x, w, s, b), _, ref = affine_case(N, K, M, 64, seed=M + 100)
+    (x, w, s, b), _, (ref, bd) = affine_case(N, K, M, 64, seed=M + 100)
     y = affine.quantized_matmul(x, w, s, b, group_size=64)
     assert y is not None
-    assert_close(y.float().cpu().numpy(), ref, what=f"affine wide N={N} M={M}")
+    assert_close(y.float().cpu().numpy(), ref, bound=bd, what=f"affine wide N={N} M={M}")
 
 
 @pytest.mark.parametrize("M", [1, 2, 8])
 @pytest.mark.parametrize("signs_seed", [None, 7])
 def test_affine_rotated_linear(M, signs_seed):
     N, K = 1088, 5120
-    (x, w, s, b), signs, ref = affine_case(N, K, M, 64, seed=20 + M, block=128, signs_seed=signs_seed)
+    (x, w, s, b), signs, (ref, bd) = affine_case(N, K, M, 64, seed=20 + M, block=128, signs_seed=signs_seed)
     y = affine.linear(x, w, s, b, signs=torch.from_numpy(signs), block=128, group_size=64)
     assert y is not None
-    assert_close(y.float().cpu().numpy(), ref, what=f"rotated M={M}")
+    assert_close(y.float().cpu().numpy(), ref, bound=bd, what=f"rotated M={M}")
 
 
 @pytest.mark.parametrize("block", [2, 32, 64, 128, 512])
@@ -140,10 +149,10 @@ def test_affine_rotated_gemv_staging(block, prestage, K):
     if K % block:
         pytest.skip("the rotation block must divide K")
     N = 700
-    (x, w, s, b), signs, ref = affine_case(N, K, 1, 64, seed=block + K, block=block, signs_seed=3)
+    (x, w, s, b), signs, (ref, bd) = affine_case(N, K, 1, 64, seed=block + K, block=block, signs_seed=3)
     y = affine.linear(x, w, s, b, signs=torch.from_numpy(signs), block=block, group_size=64, _prestage=prestage)
     assert y is not None
-    assert_close(y.float().cpu().numpy(), ref, what=f"gemv block={block} prestage={prestage} K={K}")
+    assert_close(y.float().cpu().numpy(), ref, bound=bd, what=f"gemv block={block} prestage={prestage} K={K}")
 
 
 @pytest.mark.parametrize("M", [2, 5, 16])
@@ -155,10 +164,10 @@ def test_affine_rotated_verify(M, block, K, prestage):
     workspace and the general verify kernel (K = 1152). M = 16 at K = 5120 stages x in two K
     chunks."""
     N = 530
-    (x, w, s, b), signs, ref = affine_case(N, K, M, 64, seed=M + block + K, block=block, signs_seed=5)
+    (x, w, s, b), signs, (ref, bd) = affine_case(N, K, M, 64, seed=M + block + K, block=block, signs_seed=5)
     y = affine.linear(x, w, s, b, signs=torch.from_numpy(signs), block=block, group_size=64, _prestage=prestage)
     assert y is not None
-    assert_close(y.float().cpu().numpy(), ref, what=f"verify M={M} block={block} K={K} prestage={prestage}")
+    assert_close(y.float().cpu().numpy(), ref, bound=bd, what=f"verify M={M} block={block} K={K} prestage={prestage}")
 
 
 def test_affine_bf16_scales():

@@ -1,0 +1,88 @@
+"""Every BASELINE configuration at its full shape on the GPU against the oracle, through the C ABI.
+
+Each output is held to both criteria of `assert_close`: max |y - ref| <= 1e-3 * max |ref|
+(BASELINE's bar on fp16 outputs) and, per element, |y - ref| <= 1e-4 * sum|x||w| plus half an fp16
+ulp (the reference's own per-element yardstick, Tests/IshizukiKitTests/GGMLKernelTests.swift:131-137).
+The shapes are the ones the bench times, so every timed kernel instantiation is also checked:
+  configs[0]  Q4_0 4096x4096, M = 1 (and 8)
+  configs[1]  affine 2-bit g64 + 128-point rotation, 17408x5120, M in {1, 2, 4, 8}
+  configs[2]  Q4_K / Q6_K / IQ2_XS at 25600x5120 (gate/up) and 5120x25600 (down), M in {1, 8};
+              the down projection's M = 1 GEMV has 400 units per row (64 lanes per row, ragged)
+  configs[3]  EXL3 2 bpw 5120 -> 17408, M in {1, 2, 4, 8}
+  north-star  Q4_0 / Q4_K / Q6_K / IQ2_XS at 17408x5120, M in {1, 8}
+(configs[4], the MoE FFN at T = 1, 8 and 64, is in test_moe_gpu.py.)
+Synthetic data follow the configs' distributions (ishizuki_amd.synth).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import assert_close, ggml_reference
+from ishizuki_amd import affine, exl3, ggml, synth
+from test_exl3_gpu import APPLY_ELEM, apply_reference
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _ggml_case(t, N, K, Ms, seed):
+    blk = synth.ggml_blocks(t, N, K, seed=seed)
+    wb = torch.from_numpy(blk).to(DEV)
+    x = synth.fp16_normal((max(Ms), K), seed=seed + 1)
+    ref, bound = ggml_reference(t, x, blk, N)
+    for M in Ms:
+        print(f"config ggml type={t} N={N} K={K} M={M}", flush=True)
+        y = ggml.matvec(torch.from_numpy(x[:M]).to(DEV), wb, t, N)
+        assert y is not None, "declined"
+        assert_close(y.float().cpu().numpy(), ref[:M], bound=bound[:M], what=f"type={t} {N}x{K} M={M}")
+
+
+def test_config0_q4_0_4096():
+    _ggml_case(ggml.Q4_0, 4096, 4096, (1, 8), seed=0x15A12)
+
+
+@pytest.mark.parametrize("t", [ggml.Q4_K, ggml.Q6_K, ggml.IQ2_XS])
+@pytest.mark.parametrize("N,K", [(25600, 5120), (5120, 25600)])
+def test_config2_qwen_mlp(t, N, K):
+    _ggml_case(t, N, K, (1, 8), seed=0x15A14 + t + K)
+
+
+@pytest.mark.parametrize("t", [ggml.Q4_0, ggml.Q4_K, ggml.Q6_K, ggml.IQ2_XS])
+def test_north_star_17408x5120(t):
+    _ggml_case(t, 17408, 5120, (1, 8), seed=0x15A20 + t)
+
+
+def test_config1_affine_rotated():
+    N, K, g = 17408, 5120, 64
+    codes, s, b = synth.affine_pack(N, K, group=g, seed=0x15A13)
+    signs = synth.hadamard_signs(K, seed=0x15A13)
+    x = synth.fp16_normal((8, K), seed=0x15A13 + 1)
+    xr = oracle.hadamard(x.astype(np.float32), 128, signs).astype(np.float16).astype(np.float32)
+    ref = oracle.affine_matmul(xr, codes, s.view(np.uint16), b.view(np.uint16), N, 2, g)
+    W = oracle.affine_dequant(codes, s.view(np.uint16), b.view(np.uint16), N, K, 2, g)
+    np.abs(W, out=W)
+    bound = np.abs(xr) @ W.T
+    del W
+    wd = torch.from_numpy(codes.view(np.int32)).to(DEV)
+    sd, bd = torch.from_numpy(s).to(DEV), torch.from_numpy(b).to(DEV)
+    for M in (1, 2, 4, 8):
+        print(f"config affine M={M}", flush=True)
+        y = affine.linear(torch.from_numpy(x[:M]).to(DEV), wd, sd, bd, signs=torch.from_numpy(signs), block=128,
+                          group_size=g)
+        assert y is not None
+        assert_close(y.float().cpu().numpy(), ref[:M], bound=bound[:M], what=f"affine 17408x5120 M={M}")
+
+
+def test_config3_exl3_2bpw():
+    K, N = 5120, 17408
+    t, suh, svh = synth.exl3_pack(K, N, bits2=4, seed=0x15A15)
+    ten = exl3.EXL3Tensor(torch.from_numpy(t).to(DEV), torch.from_numpy(suh).to(DEV), torch.from_numpy(svh).to(DEV),
+                          codebook=exl3.THREE_INST)
+    x = synth.fp16_normal((8, K), seed=0x15A15 + 1)
+    ref, bound = apply_reference(x, t, suh, svh, 4, 0)
+    for M in (1, 2, 4, 8):
+        print(f"config exl3 M={M}", flush=True)
+        y = exl3.apply(torch.from_numpy(x[:M]).to(DEV), ten)
+        assert y is not None
+        assert_close(y.float().cpu().numpy(), ref[:M], bound=bound[:M], elem=APPLY_ELEM, what=f"exl3 5120->17408 M={M}")

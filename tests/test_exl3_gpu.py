@@ -16,6 +16,25 @@ from ishizuki_amd import exl3, synth
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
+# apply: the rotated x is fp16, and a value on a rounding boundary may land one ulp apart between
+# two fp32 butterfly orders, which moves an output by at most 2^-11 of its bound
+APPLY_ELEM = 1e-4 + 2.0 ** -11
+
+
+def apply_reference(x, t, suh, svh, bits2, cb):
+    """(ref, bound) for EXL3Kernels.apply: the oracle's rotate -> product -> rotate, and the
+    per-element bound carried through both rotations: |xh| @ |W| for yh, then each output takes
+    1/sqrt(128) of its 128-block's yh bounds times |svh|."""
+    x = np.asarray(x, np.float32)
+    suh = np.asarray(suh, np.float32)
+    svh = np.asarray(svh, np.float32)
+    ref = oracle.exl3_apply(x, t, suh, svh, bits2, cb)
+    xh = oracle.hadamard(x, 128, suh).astype(np.float16).astype(np.float32)
+    bh = np.abs(xh) @ np.abs(oracle.exl3_dequant(t, bits2, cb))
+    M, N = bh.shape
+    blk = bh.reshape(M, N // 128, 128).sum(2, keepdims=True) / np.sqrt(128.0)
+    bound = np.broadcast_to(blk, (M, N // 128, 128)).reshape(M, N) * np.abs(svh)
+    return ref, bound
 CASES = [("r1c0", 0), ("r2c1", 1), ("r3c2", 2), ("r4c0", 0), ("r5c2", 2), ("r6c1", 1),
          ("r7c2", 2), ("r8c0", 0), ("r1h5c2", 2), ("r2h5c2", 2), ("r3h5c2", 2)]
 
@@ -56,9 +75,10 @@ def test_matvec(M, bits2, cb):
     w = oracle.exl3_dequant(t, bits2, cb)
     xh = synth.fp16_normal((M, K), seed=M)
     ref = xh.astype(np.float32) @ w
+    bd = np.abs(xh.astype(np.float32)) @ np.abs(w)
     y = exl3.matvec(torch.from_numpy(xh).to(DEV), ten)
     assert y is not None
-    assert_close(y.cpu().numpy(), ref, what=f"exl3 matvec M={M} bits2={bits2} cb={cb}")
+    assert_close(y.cpu().numpy(), ref, bound=bd, what=f"exl3 matvec M={M} bits2={bits2} cb={cb}")
 
 
 @pytest.mark.parametrize("M", [1, 3])
@@ -69,10 +89,12 @@ def test_matvec_n_not_a_multiple_of_the_wide_step(M, bits2, N):
     K = 512
     t, _, _, ten = make(K, N, bits2, 0, seed=N + bits2 + M)
     xh = synth.fp16_normal((M, K), seed=M)
-    ref = xh.astype(np.float32) @ oracle.exl3_dequant(t, bits2, 0)
+    w = oracle.exl3_dequant(t, bits2, 0)
+    ref = xh.astype(np.float32) @ w
+    bd = np.abs(xh.astype(np.float32)) @ np.abs(w)
     y = exl3.matvec(torch.from_numpy(xh).to(DEV), ten)
     assert y is not None
-    assert_close(y.cpu().numpy(), ref, what=f"exl3 matvec bits2={bits2} N={N} M={M}")
+    assert_close(y.cpu().numpy(), ref, bound=bd, what=f"exl3 matvec bits2={bits2} N={N} M={M}")
 
 
 @pytest.mark.parametrize("M", [1, 8])
@@ -83,10 +105,10 @@ def test_apply_split_partials(M, bits2, N):
     K = 5120
     t, suh, svh, ten = make(K, N, bits2, 0, seed=M + N)
     x = synth.fp16_normal((M, K), seed=M + 3)
-    ref = oracle.exl3_apply(x.astype(np.float32), t, suh, svh, bits2, 0)
+    ref, bd = apply_reference(x, t, suh, svh, bits2, 0)
     y = exl3.apply(torch.from_numpy(x).to(DEV), ten)
     assert y is not None
-    assert_close(y.float().cpu().numpy(), ref, what=f"exl3 apply split bits2={bits2} N={N} M={M}")
+    assert_close(y.float().cpu().numpy(), ref, bound=bd, elem=APPLY_ELEM, what=f"exl3 apply split bits2={bits2} N={N} M={M}")
 
 
 @pytest.mark.parametrize("M", [1, 4, 8])
@@ -94,9 +116,9 @@ def test_apply_matches_oracle(M):
     K, N = 5120, 1024
     t, suh, svh, ten = make(K, N, 4, 0, seed=40 + M)
     x = synth.fp16_normal((M, K), seed=M + 100)
-    ref = oracle.exl3_apply(x.astype(np.float32), t, suh.astype(np.float32), svh.astype(np.float32), 4, 0)
+    ref, bd = apply_reference(x, t, suh, svh, 4, 0)
     y = exl3.apply(torch.from_numpy(x).to(DEV), ten)
-    assert_close(y.float().cpu().numpy(), ref, what=f"exl3 apply M={M}")
+    assert_close(y.float().cpu().numpy(), ref, bound=bd, elem=APPLY_ELEM, what=f"exl3 apply M={M}")
 
 
 @pytest.mark.parametrize("M", [1, 3, 16])
@@ -109,10 +131,10 @@ def test_apply_fused_input_rotation(M, K, bits2, cb):
     N = 512
     t, suh, svh, ten = make(K, N, bits2, cb, seed=K + bits2 + cb)
     x = synth.fp16_normal((M, K), seed=K + 7 + M)
-    ref = oracle.exl3_apply(x.astype(np.float32), t, suh, svh, bits2, cb)
+    ref, bd = apply_reference(x, t, suh, svh, bits2, cb)
     y = exl3.apply(torch.from_numpy(x).to(DEV), ten)
     assert y is not None
-    assert_close(y.float().cpu().numpy(), ref, what=f"exl3 apply fused rotation M={M} K={K} bits2={bits2} cb={cb}")
+    assert_close(y.float().cpu().numpy(), ref, bound=bd, elem=APPLY_ELEM, what=f"exl3 apply fused rotation M={M} K={K} bits2={bits2} cb={cb}")
 
 
 @pytest.mark.parametrize("name,cb", [("qwen3", 0), ("qwen38", 2)])

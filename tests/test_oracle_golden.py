@@ -170,3 +170,93 @@ def test_moe_route_matches_numpy():
     assert np.array_equal(ids, order)
     sel = np.take_along_axis(p, order, 1)
     assert np.allclose(w, sel / sel.sum(1, keepdims=True), rtol=1e-6)
+
+
+def _affine_dense(codes, s, b, K, bits, group):
+    """W from an MLX affine pack with numpy bit operations alone (field k of the row's u32
+    stream, Quantize/WeightedAffineQuantizer.swift:142-153), in float64."""
+    per = 32 // bits
+    k = np.arange(K)
+    q = (codes[:, k // per] >> np.uint32(bits) * (k % per).astype(np.uint32)) & np.uint32((1 << bits) - 1)
+    return (np.repeat(s.astype(np.float64), group, 1) * q + np.repeat(b.astype(np.float64), group, 1))
+
+
+@pytest.mark.parametrize("bits,group", [(2, 64), (2, 128), (4, 64), (4, 128), (8, 64), (8, 128)])
+def test_affine_matmul_pinned(bits, group):
+    """oracle.affine_matmul against x @ W.T in float64 with W rebuilt from the codes by numpy: each
+    element within 1e-5 of sum |x||w| (the reference's per-element criterion,
+    GGMLKernelTests.swift:131-137). A transposed operand, a wrong group index or a dropped bias
+    each fail it."""
+    from ishizuki_amd import synth
+    N, K, M = 37, 1024, 5
+    if bits == 2:
+        codes, s, b = synth.affine_pack(N, K, group=group, seed=bits + group)
+    else:
+        codes, s, b = synth.affine_pack_bits(N, K, bits, group=group, seed=bits + group)
+    # distinct biases (not just -s) so scale and bias cannot be confused
+    b = (b.astype(np.float32) + np.float32(0.003) * np.arange(b.size).reshape(b.shape) % 7).astype(np.float16)
+    x = np.random.default_rng(bits).standard_normal((M, K)).astype(np.float16).astype(np.float32)
+    y = oracle.affine_matmul(x, codes, s.view(np.uint16), b.view(np.uint16), N, bits, group)
+    W = _affine_dense(codes, s, b, K, bits, group)
+    want = x.astype(np.float64) @ W.T
+    bound = np.abs(x).astype(np.float64) @ np.abs(W).T
+    assert np.all(np.abs(y - want) <= 1e-5 * bound + 1e-30)
+    # and the dense weight itself bit-for-bit
+    w32 = oracle.affine_dequant(codes, s.view(np.uint16), b.view(np.uint16), N, K, bits, group)
+    assert np.array_equal(w32, W.astype(np.float32))
+
+
+def _moe_loop_reference(x, logits, gate, up, down, t_, E, H, I, k):
+    """MoEBlockTests.reference (Tests/IshizukiKitTests/MoEBlockTests.swift:94-126) written out per
+    token with numpy: softmax, top-k by sorting (ties to the lower index), renormalised weights,
+    one SwiGLU per chosen expert with the fp16 activations of an fp16 model (each projection's
+    output, sigmoid, silu and the product rounded to fp16), the weighted sum in fp32 in slot order,
+    narrowed once. Weights from the golden-pinned dequantizer; dots in float64."""
+    r16 = lambda a: np.asarray(a, np.float64).astype(np.float32).astype(np.float16).astype(np.float64)
+    Wg = oracle.dequant_rows(t_, gate, E * I, H).reshape(E, I, H).astype(np.float64)
+    Wu = oracle.dequant_rows(t_, up, E * I, H).reshape(E, I, H).astype(np.float64)
+    Wd = oracle.dequant_rows(t_, down, E * H, I).reshape(E, H, I).astype(np.float64)
+    T = x.shape[0]
+    y = np.zeros((T, H))
+    bound = np.zeros((T, H))
+    for t in range(T):
+        p = np.exp(logits[t].astype(np.float64) - logits[t].max())
+        p /= p.sum()
+        order = np.argsort(-logits[t], kind="stable")[:k]
+        w = p[order] / p[order].sum()
+        acc = np.zeros(H, np.float32)
+        for s, e in enumerate(order):
+            g = r16(Wg[e] @ x[t])
+            u = r16(Wu[e] @ x[t])
+            h = r16(r16(g * r16(1.0 / (1.0 + np.exp(-g)))) * u)
+            o = r16(Wd[e] @ h)
+            acc = (acc + (o * w[s]).astype(np.float32)).astype(np.float32)
+            bound[t] += w[s] * (np.abs(Wd[e]) @ np.abs(h))
+        y[t] = r16(acc)
+    return y, bound, order
+
+
+def test_moe_swiglu_pinned():
+    """oracle.moe_swiglu against the loop-per-token reference above. An fp16 intermediate may round
+    the other way when the two dot orders straddle a rounding boundary, so each element is held to
+    one fp16 ulp of its down-projection terms (2^-10 * sum_s w_s |W_d||h_s|) plus the final
+    narrowing (2^-11 |y|). A dropped slot, a wrong weight, a skipped renormalisation, gate and up
+    swapped or silu applied to up all exceed it by orders of magnitude."""
+    from ishizuki_amd import synth
+    E, H, I, k, T, t_ = 16, 512, 256, 4, 3, 12
+    gate = synth.ggml_blocks(t_, E * I, H, seed=1, scale=4e-4)
+    up = synth.ggml_blocks(t_, E * I, H, seed=2, scale=4e-4)
+    down = synth.ggml_blocks(t_, E * H, I, seed=3, scale=4e-4)
+    x = synth.fp16_normal((T, H), seed=4).astype(np.float32)
+    logits = np.random.default_rng(5).standard_normal((T, E)).astype(np.float32)
+    ids, w = oracle.moe_route(logits, k)
+    y = oracle.moe_swiglu(t_, x, ids, w, gate, up, down, E, I)
+    want, bound, _ = _moe_loop_reference(x, logits, gate, up, down, t_, E, H, I, k)
+    assert np.isfinite(want).all() and np.abs(want).max() > 1e-3
+    err = np.abs(y - want)
+    assert np.all(err <= 2.0 ** -10 * bound + 2.0 ** -11 * np.abs(want) + 2.0 ** -24), err.max()
+    # the check has teeth: dropping the last slot is caught
+    w2 = w.copy()
+    w2[:, -1] = 0
+    y2 = oracle.moe_swiglu(t_, x, ids, w2, gate, up, down, E, I)
+    assert not np.all(np.abs(y2 - want) <= 2.0 ** -10 * bound + 2.0 ** -11 * np.abs(want) + 2.0 ** -24)
