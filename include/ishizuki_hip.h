@@ -146,6 +146,17 @@ int ishz_exl3_apply(const void *x, int x_dtype, int M, int K, const int16_t *tre
                     const uint16_t *suh, const uint16_t *svh, int N, int bits2, int codebook,
                     void *y, void *workspace, size_t workspace_bytes, ishz_stream_t stream);
 
+/* No counterpart in the reference: ishz_exl3_apply for callers that cannot allocate (code under
+   HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It allocates nothing:
+   the workspace is a static device array of ISHZ_EXL3_STATIC_SCRATCH_BYTES that each GPU holds
+   until the process ends. Shapes whose ishz_exl3_workspace_size exceeds it give ISHZ_EINVAL.
+   `stream` must belong to the current device. Calls that overlap on one GPU share the scratch
+   and race: serialise them (one stream, or events). Same results as ishz_exl3_apply. */
+#define ISHZ_EXL3_STATIC_SCRATCH_BYTES (32u << 20)
+int ishz_exl3_apply_static(const void *x, int x_dtype, int M, int K, const int16_t *trellis,
+                           const uint16_t *suh, const uint16_t *svh, int N, int bits2, int codebook,
+                           void *y, ishz_stream_t stream);
+
 /* MoEBlock routing (Text/MoEBlock.swift:124-134): softmax over E logits (fp32) per token, the
    topk largest (ties to the lower index), renormalised to sum 1 when `normalize`. ids [T][topk]
    in descending order, weights [T][topk]. */

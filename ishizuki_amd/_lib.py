@@ -33,6 +33,7 @@ _SIGS = {
     "ishz_exl3_matvec": (I, [P, I, I, I, P, I, I, I, P, P]),
     "ishz_exl3_workspace_size": (SZ, [I, I, I]),
     "ishz_exl3_apply": (I, [P, I, I, I, P, P, P, I, I, I, P, P, SZ, P]),
+    "ishz_exl3_apply_static": (I, [P, I, I, I, P, P, P, I, I, I, P, P]),
     "ishz_moe_route": (I, [P, I, I, I, I, P, P, P]),
     "ishz_moe_workspace_size": (SZ, [I, I, I, I, I]),
     "ishz_moe_swiglu": (I, [U32, P, I, I, I, P, I, I, I, P, P, P, SZ, I, P, P, P, P, SZ, P]),

@@ -15,6 +15,9 @@
 #include <type_traits>
 #include <cstdlib>
 
+#include <mutex>
+#include <string>
+
 #include "common.h"
 
 namespace ishz {
@@ -745,6 +748,37 @@ extern "C" size_t ishz_exl3_workspace_size(int M, int K, int N) {
   return ((size_t)M * K * 2 + 255) / 256 * 256 + (size_t)most * M * N * 4;
 }
 
+// Device scratch of ishz_exl3_apply_static: every GPU the library runs on holds its own copy
+// until the process ends. Host code never passes `scratch` itself (its host-side name is not a
+// device address): the per-device address from hipGetSymbolAddress is used instead.
+static __device__ __align__(256) uint8_t scratch[ISHZ_EXL3_STATIC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::once_flag scratch_once[kMaxDevices];
+void *scratch_ptr[kMaxDevices];
+hipError_t scratch_err[kMaxDevices];
+}  // namespace
+
+// This device's scratch address, looked up once per device with that device current.
+static int exl3_scratch(hipStream_t st, void **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail("hipGetDevice", e);
+  if (st) {
+    int sdev = -1;
+    if ((e = hipStreamGetDevice(st, &sdev)) != hipSuccess) return fail("hipStreamGetDevice", e);
+    if (sdev != dev) return einval("the stream belongs to another device than the current one");
+  }
+  if (dev < 0 || dev >= kMaxDevices) return einval("device index beyond the scratch table");
+  std::call_once(scratch_once[dev], [dev] {
+    scratch_err[dev] = hipGetSymbolAddress(&scratch_ptr[dev], HIP_SYMBOL(scratch));
+  });
+  if (scratch_err[dev] != hipSuccess) return fail("hipGetSymbolAddress(scratch)", scratch_err[dev]);
+  *out = scratch_ptr[dev];
+  return ISHZ_OK;
+}
+
 extern "C" int ishz_exl3_apply(const void *x, int x_dtype, int M, int K, const int16_t *trellis,
                                const uint16_t *suh, const uint16_t *svh, int N, int bits2,
                                int codebook, void *y, void *workspace, size_t workspace_bytes,
@@ -770,4 +804,22 @@ extern "C" int ishz_exl3_apply(const void *x, int x_dtype, int M, int K, const i
                      ISHZ_DT_F32, blocks, N, svh, 0, y, ISHZ_DT_F16, np);
   ISHZ_LAUNCH_CHECK("exl3 rotate launch");
   return ISHZ_OK;
+}
+
+// ishz_exl3_apply with the library's own device scratch in place of a caller workspace: no
+// allocation of any kind. Calls that overlap on one GPU share the scratch and race.
+extern "C" int ishz_exl3_apply_static(const void *x, int x_dtype, int M, int K, const int16_t *trellis,
+                                      const uint16_t *suh, const uint16_t *svh, int N, int bits2, int codebook,
+                                      void *y, ishz_stream_t stream) {
+  int rc = check_exl3(K, N, bits2, codebook);
+  if (rc) return rc;
+  if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
+  if (M < 1 || M > 16) return decline("row count outside 1..16");
+  const size_t need = ishz_exl3_workspace_size(M, K, N);
+  if (need > ISHZ_EXL3_STATIC_SCRATCH_BYTES)
+    return einval("M x K x N needs " + std::to_string(need) + " bytes of scratch, above the static " +
+                  std::to_string((size_t)ISHZ_EXL3_STATIC_SCRATCH_BYTES) + " (use ishz_exl3_apply)");
+  void *ws = nullptr;
+  if ((rc = exl3_scratch(S(stream), &ws))) return rc;
+  return ishz_exl3_apply(x, x_dtype, M, K, trellis, suh, svh, N, bits2, codebook, y, ws, need, stream);
 }
