@@ -64,7 +64,7 @@ struct FAffineN : GgmlGemv<FAffineN<BITS, GS, BF16S>> {
   };
   static constexpr int WPU = 64 * BITS / 32;  // code words per 64-weight unit
   static constexpr int BS = 64, UPB = 1, UNIT_BLOCKS = 1;
-  static constexpr int MAXB = 2, PREFB = 2, DEPTH = BITS == 4 ? 3 : 2;
+  static constexpr int RING = 5;
   static constexpr int R = 8, Q = 2, SUM_LEN = 32;
   static constexpr bool XSUM = true, GRID = false, VGRID = false, XPERM = BITS == 8;
   static DEV u4 xperm(u4 v) { return BITS == 4 ? perm04(v) : perm0213(v); }

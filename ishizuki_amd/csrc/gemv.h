@@ -1,20 +1,22 @@
 // The streaming M = 1 GEMV skeleton shared by every weight format (GGML blocks, MLX affine).
 //
-// A wave owns a contiguous, equal share of row groups (64/LPR rows each, LPR lanes per row) and
-// streams their units as one sequence: lane `sub` takes units sub, sub + LPR, ... of each row, in
-// batches of B units held in a ring of D register batches, so D - 1 batches' loads are in
-// flight while one is decoded. Loads are never predicated: a batch slot is valid for all lanes or none
-// (unless RAGGED), and an invalid slot reloads the lane's first unit, so the waitcnt pass only
-// waits for the batch being decoded. The first batches are issued before x is staged into LDS.
+// A workgroup owns a contiguous, equal share of row groups (64/LPR rows each, LPR lanes per row);
+// lane `sub` of a row takes units sub, sub + LPR, ... (its slots), so a group is upl unit batches
+// (one unit per lane per batch). The workgroup's batches are dealt to its waves in equal contiguous
+// ranges, so every wave streams the same number of units to within one; a row split between two
+// waves leaves a partial dot from each in LDS, summed in wave order at the end. A wave keeps D - 1
+// batches in flight in a register ring; loads are never predicated and every batch a loop
+// iteration loads is consumed on every path, so the compiler's waits are for the batch being
+// decoded only. The first batches are issued before x is staged into LDS.
 //
 // A format F provides: Args (pointers and sizes), Raw (one unit's registers), LaneC (per-lane
 // constants), units(K), load(args, row, u), dot(raw, UnitX, LaneC), stage_load(...) (x loads
 // issued first, kept in an XPre) and stage(...) (fills the LDS slots and sums of x, see UnitX),
-// extra_lds_bytes(args), and R / Q (slots and sums per unit). A format whose rows read different
-// activation vectors (a batch of gathered experts) also provides nx(args), the number of x
-// images (LDS is sized for all of them), xsel(args, row), the image a row reads (uniform over a
-// row group), and a stage taking the first and last image the workgroup's rows read: only those
-// are staged.
+// extra_lds_bytes(args), R / Q (slots and sums per unit), RING (the ring depth D) and occ(args)
+// (resident waves per SIMD the grid is sized for). A format whose rows read different activation
+// vectors (a batch of gathered experts) also provides nx(args), the number of x images (LDS is
+// sized for all of them), xsel(args, row), the image a row reads (uniform over a row group), and
+// a stage taking the first and last image the workgroup's rows read: only those are staged.
 #pragma once
 #include <algorithm>
 #include <cstdlib>
@@ -77,9 +79,9 @@ __host__ __device__ constexpr int gemv_threads() {
   else return 256;
 }
 
-template <class F, int LPR, int B, int D, bool RAGGED>
+template <class F, int LPR, int D, bool RAGGED>
 __global__ __launch_bounds__(gemv_threads<F>()) void gemv_kernel(typename F::Args args, const uint16_t *__restrict__ x,
-                                                   uint16_t *__restrict__ y, int nwaves) {
+                                                   uint16_t *__restrict__ y, int nwg, int part_off) {
   static_assert(LPR % 16 == 0, "lanes per row must be a multiple of 16");
   extern __shared__ __align__(16) uint32_t smem[];
   const int K = args.K, N = args.N;
@@ -89,196 +91,167 @@ __global__ __launch_bounds__(gemv_threads<F>()) void gemv_kernel(typename F::Arg
   u4 *xs = (u4 *)smem;
   float *xsum = (float *)(xs + nx * ugroups * 16 * F::R);
   u4 *extra = (u4 *)(xsum + nx * ugroups * 16 * F::Q);  // format tables / scratch
+  float *part = (float *)((char *)smem + part_off);      // [wave][row of the workgroup] partial dots
 
-  constexpr int RPW = 64 / LPR;
+  constexpr int RPW = 64 / LPR, WPG = gemv_threads<F>() / 64;
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int sub = lane % LPR, rg = lane / LPR;
-  const int nb = (units + B * LPR - 1) / (B * LPR);  // batches per row
-  const int gw = blockIdx.x * (blockDim.x >> 6) + wave;
-  // wave gw of nwaves owns row groups [gw G / nwaves, (gw + 1) G / nwaves): every wave, and so
-  // every CU of a full round, gets the same share to within one group
+  const int upl = (units + LPR - 1) / LPR;  // units per lane per row
+  // workgroup b of nwg owns row groups [b G / nwg, (b + 1) G / nwg); their upl unit batches per
+  // group are dealt to its waves in equal contiguous ranges [tb, te)
   const int G = (N + RPW - 1) / RPW;
-  auto gstart = [&](int w) { return (int)((long long)min(w, nwaves) * G / nwaves); };
-  const int g_end = gstart(gw + 1);
-  const int g_last = max(g_end - 1, 0);
+  const int gf = (int)((long long)blockIdx.x * G / nwg), gend = (int)((long long)(blockIdx.x + 1) * G / nwg);
+  const int T = (gend - gf) * upl, nrows = (gend - gf) * RPW;
+  const int tb = T * wave / WPG, te = T * (wave + 1) / WPG;
   const typename F::LaneC lc = F::lane(sub);
+  for (int i = threadIdx.x; i < WPG * nrows; i += WPG * 64) part[i] = 0.0f;  // visible after staging's barrier
 
-  // Unit of batch slot i; an invalid slot (past the row's units) reloads the lane's first unit.
-  auto unit = [&](int bb, int i) {
-    const int k = bb * B + i;
+  // Unit of slot k of a lane's row; with RAGGED, a slot past the row's units reloads its last unit.
+  auto unit = [&](int k) {
     if constexpr (RAGGED) return min(sub + k * LPR, units - 1);
-    return sub + (k * LPR < units ? k : 0) * LPR;
+    return sub + k * LPR;
   };
-  auto load_batch = [&](int g, int bb, typename F::Raw *r) {
-    const int row = min(min(g, g_last) * RPW + rg, N - 1);
-#pragma unroll
-    for (int i = 0; i < B; i++) r[i] = F::load(args, row, unit(bb, i));
+  // Batch t = (group g, slot k). A batch past the wave's last (the ring runs ahead of the consumer
+  // by D - 1) loads row 0's first unit on every lane: one cache line, never consumed.
+  auto load_b = [&](int t, int g, int k, typename F::Raw &r) {
+    const bool live = t < te;
+    r = F::load(args, live ? min(g * RPW + rg, N - 1) : 0, live ? unit(k) : 0);
   };
-
-  // Ring of D register batches: batch i sits in buf[i % D]; before batch i is decoded, batch
-  // i + D - 1 is issued into the slot batch i - 1 freed. Load and consume cursors (group,
-  // batch-in-row) advance in step. x's first staging loads go out before the weight batches:
-  // the memory counter is in order, so staging then waits only for x.
-  const int g0 = gstart(gw);
-  auto advance = [&](int &gg, int &bb) {
-    if (++bb == nb) {
-      bb = 0;
-      gg++;
+  auto advance = [&](int &g, int &k) {
+    if (++k == upl) {
+      k = 0;
+      g++;
     }
   };
+
+  // Ring of D register batches: batch t sits in buf[(t - tb) % D]; before batch t is consumed,
+  // batch t + D - 1 is issued into the slot batch t - 1 freed. Every batch a loop iteration loads
+  // is consumed on every path through the loop and results go to LDS, so the compiler's waits are
+  // for the batch being consumed only (a load left pending across the back edge, or a global
+  // store between loads, would make it wait for everything). x's first staging loads go out
+  // before the weight batches: the memory counter is in order, so staging waits only for x.
   const typename F::XPre pre = F::stage_load(args, x, units);
-  typename F::Raw buf[D][B];
-  int gl = g0, bl = 0;
+  typename F::Raw buf[D];
+  int gl = gf + (T ? tb / upl : 0), kl = T ? tb % upl : 0;
+  const int gc0 = gl, kc0 = kl;
 #pragma unroll
   for (int d = 0; d < D - 1; d++) {
-    load_batch(gl, bl, buf[d]);
-    advance(gl, bl);
+    load_b(tb + d, gl, kl, buf[d]);
+    advance(gl, kl);
   }
 
   int im0 = 0;  // first x image of this workgroup's rows
   if constexpr (gemv_multi_x<F>()) {
-    const int gfirst = gstart(blockIdx.x * (blockDim.x >> 6));
-    const int glast = max(gstart((blockIdx.x + 1) * (blockDim.x >> 6)) - 1, gfirst);
-    im0 = F::xsel(args, gfirst * RPW);
-    F::stage(args, x, xs, xsum, extra, units, pre, im0, F::xsel(args, min(glast * RPW + RPW - 1, N - 1)));
+    im0 = F::xsel(args, min(gf * RPW, N - 1));
+    F::stage(args, x, xs, xsum, extra, units, pre, im0, F::xsel(args, min(max(gend * RPW - 1, gf * RPW), N - 1)));
   } else {
     F::stage(args, x, xs, xsum, extra, units, pre);  // ends with a barrier
   }
   const uint32_t mg = vconst(0x64006400u);
   const u4 *grid = extra, *sgn = extra + F::GRID_ENTRIES;
-  const int lane_slot = (sub >> 4) * 16 * F::R + (sub & 15);
-  const int lane_sum = (sub >> 4) * 16 * F::Q + (sub & 15);
-  auto view = [&](int gg, int bb, int i) {
+  auto view = [&](int g, int k) {
     int xo = 0, so = 0;  // the group's x image
     if constexpr (gemv_multi_x<F>()) {
-      const int im = F::xsel(args, gg * RPW) - im0;
+      const int im = F::xsel(args, g * RPW) - im0;
       xo = im * ugroups * 16 * F::R;
       so = im * ugroups * 16 * F::Q;
     }
-    if constexpr (RAGGED) {
-      const int u = unit(bb, i);
-      return UnitX{xs + xo + (u >> 4) * 16 * F::R + (u & 15), xsum + so + (u >> 4) * 16 * F::Q + (u & 15), mg, grid,
-                   sgn};
-    } else {
-      const int k = bb * B + i;
-      return UnitX{xs + xo + lane_slot + k * LPR * F::R, xsum + so + lane_sum + k * LPR * F::Q, mg, grid, sgn};
-    }
+    const int u = unit(k);
+    return UnitX{xs + xo + (u >> 4) * 16 * F::R + (u & 15), xsum + so + (u >> 4) * 16 * F::Q + (u & 15), mg, grid, sgn};
   };
 
+  // RAGGED slots past the row's units are decoded (from a real unit) and masked out, never
+  // branched around: see the ring above. A row's partial goes to LDS at its last slot or at the
+  // wave's last batch.
   float acc = 0.0f;
-  auto consume = [&](int gg, int bb, const typename F::Raw *r) {
-#pragma unroll
-    for (int i = 0; i < B; i++) {
-      if constexpr (RAGGED) {
-        const float v = F::dot(r[i], view(gg, bb, i), lc);
-        acc += sub + (bb * B + i) * LPR < units ? v : 0.0f;
-      } else if ((bb * B + i) * LPR < units) {
-        acc += F::dot(r[i], view(gg, bb, i), lc);
-      }
-    }
-    if (bb == nb - 1) {
-      acc = group_sum<LPR>(acc);
-      const int row = gg * RPW + rg;
-      if (sub == 0 && row < N) y[row] = f2h(acc);
+  auto consume = [&](int t, int g, int k, const typename F::Raw &r) {
+    const float v = F::dot(r, view(g, k), lc);
+    if constexpr (RAGGED) acc += sub + k * LPR < units ? v : 0.0f;
+    else acc += v;
+    if (k == upl - 1 || t == te - 1) {
+      const float s = group_sum<LPR>(acc);
+      if (sub == 0) part[wave * nrows + (g - gf) * RPW + rg] = s;
       acc = 0.0f;
     }
   };
-  int gc = g0, bc = 0;
-  while (gc < g_end) {
+  int gc = gc0, kc = kc0, t = tb;
+  for (; t + D <= te; t += D) {
 #pragma unroll
     for (int d = 0; d < D; d++) {
-      load_batch(gl, bl, buf[(d + D - 1) % D]);
-      advance(gl, bl);
-      if (gc < g_end) consume(gc, bc, buf[d]);
-      advance(gc, bc);
+      load_b(t + d + D - 1, gl, kl, buf[(d + D - 1) % D]);
+      advance(gl, kl);
+      consume(t + d, gc, kc, buf[d]);
+      advance(gc, kc);
     }
+  }
+  // the last (te - tb) % D batches are already in buf[0 ..]
+#pragma unroll
+  for (int d = 0; d < D - 1; d++)
+    if (t + d < te) {
+      consume(t + d, gc, kc, buf[d]);
+      advance(gc, kc);
+    }
+
+  // Each output: the partials of the waves whose batch ranges meet its group, in wave order.
+  __syncthreads();
+  for (int i = threadIdx.x; i < nrows; i += WPG * 64) {
+    const int b0 = (i / RPW) * upl, b1 = b0 + upl - 1;
+    const int w0 = (WPG * (b0 + 1) - 1) / T, w1 = (WPG * (b1 + 1) - 1) / T;  // waves holding b0, b1
+    float s = 0.0f;
+    for (int w = w0; w <= w1; w++) s += part[w * nrows + i];
+    if (gf * RPW + i < N) y[gf * RPW + i] = f2h(s);
   }
 }
 
 int gemv_num_cu();
-int gemv_batch_override();  // ISHZ_GEMV_B (tuning)
-int gemv_occ_override();    // ISHZ_GEMV_OCC: resident waves per SIMD the grid is sized for (tuning)
 
-// Grid: one resident round of waves (at most what the compiled kernel's registers and this
-// launch's LDS allow), each wave an equal share of row groups.
-template <class F, int LPR, int B, int D, bool RAGGED>
-static int launch_gemv_kd(const typename F::Args &a, const void *x, void *y, hipStream_t st) {
+// Grid: one resident round of workgroups (at most what the compiled kernel's registers and this
+// launch's LDS allow), each an equal share of row groups. LDS: the staged x images and sums, the
+// format's tables, then the waves' partial dots for the workgroup's rows.
+template <class F, int LPR, bool RAGGED>
+static int launch_gemv_k(const typename F::Args &a, const void *x, void *y, hipStream_t st) {
   constexpr int RPW = 64 / LPR;
+  constexpr int NT = gemv_threads<F>(), WPG = NT / 64;
   const int units = F::units(a.K);
   const size_t ug = (size_t)(units + 15) / 16;
-  const size_t lds = gemv_nx<F>(a) * (ug * 16 * F::R * 16 + ug * 16 * F::Q * 4) + F::extra_lds_bytes(a);
-  if (lds > 160 * 1024) return decline("K too large for the GEMV's LDS copy of x");
-  auto kern = gemv_kernel<F, LPR, B, D, RAGGED>;
-  constexpr int NT = gemv_threads<F>(), WPG = NT / 64;
-  int per_cu = 0;  // workgroups per CU, so per_cu * WPG / 4 waves per SIMD
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, NT, lds) != hipSuccess || per_cu < 1)
-    per_cu = 1;
+  const size_t xlds = gemv_nx<F>(a) * (ug * 16 * F::R * 16 + ug * 16 * F::Q * 4) + F::extra_lds_bytes(a);
+  const size_t part_off = (xlds + 15) / 16 * 16;
+  if (part_off > 160 * 1024) return decline("K too large for the GEMV's LDS copy of x");
+  auto kern = gemv_kernel<F, LPR, F::RING, RAGGED>;
   const int groups = (a.N + RPW - 1) / RPW;
-  const int occ = gemv_occ_override() > 0 ? gemv_occ_override() : F::occ(a);
-  const int capacity = gemv_num_cu() * 4 * std::min(occ, std::max(per_cu * WPG / 4, 1));
-  const int waves = std::min(capacity, groups);  // one resident round, groups spread evenly
-  hipLaunchKernelGGL(kern, dim3((waves + WPG - 1) / WPG), dim3(NT), lds, st, a, (const uint16_t *)x, (uint16_t *)y,
-                     waves);
+  const int wg_cap = std::max(F::occ(a) * 4 / WPG, 1);  // workgroups per CU the grid is sized for
+  int nwg = 0;
+  size_t lds = 0;
+  // the rows per workgroup depend on the workgroup count, and the occupancy on the LDS: settle both
+  for (int per_cu = wg_cap, it = 0; it < 3; it++) {
+    nwg = std::min(gemv_num_cu() * std::min(per_cu, wg_cap), groups);
+    const size_t rows = (size_t)(groups + nwg - 1) / nwg * RPW;
+    lds = part_off + WPG * rows * 4;
+    if (lds > 160 * 1024) {  // very tall outputs: more workgroups, several rounds
+      const size_t room = (160 * 1024 - part_off) / (WPG * 4 * RPW);
+      if (room < 1) return decline("no LDS left for the GEMV's partial sums");
+      nwg = std::min((int)((groups + room - 1) / room), groups);
+      lds = part_off + WPG * ((size_t)(groups + nwg - 1) / nwg * RPW) * 4;
+      break;
+    }
+    int pc = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, kern, NT, lds) != hipSuccess || pc < 1) pc = 1;
+    if (pc >= per_cu || pc >= wg_cap) break;
+    per_cu = pc;
+  }
+  hipLaunchKernelGGL(kern, dim3(nwg), dim3(NT), lds, st, a, (const uint16_t *)x, (uint16_t *)y, nwg, (int)part_off);
   ISHZ_LAUNCH_CHECK("gemv launch");
   return ISHZ_OK;
 }
 
-int gemv_depth_override();  // ISHZ_GEMV_D (tuning)
-
-template <class F, int LPR, int B, bool RAGGED>
-static int launch_gemv_k(const typename F::Args &a, const void *x, void *y, hipStream_t st) {
-  switch (gemv_depth_override() ? gemv_depth_override() : F::DEPTH) {
-    case 4: return launch_gemv_kd<F, LPR, B, 4, RAGGED>(a, x, y, st);
-    case 3: return launch_gemv_kd<F, LPR, B, 3, RAGGED>(a, x, y, st);
-    default: return launch_gemv_kd<F, LPR, B, 2, RAGGED>(a, x, y, st);
-  }
-}
-
-template <class F, int LPR, int B>
-static int launch_gemv_lb(const typename F::Args &a, const void *x, void *y, hipStream_t st) {
-  if (F::units(a.K) % LPR) return launch_gemv_k<F, LPR, B, true>(a, x, y, st);
-  return launch_gemv_k<F, LPR, B, false>(a, x, y, st);
-}
-
-
-// Units per batch: ISHZ_GEMV_B, else the largest of F::PREFB, F::PREFB - 1, ... 2 that divides
-// the units each lane streams per row.
-template <class F, int LPR>
-static int launch_gemv_l(const typename F::Args &a, const void *x, void *y, hipStream_t st) {
-  const int upl = (F::units(a.K) + LPR - 1) / LPR;  // units per lane per row
-  int b = gemv_batch_override();
-  if (b < 2 || b > F::MAXB) {
-    b = 2;
-    for (int c = F::PREFB; c > 2; c--)
-      if (upl % c == 0) {
-        b = c;
-        break;
-      }
-  }
-  switch (b) {
-    case 5: if constexpr (F::MAXB >= 5) return launch_gemv_lb<F, LPR, 5>(a, x, y, st);
-    [[fallthrough]];
-    case 4: if constexpr (F::MAXB >= 4) return launch_gemv_lb<F, LPR, 4>(a, x, y, st);
-    [[fallthrough]];
-    case 3: if constexpr (F::MAXB >= 3) return launch_gemv_lb<F, LPR, 3>(a, x, y, st);
-    [[fallthrough]];
-    default: return launch_gemv_lb<F, LPR, 2>(a, x, y, st);
-  }
-}
-
-int gemv_lpr_override();  // ISHZ_GEMV_LPR (tuning)
-
+// Lanes per row: 16 for rows of up to 160 units, 32 up to 384, else 64. RAGGED: the row's units
+// are not a whole number of every lane's slots.
 template <class F>
 static int launch_gemv(const typename F::Args &a, const void *x, void *y, hipStream_t st) {
   const int units = F::units(a.K);
-  switch (gemv_lpr_override()) {
-    case 16: return launch_gemv_l<F, 16>(a, x, y, st);
-    case 32: return launch_gemv_l<F, 32>(a, x, y, st);
-    case 64: return launch_gemv_l<F, 64>(a, x, y, st);
-  }
-  if (units <= 160) return launch_gemv_l<F, 16>(a, x, y, st);
-  if (units <= 384) return launch_gemv_l<F, 32>(a, x, y, st);
-  return launch_gemv_l<F, 64>(a, x, y, st);
+  if (units <= 160) return units % 16 ? launch_gemv_k<F, 16, true>(a, x, y, st) : launch_gemv_k<F, 16, false>(a, x, y, st);
+  if (units <= 384) return units % 32 ? launch_gemv_k<F, 32, true>(a, x, y, st) : launch_gemv_k<F, 32, false>(a, x, y, st);
+  return units % 64 ? launch_gemv_k<F, 64, true>(a, x, y, st) : launch_gemv_k<F, 64, false>(a, x, y, st);
 }
 
 }  // namespace ishz

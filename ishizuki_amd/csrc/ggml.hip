@@ -314,26 +314,6 @@ static int num_cu() {
 }
 
 int gemv_num_cu() { return num_cu(); }
-static int env_int(const char *name) {
-  const char *e = getenv(name);
-  return e ? atoi(e) : 0;
-}
-int gemv_batch_override() {
-  static const int v = env_int("ISHZ_GEMV_B");
-  return v;
-}
-int gemv_depth_override() {
-  static const int v = env_int("ISHZ_GEMV_D");
-  return v;
-}
-int gemv_lpr_override() {
-  static const int v = env_int("ISHZ_GEMV_LPR");
-  return v;
-}
-int gemv_occ_override() {
-  static const int v = env_int("ISHZ_GEMV_OCC");
-  return v;
-}
 
 template <class F>
 static int verify(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st);
