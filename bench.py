@@ -4,15 +4,21 @@ Headline (BASELINE.json metric "weight-stream GB/s (% HBM peak) + us per quant m
 M=8", configs[1]): one step = one rotated MLX-affine 2-bit projection (Ternary Bonsai 27B style,
 17408 x 5120, group 64, 128-point Walsh-Hadamard on the input fused into the GEMV) at M=1, over
 synthetic seeded weights already resident in HBM. value = algorithmic weight-stream bytes / time
-per call (GB/s, 1e9). The weights rotate through >= 512 MB of copies so the 256 MB Infinity Cache
+per call (GB/s, 1e9). The weights rotate through >= 600 MB of copies so the 256 MB Infinity Cache
 cannot serve them. Calls are captured once into a HIP graph and replayed, so the timed region
 holds kernel time, not Python launch overhead.
 
-Also printed (same JSON line, "families"): us/call and GB/s at M = 1 and 8 for every family at
-17408 x 5120 (Q4_0, Q4_K, Q6_K, IQ2_XS, affine g64 + WHT, EXL3 2 bpw), the MoE FFN, and, with
---all, every BASELINE config and the other GGUF formats (Q2_K, IQ4_XS, IQ2_XXS, IQ2_S, IQ3_XXS,
-IQ3_S, IQ1_S, IQ1_M). cpu_baseline: the CPU oracle (dequantize-then-fp32-dot, OpenMP on
-all host cores) on a bounded row sample of the headline workload.
+Also printed (same JSON line, "families"), every BASELINE config at its own shape:
+  cfg0  Q4_0 4096x4096, M = 1 and 8
+  cfg1  affine 2-bit g64 + WHT 17408x5120, M = 1, 2, 4, 8
+  cfg2  Q4_K, Q6_K, IQ2_XS at 25600x5120 (gate/up) and 5120x25600 (down), M = 1 and 8
+  cfg3  EXL3 2 bpw 5120 -> 17408, M = 1, 2, 4, 8
+  cfg4  MoE FFN, 128 Q4_K experts, H 2048, I 768, top-8, T = 1, 8, 64
+and the north-star shape 17408x5120 for Q4_0, Q4_K, Q6_K and IQ2_XS at M = 1 and 8. With --all,
+also the other GGUF formats (Q2_K, IQ4_XS, IQ2_XXS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M), the
+4- and 8-bit affine packs and the MoE over affine experts. cpu_baseline: the CPU restatement
+(oracle/ishz_oracle.c, timed in C: rotate, then dequantize-then-dot; and the fused decode-dot)
+on the full headline matrix, OpenMP on the host's cores, median of 10.
 """
 import argparse
 import json
@@ -32,7 +38,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--all", action="store_true", help="every BASELINE config, not just 17408x5120")
+    ap.add_argument("--all", action="store_true", help="also the other GGUF formats, affine 4/8-bit and MoE over "
+                                                       "affine experts")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of family names to run (debug)")
     ap.add_argument("--policy", action="store_true",
@@ -152,8 +159,9 @@ def main():
         return max(2, int(np.ceil(CACHE_DEFEAT / max(nbytes, 1))))
 
     def timed(calls, steps, warmup):
-        """Capture one pass over `calls` (one per weight copy) in a HIP graph; replay until
-        `steps` calls ran. Returns seconds per call (events on the capture stream)."""
+        """Capture one pass over `calls` (one per weight copy) in a HIP graph, and the first
+        steps % len(calls) of them in a second one; time exactly `steps` calls (whole passes, then
+        the remainder). Returns seconds per call (events on the capture stream) and the count."""
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
@@ -161,22 +169,30 @@ def main():
                 c()
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
+        steps = max(1, steps)
+        full, rem = divmod(steps, len(calls))
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for c in calls:
                 c()
-        reps = max(1, (steps + len(calls) - 1) // len(calls))
-        wreps = max(1, (warmup + len(calls) - 1) // len(calls))
-        for _ in range(wreps):
+        g2 = None
+        if rem:
+            g2 = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g2):
+                for c in calls[:rem]:
+                    c()
+        for _ in range(max(1, (warmup + len(calls) - 1) // len(calls))):
             g.replay()
         torch.cuda.synchronize()
         st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         st.record()
-        for _ in range(reps):
+        for _ in range(full):
             g.replay()
+        if g2 is not None:
+            g2.replay()
         en.record()
         torch.cuda.synchronize()
-        return st.elapsed_time(en) * 1e-3 / (reps * len(calls)), reps * len(calls)
+        return st.elapsed_time(en) * 1e-3 / steps, steps
 
     # ------------------------------------------------------------------ workloads
     def ggml_case(t, N, K, M, seed=1):
@@ -253,10 +269,13 @@ def main():
                                                  ptr(wsp), wsb, torch.cuda.current_stream().cuda_stream) for tt in ts]
         return calls, nb + 2 * (K + N), nb + 2 * (K + N) + 2 * M * (K + N)
 
-    def moe_case(T, E=128, H=2048, I=768, k=8, seed=4):
-        gate = synth.ggml_blocks(ggml.Q4_K, E * I, H, seed=seed)
-        up = synth.ggml_blocks(ggml.Q4_K, E * I, H, seed=seed + 1)
-        down = synth.ggml_blocks(ggml.Q4_K, E * H, I, seed=seed + 2)
+    def moe_case(T, E=128, H=2048, I=768, k=8, seed=4, scale=4e-4):
+        # super-scales |N| * 4e-4 rather than the config's |N| * 0.01: with uniformly random 6-bit
+        # sub-scales the latter overflows fp16 in the SwiGLU intermediates (outputs inf); timing
+        # does not depend on the values, and the outputs are checked finite before timing
+        gate = synth.ggml_blocks(ggml.Q4_K, E * I, H, seed=seed, scale=scale)
+        up = synth.ggml_blocks(ggml.Q4_K, E * I, H, seed=seed + 1, scale=scale)
+        down = synth.ggml_blocks(ggml.Q4_K, E * H, I, seed=seed + 2, scale=scale)
         ex = moe.GGMLExperts(*(torch.from_numpy(a).to(dev) for a in (gate, up, down)), ggml.Q4_K, E, H, I)
         pool = 3 * ex.expert_bytes * E
         exs = [ex] + [moe.GGMLExperts(ex.gate.clone(), ex.up.clone(), ex.down.clone(), ggml.Q4_K, E, H, I)
@@ -274,6 +293,9 @@ def main():
         calls = [lambda e=e: L.ishz_moe_swiglu(ggml.Q4_K, ptr(x), 1, T, H, ptr(logits), E, k, 1, ptr(e.gate),
                                                ptr(e.up), ptr(e.down), e.expert_bytes, I, ptr(y), None, None,
                                                ptr(wsp), wsb, torch.cuda.current_stream().cuda_stream) for e in exs]
+        calls[0]()
+        torch.cuda.synchronize()
+        assert bool(torch.isfinite(y).all()), "MoE bench outputs must be finite"
         nb = distinct * 3 * ex.expert_bytes
         return calls, nb, nb, distinct
 
@@ -329,82 +351,75 @@ def main():
     head, head_sec, head_n = measure("affine2_g64_wht128", lambda: affine_case(NS, KS, 1), 1, args.steps, args.warmup)
     rd, rd_sec, _ = measure("stream_read", lambda: read_case(head["weight_bytes"]), 1, args.steps, args.warmup)
 
-    plan = [
-        ("q4_0", lambda M: ggml_case(ggml.Q4_0, NS, KS, M)),
-        ("q4_k", lambda M: ggml_case(ggml.Q4_K, NS, KS, M)),
-        ("q6_k", lambda M: ggml_case(ggml.Q6_K, NS, KS, M)),
-        ("iq2_xs", lambda M: ggml_case(ggml.IQ2_XS, NS, KS, M)),
-        ("affine2_g64_wht128", lambda M: affine_case(NS, KS, M)),
-        ("exl3_2bpw", lambda M: exl3_case(KS, NS, M)),
-    ]
-    # 4- and 8-bit MLX affine packs (--all, or by name in --only)
-    for bits in (4, 8):
-        nm = f"affine{bits}_g64"
-        if args.all or nm in only:
-            plan.append((nm, lambda M, bits=bits: affine_nbit_case(NS, KS, M, bits)))
-    # the other GGUF formats (--all, or by name in --only)
-    for t in (ggml.Q2_K, ggml.IQ4_XS, ggml.IQ2_XXS, ggml.IQ2_S, ggml.IQ3_XXS, ggml.IQ3_S, ggml.IQ1_S, ggml.IQ1_M):
-        nm = ggml.NAMES[t].lower()
-        if args.all or nm in only:
-            plan.append((nm, lambda M, t=t: ggml_case(t, NS, KS, M)))
     fam_steps = max(50, args.steps // 2)
-    for name, b in plan:
+
+    def add(tag, name, builder, M, shape, nk=None, extra=None):
         if only and name not in only:
-            continue
+            return
+        r, _, _ = measure(name, builder, M, fam_steps, args.warmup, nk=nk, extra=extra)
+        r["config"] = tag
+        r["shape"] = shape
+        families.append(r)
+
+    # cfg0: GGUF Q4_0 4096x4096
+    for M in (1, 8):
+        add("cfg0", "q4_0", lambda M=M: ggml_case(ggml.Q4_0, 4096, 4096, M), M, "4096x4096", nk=(4096, 4096))
+    # cfg1: the headline family at every drafted row count
+    for M in (1, 2, 4, 8):
+        add("cfg1", "affine2_g64_wht128", lambda M=M: affine_case(NS, KS, M), M, f"{NS}x{KS}", nk=(NS, KS))
+    # cfg2: K- and i-quants at the Qwen-27B MLP shapes
+    for t, nm in ((ggml.Q4_K, "q4_k"), (ggml.Q6_K, "q6_k"), (ggml.IQ2_XS, "iq2_xs")):
+        for (N, K) in ((25600, 5120), (5120, 25600)):
+            for M in (1, 8):
+                add("cfg2", nm, lambda t=t, N=N, K=K, M=M: ggml_case(t, N, K, M), M, f"{N}x{K}", nk=(N, K))
+    # cfg3: EXL3 2 bpw
+    for M in (1, 2, 4, 8):
+        add("cfg3", "exl3_2bpw", lambda M=M: exl3_case(KS, NS, M), M, f"{NS}x{KS}", nk=(NS, KS))
+    # cfg4: MoE FFN
+    for T in (1, 8, 64):
+        add("cfg4", "moe_q4k_e128_h2048_i768_top8", lambda T=T: moe_case(T), T, "E128 H2048 I768 k8",
+            extra=lambda o: {"distinct_experts": int(o[3])})
+    # the north-star shape for the GGUF formats
+    for t, nm in ((ggml.Q4_0, "q4_0"), (ggml.Q4_K, "q4_k"), (ggml.Q6_K, "q6_k"), (ggml.IQ2_XS, "iq2_xs")):
         for M in (1, 8):
-            r, _, _ = measure(f"{name}", lambda b=b, M=M: b(M), M, fam_steps, args.warmup, nk=(NS, KS))
-            r["shape"] = f"{NS}x{KS}"
-            families.append(r)
-    if not only or "moe" in only:
-        for T in (1, 8, 64):
-            r, _, _ = measure("moe_q4k_e128_h2048_i768_top8", lambda T=T: moe_case(T), T, fam_steps, args.warmup,
-                              extra=lambda o: {"distinct_experts": int(o[3])})
-            families.append(r)
-    if args.all or "moe_affine4" in only:
-        for T in (1, 8, 64):
-            r, _, _ = measure("moe_affine4_g64_e128_h2048_i768_top8", lambda T=T: moe_affine_case(T), T, fam_steps,
-                              args.warmup, extra=lambda o: {"distinct_experts": int(o[3])})
-            families.append(r)
+            add("northstar", nm, lambda t=t, M=M: ggml_case(t, NS, KS, M), M, f"{NS}x{KS}", nk=(NS, KS))
     if args.all:
-        for M in (1,):
-            r, _, _ = measure("q4_0_cfg0", lambda: ggml_case(ggml.Q4_0, 4096, 4096, 1), 1, fam_steps, args.warmup)
-            r["shape"] = "4096x4096"
-            families.append(r)
-        for t, nm in ((ggml.Q4_K, "q4_k"), (ggml.Q6_K, "q6_k"), (ggml.IQ2_XS, "iq2_xs")):
-            for (N, K) in ((25600, 5120), (5120, 25600)):
-                for M in (1, 8):
-                    r, _, _ = measure(f"{nm}_mlp", lambda t=t, N=N, K=K, M=M: ggml_case(t, N, K, M), M, fam_steps,
-                                      args.warmup, nk=(N, K))
-                    r["shape"] = f"{N}x{K}"
-                    families.append(r)
-        for M in (2, 4):
-            r, _, _ = measure("affine2_g64_wht128", lambda M=M: affine_case(NS, KS, M), M, fam_steps, args.warmup,
-                              nk=(NS, KS))
-            families.append(r)
-            r, _, _ = measure("exl3_2bpw", lambda M=M: exl3_case(KS, NS, M), M, fam_steps, args.warmup, nk=(NS, KS))
-            families.append(r)
+        for bits in (4, 8):
+            for M in (1, 8):
+                add("extra", f"affine{bits}_g64", lambda M=M, bits=bits: affine_nbit_case(NS, KS, M, bits), M,
+                    f"{NS}x{KS}", nk=(NS, KS))
+        for t in (ggml.Q2_K, ggml.IQ4_XS, ggml.IQ2_XXS, ggml.IQ2_S, ggml.IQ3_XXS, ggml.IQ3_S, ggml.IQ1_S, ggml.IQ1_M):
+            for M in (1, 8):
+                add("extra", ggml.NAMES[t].lower(), lambda t=t, M=M: ggml_case(t, NS, KS, M), M, f"{NS}x{KS}",
+                    nk=(NS, KS))
+        for T in (1, 8, 64):
+            add("extra", "moe_affine4_g64_e128_h2048_i768_top8", lambda T=T: moe_affine_case(T), T,
+                "E128 H2048 I768 k8", extra=lambda o: {"distinct_experts": int(o[3])})
 
     # ------------------------------------------------------------------ CPU baseline
     cpu = None
     if not args.no_cpu:
+        import ctypes
+
         import oracle
-        threads = os.cpu_count() or 1
-        rows = 2048
-        codes, s, b = synth.affine_pack(rows, KS, group=64, seed=2)
-        x = synth.fp16_normal((1, KS), seed=3).astype(np.float32)
-        xr = oracle.hadamard(x, 128, synth.hadamard_signs(KS, seed=4)).astype(np.float16).astype(np.float32)
-        oracle.affine_matmul(xr, codes, s.view(np.uint16), b.view(np.uint16), rows, 2, 64, threads=threads)
-        t0 = time.perf_counter()
-        reps = 0
-        while time.perf_counter() - t0 < 10.0 and reps < 200:
-            xr = oracle.hadamard(x, 128, synth.hadamard_signs(KS, seed=4)).astype(np.float16).astype(np.float32)
-            oracle.affine_matmul(xr, codes, s.view(np.uint16), b.view(np.uint16), rows, 2, 64, threads=threads)
-            reps += 1
-        dt = (time.perf_counter() - t0) / reps
-        row_bytes = KS // 4 + 2 * 2 * (KS // 64)
-        cpu = {"value": round(rows * row_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-               "sample": f"oracle rotate + dequantize-then-fp32-dot of {rows} of {NS} rows (K={KS}, M=1), "
-                         f"{reps} reps over {dt * reps:.1f} s, OpenMP {threads} threads"}
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count() or 1
+        codes, sc, bi = synth.affine_pack(NS, KS, group=64, seed=2)
+        xh = synth.fp16_normal((1, KS), seed=3).view(np.uint16)
+        signs = synth.hadamard_signs(KS, seed=4)
+        yc = np.zeros(NS, np.float32)
+        P = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+        L = oracle.lib()
+        med = {}
+        for variant in (0, 1):
+            med[variant] = L.ishzo_bench_affine_linear(P(xh), KS, P(signs), 128, P(codes.view(np.uint32)),
+                                                       P(sc.view(np.uint16)), P(bi.view(np.uint16)), NS, 64,
+                                                       variant, 10, threads, P(yc))
+        wb = head["weight_bytes"]
+        cpu = {"value": round(wb / med[0] / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+               "us_per_call": round(med[0] * 1e6, 1),
+               "sample": f"the full headline call ({NS}x{KS}, M=1): oracle/ishz_oracle.c rotate + dequantize-then-"
+                         f"fp32-dot, OpenMP {threads} threads, median of 10 calls timed in C",
+               "fused_decode_dot": {"value": round(wb / med[1] / 1e9, 3), "us_per_call": round(med[1] * 1e6, 1)}}
 
     us = head_sec * 1e6
     line = {

@@ -449,7 +449,7 @@ template <int GS>
 static int affine_verify_launch(const void *x, int M, int K, const uint32_t *codes,
                                 const void *scales, const void *biases, int bf16s, int N, void *y,
                                 hipStream_t st) {
-  if (K % 256 == 0 && !getenv("ISHZ_OLD_VERIFY"))
+  if (K % 256 == 0)
     return bf16s ? affine_vgemm_nq<GS, true>(x, M, K, codes, scales, biases, N, y, st)
                  : affine_vgemm_nq<GS, false>(x, M, K, codes, scales, biases, N, y, st);
   constexpr int T = 2;
@@ -564,9 +564,9 @@ extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, cons
     if (rc) return rc;
     return affine_nbit_dispatch(workspace, M, K, codes, scales, biases, bf16s, N, bits, group, y, st);
   }
-  if (block == 0 || (M == 1 && !getenv("ISHZ_M1_MFMA")))
+  if (block == 0 || M == 1)
     return affine_dispatch(x, M, K, signs, block, codes, scales, biases, bf16s, N, group, y, st);
-  if (block <= 128 && K % 256 == 0 && !getenv("ISHZ_OLD_VERIFY")) {
+  if (block <= 128 && K % 256 == 0) {
     // x rotated and staged once into the workspace (every token's image), else the rotation is
     // fused into each workgroup's staging
     const u4 *img = nullptr;

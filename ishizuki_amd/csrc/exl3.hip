@@ -36,38 +36,37 @@ DEV _Float16 exl3_decode(uint32_t s, int cb) {
   return __builtin_bit_cast(_Float16, (uint16_t)x) + __builtin_bit_cast(_Float16, (uint16_t)(x >> 16));
 }
 
+// Where the states lie in a tile's bit ring. At an integer rate of KA bits per weight, position p
+// consumes KA bits and its state ends at ring bit KA (p + 1). At a half rate (KA + 1/2 bits) an
+// even/odd pair consumes 2 KA + 1 bits, the even position KA of them and the odd one KA + 1. A
+// state is the 16 ring bits ending there, read MSB first (bit 0 is the top bit of word 0), so it
+// reaches back into the bits of earlier positions and wraps around the ring.
 template <int KA, bool HALF>
 struct Trellis {
-  static constexpr int RING = HALF ? 128 * (2 * KA + 1) : 256 * KA;
+  static constexpr int RING = HALF ? 128 * (2 * KA + 1) : 256 * KA;  // bits per 16x16 tile
   static constexpr int WORDS = RING / 32;
-  static DEV int end(int p) {
-    return HALF ? (p >> 1) * (2 * KA + 1) + KA + (p & 1) * (KA + 1) : (p + 1) * KA;
+  static __host__ __device__ constexpr int bit_end(int p) {
+    return HALF ? (p / 2) * (2 * KA + 1) + KA + (p % 2) * (KA + 1) : (p + 1) * KA;
   }
-  // Bit offsets (after the window start) where the states of p0..p0+3 end; p0 is even.
-  static constexpr int rel(int i) {
-    return HALF ? 16 + (i >> 1) * (2 * KA + 1) + (i & 1) * (KA + 1) : 16 + i * KA;
+  // First ring bit of position p's state.
+  static DEV int first_bit(int p) { return (bit_end(p) + RING - 16) % RING; }
+  // Start of the state of position p0 + i relative to that of p0 (p0 even).
+  static constexpr int offset(int i) { return bit_end(i) - bit_end(0); }
+  // The 16-bit state starting at ring bit b: the 32 bits from b are one funnel shift of the word
+  // holding b and the next word (b on a word boundary: that word alone); the state is the top half.
+  static DEV uint32_t state(const uint32_t *tile, int b) {
+    const int w = b >> 5, o = b & 31;
+    const uint32_t hi = tile[w];
+    const uint32_t bits32 = o ? __builtin_amdgcn_alignbit(hi, tile[(w + 1) % WORDS], 32 - o) : hi;
+    return bits32 >> 16;
   }
-  // Per-lane constants for positions p0..p0+3: first word and shift of the 64-bit window.
-  struct Win {
-    int j0, j1, j2, sh;
-  };
-  static DEV Win window(int p0) {
-    const int lo = (end(p0) + RING - 16) % RING;
-    const int i0 = lo >> 5;
-    return {i0, (i0 + 1) % WORDS, (i0 + 2) % WORDS, lo & 31};
-  }
-  // Decode four weights from a tile's words; returns them as two packed fp16 pairs.
-  static DEV u2 decode4(const uint32_t *tile, const Win &wn, int cb) {
-    const uint64_t w0 = tile[wn.j0], w1 = tile[wn.j1], w2 = tile[wn.j2];
-    uint64_t a = ((w0 << 32) | w1) << wn.sh;
-    if (wn.sh) a |= w2 >> (32 - wn.sh);
-    uint16_t h[4];
+  // The four weights at positions p0 .. p0 + 3, as two packed fp16 pairs.
+  static DEV u2 decode4(const uint32_t *tile, int p0, int cb) {
+    uint32_t h[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t s = (uint32_t)(a >> (64 - rel(i))) & 0xffffu;
-      h[i] = __builtin_bit_cast(uint16_t, exl3_decode(s, cb));
-    }
-    return u2{(uint32_t)h[0] | (uint32_t)h[1] << 16, (uint32_t)h[2] | (uint32_t)h[3] << 16};
+    for (int i = 0; i < 4; i++)
+      h[i] = __builtin_bit_cast(uint16_t, exl3_decode(state(tile, (first_bit(p0) + offset(i)) % RING), cb));
+    return u2{h[0] | h[1] << 16, h[2] | h[3] << 16};
   }
 };
 
@@ -85,7 +84,7 @@ __global__ __launch_bounds__(1024) void exl3_mm(const uint16_t *__restrict__ xh,
   const int lane = threadIdx.x & 63, wave = wave_id(), KS = blockDim.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int tn = blockIdx.x, tiles_n = N / 16, tiles_k = K / 16;
-  const typename TR::Win wn = TR::window(8 * (4 * (j & 7) + g) + 4 * (j >> 3));
+  const int p0 = 8 * (4 * (j & 7) + g) + 4 * (j >> 3);
   const uint32_t *col = trellis + (size_t)tn * TR::WORDS;
   const size_t tstride = (size_t)tiles_n * TR::WORDS;
 
@@ -94,7 +93,7 @@ __global__ __launch_bounds__(1024) void exl3_mm(const uint16_t *__restrict__ xh,
     const uint16_t *xr = xh + (size_t)(tok ? j : 0) * K + 2 * g;
     f4 acc = {0, 0, 0, 0};
     for (int tk = wave; tk < tiles_k; tk += KS) {
-      const u2 B = TR::decode4(col + tk * tstride, wn, cb);
+      const u2 B = TR::decode4(col + tk * tstride, p0, cb);
       const u2 A = tok ? u2{*(const uint32_t *)(xr + 16 * tk), *(const uint32_t *)(xr + 16 * tk + 8)}
                        : u2{0, 0};
       acc = mfma16(as_h4(A), as_h4(B), acc);
@@ -113,7 +112,7 @@ __global__ __launch_bounds__(1024) void exl3_mm(const uint16_t *__restrict__ xh,
     const uint16_t *xr = xh + 2 * g;
     float acc = 0.0f;
     for (int tk = wave; tk < tiles_k; tk += KS) {
-      const u2 B = TR::decode4(col + tk * tstride, wn, cb);
+      const u2 B = TR::decode4(col + tk * tstride, p0, cb);
       acc = dot2(B.x, *(const uint32_t *)(xr + 16 * tk), acc);
       acc = dot2(B.y, *(const uint32_t *)(xr + 16 * tk + 8), acc);
     }
@@ -137,15 +136,17 @@ __global__ __launch_bounds__(1024) void exl3_mm(const uint16_t *__restrict__ xh,
 template <int KA, bool HALF>
 struct Trellis32 {
   using TR = Trellis<KA, HALF>;
-  static constexpr bool FITS = TR::rel(3) <= 32;
+  static constexpr bool FITS = TR::offset(3) <= 16;  // the four states within 32 bits
+  // The lane's 32-bit window (from the first bit of p0's state): words ja, jb funnel-shifted by amt.
   struct Win {
     int ja, jb, amt;
   };
   static DEV Win window(int p0) {
-    const int lo = (TR::end(p0) + TR::RING - 16) % TR::RING;
-    const int ja = lo >> 5, sh = lo & 31;
-    return sh ? Win{ja, (ja + 1) % TR::WORDS, 32 - sh} : Win{ja, ja, 0};
+    const int b = TR::first_bit(p0), w = b >> 5, o = b & 31;
+    return o ? Win{w, (w + 1) % TR::WORDS, 32 - o} : Win{w, w, 0};
   }
+  // Bit-field offset of state i inside the window.
+  static constexpr int field(int i) { return 16 - TR::offset(i); }
 };
 
 // Codebook images of two states, packed as fp16 (a in the low half): exl3_decode, pairwise.
@@ -236,10 +237,10 @@ __global__ __launch_bounds__(1024) void exl3_mm2(const uint16_t *__restrict__ xh
 #pragma unroll
       for (int t = 0; t < TN; t++) {
         const uint32_t win = __builtin_amdgcn_alignbit(r.w[t][0], r.w[t][1], wn.amt);
-        const uint32_t s0 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(0), 16);
-        const uint32_t s1 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(1), 16);
-        const uint32_t s2 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(2), 16);
-        const uint32_t s3 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(3), 16);
+        const uint32_t s0 = __builtin_amdgcn_ubfe(win, T32::field(0), 16);
+        const uint32_t s1 = __builtin_amdgcn_ubfe(win, T32::field(1), 16);
+        const uint32_t s2 = __builtin_amdgcn_ubfe(win, T32::field(2), 16);
+        const uint32_t s3 = __builtin_amdgcn_ubfe(win, T32::field(3), 16);
         const uint32_t b01 = exl3_decode2<CB>(s0, s1), b23 = exl3_decode2<CB>(s2, s3);
         if constexpr (MF) {
           const u2 A = live ? u2{r.xa, r.xb} : u2{0, 0};
@@ -399,10 +400,10 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
       for (int t = 0; t < TN; t++) {
         const uint32_t w0 = stage[t * W + wn.ja], w1 = stage[t * W + wn.jb];
         const uint32_t win = __builtin_amdgcn_alignbit(w0, w1, wn.amt);
-        const uint32_t s0 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(0), 16);
-        const uint32_t s1 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(1), 16);
-        const uint32_t s2 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(2), 16);
-        const uint32_t s3 = __builtin_amdgcn_ubfe(win, 32 - TR::rel(3), 16);
+        const uint32_t s0 = __builtin_amdgcn_ubfe(win, T32::field(0), 16);
+        const uint32_t s1 = __builtin_amdgcn_ubfe(win, T32::field(1), 16);
+        const uint32_t s2 = __builtin_amdgcn_ubfe(win, T32::field(2), 16);
+        const uint32_t s3 = __builtin_amdgcn_ubfe(win, T32::field(3), 16);
         if constexpr (HALVES) {
           float a = dot2(exl3_halves<CB>(s0), xd[0], acc[t]);
           a = dot2(exl3_halves<CB>(s1), xd[1], a);
@@ -478,7 +479,7 @@ __global__ __launch_bounds__(256) void exl3_dequant_kernel(const uint32_t *__res
   const int tiles_n = N / 16;
   if (tile >= (size_t)(K / 16) * tiles_n) return;
   const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
-  const u2 v = TR::decode4(trellis + tile * TR::WORDS, TR::window(8 * (4 * (j & 7) + g) + 4 * (j >> 3)), cb);
+  const u2 v = TR::decode4(trellis + tile * TR::WORDS, 8 * (4 * (j & 7) + g) + 4 * (j >> 3), cb);
   const size_t tk = tile / tiles_n, tn = tile % tiles_n;
   const uint16_t h[4] = {(uint16_t)v.x, (uint16_t)(v.x >> 16), (uint16_t)v.y, (uint16_t)(v.y >> 16)};
   const int rows[4] = {2 * g, 2 * g + 1, 2 * g + 8, 2 * g + 9};
@@ -621,12 +622,7 @@ extern "C" int ishz_exl3_rotate(const void *x, int in_dtype, int rows, int width
 // K splits of the wide-step kernel: about four workgroups per CU for one row, two with MFMA rows
 // (tn_blocks workgroups per split), at most 64.
 static int exl3_splits(int M, int K, int tn_blocks) {
-  static const int split_env = [] {
-    const char *e = getenv("ISHZ_EXL3_SPLITS");  // tuning
-    return e ? atoi(e) : 0;
-  }();
   const int tiles_k = K / 16;
-  if (split_env > 0) return std::min(split_env, tiles_k);
   return std::max(1, std::min({tiles_k / 4, (M == 1 ? 4 : 2) * num_cu_e() / tn_blocks, 64}));
 }
 
@@ -643,9 +639,8 @@ static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis
   while (ks < 16 && ks < tiles_k && wgs * ks < num_cu_e() * 16) ks *= 2;
   return by_rate(bits2, [&]<int KA, bool HALF>() -> int {
     if constexpr (!HALF && (KA == 1 || KA == 2 || KA == 4)) {
-      static const bool mm2 = getenv("ISHZ_EXL3_MM2") != nullptr;
       constexpr int TN = 32 / KA, KS3 = 4, D = 4;  // a step covers TN column tiles: N must tile by them
-      if (!getenv("ISHZ_EXL3_OLD") && !mm2 && (N / 16) % TN == 0) {
+      if ((N / 16) % TN == 0) {
         if (suh && M != 1) return einval("the fused input rotation is for one row");
         const int tn_blocks = N / 16 / TN;
         const int per = (tiles_k + exl3_splits(M, K, tn_blocks) - 1) / exl3_splits(M, K, tn_blocks);
@@ -677,15 +672,10 @@ static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis
     }
     if (suh) return einval("the fused input rotation needs the wide-step kernel");
     if constexpr (Trellis32<KA, HALF>::FITS) {
-      if (!getenv("ISHZ_EXL3_OLD")) {
-        // TN = 4 column tiles per workgroup (N % 128 == 0 makes N / 16 a multiple of 8); 8 waves
-        // split the K tiles.
-        constexpr int TN = 4;
-        static const int cfg = [] {
-          const char *e = getenv("ISHZ_EXL3_CFG");  // tuning: waves per workgroup x 100 + ring depth
-          return e ? atoi(e) : 404;
-        }();
-        const int KS2 = cfg / 100;
+      {
+        // TN = 4 column tiles per workgroup (N % 128 == 0 makes N / 16 a multiple of 8); 4 waves
+        // split the K tiles, each with a 4-deep prefetch ring.
+        constexpr int TN = 4, KS2 = 4;
         const size_t lds = M == 1 ? (size_t)KS2 * TN * 16 * 4 : (size_t)KS2 * TN * 256 * 4;
         auto go = [&]<int CB>() -> int {
           auto launch = [&]<int D>() {
@@ -696,8 +686,7 @@ static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis
               hipLaunchKernelGGL((exl3_mm2<KA, HALF, CB, true, TN, D>), dim3(N / 16 / TN), dim3(64 * KS2), lds,
                                  st, (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, yh);
           };
-          if (cfg % 100 == 4) launch.template operator()<4>();
-          else launch.template operator()<8>();
+          launch.template operator()<4>();
           ISHZ_LAUNCH_CHECK("exl3 matvec launch");
           return ISHZ_OK;
         };
@@ -732,9 +721,8 @@ extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const
 // workgroup rotates ~8x the blocks before its first MFMA, which measured slower (17408x5120 at
 // 2 bpw: 37.8 us against 34.7 us for the separate rotation launch).
 static bool exl3_fused_rotation(int M, int K, int N, int bits2) {
-  static const bool off = getenv("ISHZ_EXL3_OLD") || getenv("ISHZ_EXL3_MM2");
   const int KA = bits2 / 2;
-  if (M != 1 || off || !(bits2 == 2 || bits2 == 4 || bits2 == 8) || (N / 16) % (32 / KA)) return false;
+  if (M != 1 || !(bits2 == 2 || bits2 == 4 || bits2 == 8) || (N / 16) % (32 / KA)) return false;
   const int TN = 32 / KA, tiles_k = K / 16, splits = exl3_splits(M, K, N / 16 / TN);
   const size_t per = (tiles_k + splits - 1) / splits;
   const size_t own = 4 * 256 * 4 + (M == 1 ? (size_t)4 * TN * 16 * 4 : (size_t)TN * 256 * 4);

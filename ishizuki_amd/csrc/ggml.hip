@@ -12,12 +12,13 @@
 namespace ishz {
 
 // ----------------------------------------------------------------------------- tables in LDS
-// IQ2_XS grid entries as fp16 (values 8, 25, 43) and the 128 sign patterns of ksigns
-// (index | parity << 7) as fp16 sign-bit masks, either in the permuted pair order of the GEMV
-// (x0,x2,x1,x3,...) or in natural order for the MFMA B operand.
+// IQ2_XS grid entries as fp16 (values 8, 25, 43), either in the permuted pair order of the GEMV
+// (x0,x2,x1,x3,...) or in natural order for the MFMA B operand; with `sgn`, also the 128 sign
+// patterns of ksigns (index | parity << 7) as natural-order fp16 sign-bit masks (the GEMV computes
+// its masks in registers).
 template <bool PERM>
 DEV void build_iq2xs_tables(u4 *grid, u4 *sgn) {
-  for (int e = threadIdx.x; e < 512 + 128; e += blockDim.x) {
+  for (int e = threadIdx.x; e < 512 + (sgn ? 128 : 0); e += blockDim.x) {
     if (e < 512) {
       const uint64_t v = ishz_iq2xs_grid[e];
       uint32_t hv[8];
@@ -31,10 +32,7 @@ DEV void build_iq2xs_tables(u4 *grid, u4 *sgn) {
       const int i = e - 512;
       const uint32_t s = (uint32_t)i | (uint32_t)(__builtin_popcount(i) & 1) << 7;
       auto bit = [&](int j) { return ((s >> j) & 1u) << 15; };
-      sgn[i] = PERM ? u4{bit(0) | bit(2) << 16, bit(1) | bit(3) << 16, bit(4) | bit(6) << 16,
-                         bit(5) | bit(7) << 16}
-                    : u4{bit(0) | bit(1) << 16, bit(2) | bit(3) << 16, bit(4) | bit(5) << 16,
-                         bit(6) | bit(7) << 16};
+      sgn[i] = u4{bit(0) | bit(1) << 16, bit(2) | bit(3) << 16, bit(4) | bit(5) << 16, bit(6) | bit(7) << 16};
     }
   }
 }
@@ -340,8 +338,7 @@ static int launch_verify(const void *x, int M, int K, const void *w, int N, void
 
 template <class F>
 static int verify(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st) {
-  static const bool old = getenv("ISHZ_OLD_VERIFY") != nullptr;
-  if (M >= 2 && K % 256 == 0 && !old) return vgemm<F>(x, M, K, w, N, y, st);
+  if (M >= 2 && K % 256 == 0) return vgemm<F>(x, M, K, w, N, y, st);
   if (N >= 4096) return launch_verify<F, 2>(x, M, K, w, N, y, st);
   return launch_verify<F, 1>(x, M, K, w, N, y, st);
 }

@@ -60,13 +60,15 @@ struct GgmlGemv {
   // (fewer, longer waves amortise the x staging every workgroup repeats).
   static int occ(const Args &) { return 2; }
   static __host__ __device__ int units(int K) { return K / D::BS * D::UPB / D::UNIT_BLOCKS; }
-  static size_t extra_lds_bytes(const Args &) { return D::tab_bytes(); }
+  static size_t extra_lds_bytes(const Args &) { return D::gemv_tab_bytes(); }
   // LDS tables (codebooks, sign masks) the decoders index: bytes, and the builder every
   // workgroup runs once (GEMV: pair-permuted like x; verify: natural order). IQ2_XS's here;
   // formats with other tables replace all three.
   static constexpr size_t tab_bytes() { return D::GRID ? (512 + 128) * 16 : 0; }
+  // the GEMV reads IQ2_XS's codebook only (its sign masks are computed in registers)
+  static constexpr size_t gemv_tab_bytes() { return D::GRID ? 512 * 16 : D::tab_bytes(); }
   static DEV void gemv_tables(u4 *t) {
-    if constexpr (D::GRID) build_iq2xs_tables_perm(t, t + 512);
+    if constexpr (D::GRID) build_iq2xs_tables_perm(t, nullptr);
   }
   static DEV void vtables(u4 *t) {
     if constexpr (D::VGRID) build_iq2xs_tables_nat(t, t + 512);

@@ -46,19 +46,8 @@ DEV void tab_grid4(const uint32_t *g, int n, u2 *dst) {
     dst[e] = u2{h[0] | h[1] << 16, h[2] | h[3] << 16};
   }
 }
-// Sign masks: entry i flips the fp16 sign of weight j when bit j of the pattern is set. With
-// KSIGNS the pattern is ggml's ksigns_iq2xs[i] (7 stored bits plus an even-parity eighth).
-template <bool KSIGNS>
-DEV void tab_signs(u4 *dst) {
-  constexpr int n = KSIGNS ? 128 : 256;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const uint32_t s = KSIGNS ? ((uint32_t)i | (uint32_t)(__builtin_popcount(i) & 1) << 7) : (uint32_t)i;
-    auto bit = [&](int j) { return ((s >> j) & 1u) << 15; };
-    dst[i] = u4{bit(0) | bit(1) << 16, bit(2) | bit(3) << 16, bit(4) | bit(5) << 16, bit(6) | bit(7) << 16};
-  }
-}
-
-// The same masks computed in registers (no LDS read): word w is s * (2^(15-2w) + 2^(30-2w)),
+// Sign masks, computed in registers: bit j of the 8-bit pattern s flips the fp16 sign of weight j
+// (natural pair order). Word w is s * (2^(15-2w) + 2^(30-2w)),
 // whose two shifted copies of the 8-bit pattern occupy disjoint bits, so bits 15 and 31 hold signs
 // 2w and 2w + 1; everything else is masked off.
 DEV u4 sign_words(uint32_t s) {
@@ -249,11 +238,8 @@ struct FIQ2_XXS : GgmlQuarter<FIQ2_XXS> {
   static constexpr int VNS = 2, VDEPTH = 4, Q = 1, SUM_LEN = 32;
   static constexpr bool XSUM = false, XPERM = false;
   static constexpr float OFF = 0.0f;
-  static constexpr size_t TAB_BYTES = (256 + 128) * 16;
-  static DEV void build_tab(u4 *t) {
-    tab_grid8<false>(ishz_iq2xxs_grid, 256, t);
-    tab_signs<true>(t + 256);
-  }
+  static constexpr size_t TAB_BYTES = 256 * 16;
+  static DEV void build_tab(u4 *t) { tab_grid8<false>(ishz_iq2xxs_grid, 256, t); }
   static DEV int xk(int g, int r) { return 64 * g + 8 * r; }
   static DEV VRaw vload(const uint8_t *row, int j, int g) {
     const uint8_t *p = row + (size_t)j * TS;
@@ -285,11 +271,8 @@ struct FIQ2_S : GgmlQuarter<FIQ2_S> {
   static constexpr int VNS = 4, VDEPTH = 3, Q = 1, SUM_LEN = 16;
   static constexpr bool XSUM = false, XPERM = false;
   static constexpr float OFF = 0.0f;
-  static constexpr size_t TAB_BYTES = (1024 + 256) * 16;
-  static DEV void build_tab(u4 *t) {
-    tab_grid8<false>(ishz_iq2s_grid, 1024, t);
-    tab_signs<false>(t + 1024);
-  }
+  static constexpr size_t TAB_BYTES = 1024 * 16;
+  static DEV void build_tab(u4 *t) { tab_grid8<false>(ishz_iq2s_grid, 1024, t); }
   static DEV int xk(int g, int r) { return 64 * g + 8 * r; }
   static DEV VRaw vload(const uint8_t *row, int j, int g) {
     const uint8_t *p = row + (size_t)j * TS;
@@ -327,18 +310,15 @@ struct FIQ3_XXS : GgmlQuarter<FIQ3_XXS> {
   static constexpr int VNS = 2, VDEPTH = 3, Q = 1, SUM_LEN = 32;
   static constexpr bool XSUM = false, XPERM = false;
   static constexpr float OFF = 0.0f;
-  static constexpr size_t TAB_BYTES = 128 * 16 + 256 * 8;
-  static DEV void build_tab(u4 *t) {
-    tab_signs<true>(t);
-    tab_grid4(ishz_iq3xxs_grid, 256, (u2 *)(t + 128));
-  }
+  static constexpr size_t TAB_BYTES = 256 * 8;
+  static DEV void build_tab(u4 *t) { tab_grid4(ishz_iq3xxs_grid, 256, (u2 *)t); }
   static DEV int xk(int g, int r) { return 64 * g + 8 * r; }
   static DEV VRaw vload(const uint8_t *row, int j, int g) {
     const uint8_t *p = row + (size_t)j * TS;
     return {ld16<2>(p + 2 + 16 * g), ld8<2>(p + 66 + 8 * g), ld2(p)};
   }
   static DEV void vdecode(const VRaw &r, u4 *B, uint32_t, const u4 *t, const u4 *) {
-    const u2 *grid = (const u2 *)(t + 128);
+    const u2 *grid = (const u2 *)t;
 #pragma unroll
     for (int h = 0; h < 2; h++)
 #pragma unroll
@@ -368,11 +348,8 @@ struct FIQ3_S : GgmlQuarter<FIQ3_S> {
   static constexpr int VNS = 2, VDEPTH = 3, Q = 1, SUM_LEN = 32;
   static constexpr bool XSUM = false, XPERM = false;
   static constexpr float OFF = 0.0f;
-  static constexpr size_t TAB_BYTES = 256 * 16 + 512 * 8;
-  static DEV void build_tab(u4 *t) {
-    tab_signs<false>(t);
-    tab_grid4(ishz_iq3s_grid, 512, (u2 *)(t + 256));
-  }
+  static constexpr size_t TAB_BYTES = 512 * 8;
+  static DEV void build_tab(u4 *t) { tab_grid4(ishz_iq3s_grid, 512, (u2 *)t); }
   static DEV int xk(int g, int r) { return 64 * g + 8 * r; }
   static DEV VRaw vload(const uint8_t *row, int j, int g) {
     const uint8_t *p = row + (size_t)j * TS;
@@ -380,7 +357,7 @@ struct FIQ3_S : GgmlQuarter<FIQ3_S> {
   }
   // Index 2l of sub-block ib takes its 9th bit from bit 2l of qh[ib], index 2l + 1 from bit 2l + 1.
   static DEV void vdecode(const VRaw &r, u4 *B, uint32_t, const u4 *t, const u4 *) {
-    const u2 *grid = (const u2 *)(t + 256);
+    const u2 *grid = (const u2 *)t;
 #pragma unroll
     for (int h = 0; h < 2; h++) {
       const uint32_t qh = byte_of(r.qh, h);

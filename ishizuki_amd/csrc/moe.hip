@@ -511,12 +511,8 @@ struct FMoeDown : F {
 // an expert with more tokens takes further passes.
 template <class F, class P>
 static int moe_vgemm(const P &p, int T, int E, int k, int K, int rows, int groups, int tiles_per_wg, hipStream_t st) {
-  static const int nq_env = [] {
-    const char *e = getenv("ISHZ_MOE_NQ");  // tuning: token quads per pass
-    return e ? atoi(e) : 0;
-  }();
   const int want = (2 * T * k / std::max(E, 1) + 2 + 3) / 4;
-  switch (nq_env > 0 ? nq_env : std::max(1, std::min({4, (T + 3) / 4, want}))) {
+  switch (std::max(1, std::min({4, (T + 3) / 4, want}))) {
     case 1: return launch_vgemm_p<F, P, 1>(p, K, rows, groups, tiles_per_wg, st);
     case 2: return launch_vgemm_p<F, P, 2>(p, K, rows, groups, tiles_per_wg, st);
     case 3: return launch_vgemm_p<F, P, 3>(p, K, rows, groups, tiles_per_wg, st);
@@ -574,9 +570,8 @@ static int ks_for(int tiles, int nblk) {
 // One or two tokens take the gathered GEMVs when down's LDS (every pair's staged h and x image,
 // about 2 I + 2.9 I bytes per pair) fits; otherwise the per-block kernels.
 static bool gathered_gemv(int T, int H, int I, int k) {
-  static const bool old = getenv("ISHZ_OLD_MOE") != nullptr;
   const size_t per_pair = (size_t)2 * I + ((size_t)I / 64 + 15) / 16 * 16 * (8 * 16 + 4 * 4);
-  return H % 256 == 0 && I % 256 == 0 && T <= 2 && !old && (size_t)T * k * per_pair <= 144 * 1024;
+  return H % 256 == 0 && I % 256 == 0 && T <= 2 && (size_t)T * k * per_pair <= 144 * 1024;
 }
 
 template <class F>
@@ -584,7 +579,6 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
                    const void *up, const void *down, MoeRoute R, uint16_t *h, uint16_t *gu, uint16_t *o,
                    void *y, hipStream_t st) {
   const int amax = std::min(E, T * k);
-  static const bool old = getenv("ISHZ_OLD_MOE") != nullptr;
   const size_t total = (size_t)T * H;
   // one or two tokens: every (token, slot) pair is a GEMV; two launches of the streaming GEMV
   if (gathered_gemv(T, H, I, k)) {
@@ -603,7 +597,7 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
   }
   // streaming MFMA kernels from 3 tokens up; one or two tokens (a GEMV per expert) run faster on
   // the per-block kernels below, which start streaming without staging x
-  if (H % 256 == 0 && I % 256 == 0 && T > 2 && !old) {
+  if (H % 256 == 0 && I % 256 == 0 && T > 2) {
     // tiles per workgroup: about two workgroups per CU over the routed experts (gate/up: an even
     // count, whole SwiGLU pairs); with 8 or more a wave takes whole tiles
     const int tiles_gu = 2 * ((I + 15) / 16), tiles_dn = (H + 15) / 16;

@@ -49,6 +49,7 @@ def lib():
             "ishzo_exl3_apply": (I, [P, I, I, P, P, P, I, I, I, P, I]),
             "ishzo_moe_route": (None, [P, I, I, I, I, P, P]),
             "ishzo_moe_swiglu": (I, [U, P, I, I, P, P, I, P, P, P, I, I, P, I]),
+            "ishzo_bench_affine_linear": (ctypes.c_double, [P, I, P, I, P, P, P, I, I, I, I, I, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)

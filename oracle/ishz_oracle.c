@@ -12,6 +12,7 @@
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 #ifdef _OPENMP
 #include <omp.h>
 #endif
@@ -494,6 +495,86 @@ int ishzo_affine_matmul(const float *x, int M, int K, const uint32_t *codes,
   }
   free(w);
   return rc;
+}
+
+/* ---------------------------------------------------------------- CPU baseline (bench.py only) */
+
+static double now_s(void) {
+  struct timespec t;
+  clock_gettime(CLOCK_MONOTONIC, &t);
+  return (double)t.tv_sec + 1e-9 * (double)t.tv_nsec;
+}
+
+static int cmp_double(const void *a, const void *b) {
+  double x = *(const double *)a, y = *(const double *)b;
+  return (x > y) - (x < y);
+}
+
+/* One rotated 2-bit affine GEMV (PackedLinear's rotated path, Core/Hadamard.swift:180-231) on the
+   CPU: x (fp16) is rotated by hadamardRotate and rounded to fp16, then y = x.W^T with
+     variant 0: W dequantized in full into a dense fp32 [N][K] (the reference's CPU definition of
+                a quantized matmul: dequantize, then an fp32 dot per output),
+     variant 1: each word's 16 codes decoded inside the dot, per group
+                s * sum(q x) + b * sum(x), no dense W.
+   OpenMP over output rows. Each of `reps` calls is timed separately; returns the median seconds.
+   y gets the last call's output (fp32). */
+double ishzo_bench_affine_linear(const uint16_t *xh, int K, const float *signs, int block,
+                                 const uint32_t *codes, const uint16_t *scales, const uint16_t *biases,
+                                 int N, int group, int variant, int reps, int threads, float *y) {
+  if (K % group || K % 16 || reps < 1 || reps > 64) return -1.0;
+  set_threads(threads);
+  const int wpr = K / 16, gpr = K / group;
+  float *xr = (float *)malloc((size_t)K * sizeof(float));
+  float *xs = (float *)malloc((size_t)gpr * sizeof(float));
+  float *w = variant == 0 ? (float *)malloc((size_t)N * (size_t)K * sizeof(float)) : NULL;
+  if (!xr || !xs || (variant == 0 && !w)) {
+    free(xr);
+    free(xs);
+    free(w);
+    return -1.0;
+  }
+  double t[64];
+  for (int r = 0; r < reps; r++) {
+    double t0 = now_s();
+    for (int k = 0; k < K; k++) xr[k] = ishzo_half_to_float(xh[k]);
+    if (block > 1) ishzo_hadamard(xr, 1, K, block, signs, 0, xr);
+    for (int k = 0; k < K; k++) xr[k] = ishzo_half_to_float(ishzo_float_to_half(xr[k]));
+    if (variant == 0) {
+      ishzo_affine_dequant(codes, scales, biases, N, K, 2, group, w);
+#pragma omp parallel for schedule(static)
+      for (int n = 0; n < N; n++) y[n] = dot_f32(xr, w + (size_t)n * K, K);
+    } else {
+      for (int g = 0; g < gpr; g++) {
+        float a = 0.0f;
+        for (int k = g * group; k < (g + 1) * group; k++) a += xr[k];
+        xs[g] = a;
+      }
+#pragma omp parallel for schedule(static)
+      for (int n = 0; n < N; n++) {
+        const uint32_t *row = codes + (size_t)n * wpr;
+        float acc = 0.0f;
+        for (int g = 0; g < gpr; g++) {
+          float qx = 0.0f;
+          for (int c = g * group / 16; c < (g + 1) * group / 16; c++) {
+            const uint32_t word = row[c];
+            const float *xv = xr + 16 * c;
+            float part = 0.0f;
+            for (int j = 0; j < 16; j++) part += (float)((word >> (2 * j)) & 3u) * xv[j];
+            qx += part;
+          }
+          acc += ishzo_half_to_float(scales[(size_t)n * gpr + g]) * qx +
+                 ishzo_half_to_float(biases[(size_t)n * gpr + g]) * xs[g];
+        }
+        y[n] = acc;
+      }
+    }
+    t[r] = now_s() - t0;
+  }
+  free(xr);
+  free(xs);
+  free(w);
+  qsort(t, (size_t)reps, sizeof(double), cmp_double);
+  return reps % 2 ? t[reps / 2] : 0.5 * (t[reps / 2 - 1] + t[reps / 2]);
 }
 
 /* ---------------------------------------------------------------- Hadamard */

@@ -59,6 +59,13 @@ int ishzo_affine_matmul(const float *x, int M, int K, const uint32_t *codes,
                         const uint16_t *scales, const uint16_t *biases, int N, int bits,
                         int group, float *y, int threads);
 
+/* CPU baseline of the rotated 2-bit affine GEMV (bench.py's cpu_baseline leg): rotate x, then
+   variant 0 dequantize-then-dot or variant 1 fused decode-dot; OpenMP over rows; the median of
+   `reps` (<= 64) timings in seconds (negative on bad arguments). y: fp32 [N]. */
+double ishzo_bench_affine_linear(const uint16_t *xh, int K, const float *signs, int block,
+                                 const uint32_t *codes, const uint16_t *scales, const uint16_t *biases,
+                                 int N, int group, int variant, int reps, int threads, float *y);
+
 /* Blockwise normalised Walsh-Hadamard (Sylvester order) in fp32: y = WHT_b(x*signs)/sqrt(b)
    (inverse: signs applied after). signs may be NULL (all +1). x and y may alias. */
 void ishzo_hadamard(const float *x, int rows, int width, int block, const float *signs,

@@ -36,3 +36,29 @@ def test_modulemap_names_the_header():
     here = os.path.dirname(_lib.HEADER)
     text = open(os.path.join(here, "module.modulemap")).read()
     assert 'header "ishizuki_hip.h"' in text and 'link "ishizuki_hip"' in text
+
+
+def test_header_compiles_as_c11_and_links(tmp_path):
+    """A C caller (what the Swift module map imports) compiles against the header with gcc
+    -std=c11 -Wall -Werror, links against the library, and gets the library's answers back: the
+    version, the block geometry and a decline that never reaches the GPU."""
+    import subprocess
+    src = tmp_path / "caller.c"
+    src.write_text(r'''
+#include "ishizuki_hip.h"
+#include <stdio.h>
+#include <string.h>
+int main(void) {
+  char dummy[16] = {0};
+  int rc = ishz_ggml_matvec(12, dummy, ISHZ_DT_F16, 17, 256, dummy, 1u << 20, 4, dummy, NULL);
+  printf("%d %d %d %d %d\n", ishz_version() >= 100, ishz_ggml_block_size(12), ishz_ggml_type_size(14),
+         rc == ISHZ_DECLINED, strstr(ishz_last_error(), "declined") != NULL);
+  return 0;
+}
+''')
+    exe = tmp_path / "caller"
+    libdir = os.path.dirname(_lib.LIB_PATH)
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Wextra", "-Werror", "-pedantic", "-I", os.path.dirname(_lib.HEADER),
+                    str(src), "-L", libdir, "-lishizuki_hip", f"-Wl,-rpath,{libdir}", "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
+    assert out == ["1", "256", "210", "1", "1"]

@@ -260,3 +260,30 @@ def test_moe_swiglu_pinned():
     w2[:, -1] = 0
     y2 = oracle.moe_swiglu(t_, x, ids, w2, gate, up, down, E, I)
     assert not np.all(np.abs(y2 - want) <= 2.0 ** -10 * bound + 2.0 ** -11 * np.abs(want) + 2.0 ** -24)
+
+
+def test_cpu_baseline_matches_the_oracle():
+    """bench.py's cpu_baseline leg (ishzo_bench_affine_linear): the dequantize-then-dot variant is
+    the oracle's rotate + affine_matmul bit for bit; the fused decode-dot differs only in
+    summation order."""
+    import ctypes
+
+    from ishizuki_amd import synth
+    N, K = 96, 1024
+    codes, s, b = synth.affine_pack(N, K, group=64, seed=2)
+    x = synth.fp16_normal((1, K), seed=3)
+    sg = synth.hadamard_signs(K, seed=4)
+    P = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    L = oracle.lib()
+    ys = []
+    for variant in (0, 1):
+        y = np.zeros(N, np.float32)
+        t = L.ishzo_bench_affine_linear(P(x.view(np.uint16)), K, P(sg), 128, P(codes.view(np.uint32)),
+                                        P(s.view(np.uint16)), P(b.view(np.uint16)), N, 64, variant, 3, 2, P(y))
+        assert t > 0
+        ys.append(y)
+    xr = oracle.hadamard(x.astype(np.float32), 128, sg).astype(np.float16).astype(np.float32)
+    ref = oracle.affine_matmul(xr, codes, s.view(np.uint16), b.view(np.uint16), N, 2, 64)
+    assert np.array_equal(ys[0], ref[0])
+    bound = np.abs(xr[0]) @ np.abs(oracle.affine_dequant(codes, s.view(np.uint16), b.view(np.uint16), N, K, 2, 64)).T
+    assert np.all(np.abs(ys[1] - ref[0]) <= 1e-5 * bound + 1e-6)
