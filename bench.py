@@ -291,7 +291,7 @@ def main():
         wsb = L.ishz_moe_workspace_size(T, H, E, I, k)
         wsp = torch.empty(wsb, dtype=torch.uint8, device=dev)
         calls = [lambda e=e: L.ishz_moe_swiglu(ggml.Q4_K, ptr(x), 1, T, H, ptr(logits), E, k, 1, ptr(e.gate),
-                                               ptr(e.up), ptr(e.down), e.expert_bytes, I, ptr(y), None, None,
+                                               ptr(e.up), ptr(e.down), e.expert_bytes, I, None, None, ptr(y), None, None,
                                                ptr(wsp), wsb, torch.cuda.current_stream().cuda_stream) for e in exs]
         calls[0]()
         torch.cuda.synchronize()
@@ -321,7 +321,8 @@ def main():
         wsb = L.ishz_moe_workspace_size(T, H, E, I, k)
         wsp = torch.empty(wsb, dtype=torch.uint8, device=dev)
         calls = [lambda c=c: L.ishz_moe_swiglu_affine(
-            ptr(x), 1, T, H, ptr(logits), E, k, 1, *(ptr(t) for p in c for t in p), 1, bits, 64, I, ptr(y), None, None,
+            ptr(x), 1, T, H, ptr(logits), E, k, 1, *(ptr(t) for p in c for t in p), 1, bits, 64, I, None, None, ptr(y),
+            None, None,
             ptr(wsp), wsb, torch.cuda.current_stream().cuda_stream) for c in copies]
         nb = distinct * per_expert
         return calls, nb, nb, distinct

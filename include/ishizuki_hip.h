@@ -168,10 +168,12 @@ int ishz_moe_route(const float *logits, int T, int E, int topk, int normalize, i
    down(silu(gate(x)) * up(x)) with fp16 intermediates, weighted and summed in fp32 into
    y [T][H] (fp16). gate/up hold E experts of [I][H] blocks back to back, down E experts of
    [H][I]; expert_bytes is the size of one expert's matrix. Only routed experts' blocks are
-   read. type: Q4_K (also Q4_0, Q6_K). ids_out / weights_out (optional, [T][topk]) receive the
-   routing. workspace: ishz_moe_workspace_size bytes. (The reference runs this through MLX's
-   gatherQuantizedMM over affine experts; GGUF experts are a composition of its routing with the
-   GGML kernels.) */
+   read. type: Q4_K (also Q4_0, Q6_K). shared / shared_gate (optional, both or neither): the
+   shared expert's output shared(x) [T][H] and gate logit sharedGate(x) [T], fp16, computed by
+   the caller's own projections; sigmoid(gate) * shared is added in fp32 before the one cast
+   (:158-160). ids_out / weights_out (optional, [T][topk]) receive the routing. workspace:
+   ishz_moe_workspace_size bytes. (The reference runs this through MLX's gatherQuantizedMM over
+   affine experts; GGUF experts are a composition of its routing with the GGML kernels.) */
 size_t ishz_moe_workspace_size(int T, int H, int E, int I, int topk);
 
 /* The same FFN over MLX affine stacked experts, the reference's own expert format
@@ -184,13 +186,14 @@ int ishz_moe_swiglu_affine(const void *x, int x_dtype, int T, int H, const float
                            const void *gate_biases, const uint32_t *up_codes, const void *up_scales,
                            const void *up_biases, const uint32_t *down_codes, const void *down_scales,
                            const void *down_biases, int scale_dtype, int bits, int group, int I,
-                           void *y, int32_t *ids_out, float *weights_out, void *workspace,
-                           size_t workspace_bytes, ishz_stream_t stream);
+                           const void *shared, const void *shared_gate, void *y, int32_t *ids_out,
+                           float *weights_out, void *workspace, size_t workspace_bytes,
+                           ishz_stream_t stream);
 int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T, int H, const float *logits,
                     int E, int topk, int normalize, const void *gate, const void *up,
-                    const void *down, size_t expert_bytes, int I, void *y, int32_t *ids_out,
-                    float *weights_out, void *workspace, size_t workspace_bytes,
-                    ishz_stream_t stream);
+                    const void *down, size_t expert_bytes, int I, const void *shared,
+                    const void *shared_gate, void *y, int32_t *ids_out, float *weights_out,
+                    void *workspace, size_t workspace_bytes, ishz_stream_t stream);
 
 /* ---------------------------------------------------------------- GGUF container (host side)
  * GGUFFile (Config/GGUFFile.swift:179-397): header, metadata and tensor table of a .gguf file,

@@ -36,8 +36,9 @@ _SIGS = {
     "ishz_exl3_apply_static": (I, [P, I, I, I, P, P, P, I, I, I, P, P]),
     "ishz_moe_route": (I, [P, I, I, I, I, P, P, P]),
     "ishz_moe_workspace_size": (SZ, [I, I, I, I, I]),
-    "ishz_moe_swiglu": (I, [U32, P, I, I, I, P, I, I, I, P, P, P, SZ, I, P, P, P, P, SZ, P]),
-    "ishz_moe_swiglu_affine": (I, [P, I, I, I, P, I, I, I, P, P, P, P, P, P, P, P, P, I, I, I, I, P, P, P, P, SZ, P]),
+    "ishz_moe_swiglu": (I, [U32, P, I, I, I, P, I, I, I, P, P, P, SZ, I, P, P, P, P, P, P, SZ, P]),
+    "ishz_moe_swiglu_affine": (I, [P, I, I, I, P, I, I, I, P, P, P, P, P, P, P, P, P, I, I, I, I, P, P, P, P, P, P, SZ,
+                                   P]),
     "ishz_ggml_type_known": (I, [U32]),
     "ishz_ggml_geometry": (I, [U32, ctypes.POINTER(I), ctypes.POINTER(I)]),
     "ishz_gguf_open": (I, [ctypes.c_char_p, ctypes.POINTER(P)]),

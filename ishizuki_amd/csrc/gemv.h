@@ -71,6 +71,30 @@ __host__ __device__ int gemv_nx(const typename F::Args &a) {
   else return 1;
 }
 
+// Optional format hooks. prepare(args, lds, xs): runs first, before any weight load, and returns a
+// value handed to every load(args, prep, row, u) (the gathered-expert formats route their tokens
+// there, so the loads know which expert a row reads). group_align(args, RPW): workgroup row
+// ranges start on multiples of this many row groups. store(args, y, row0, nrows, vals): writes
+// the workgroup's outputs from their final dots in LDS (vals[i] is row row0 + i). X_ALL: every x
+// image is staged (image i at slot i), not only those of the workgroup's rows.
+template <class F>
+__host__ __device__ constexpr bool gemv_has_prepare() {
+  return requires { &F::prepare; };
+}
+template <class F>
+__host__ __device__ constexpr bool gemv_has_align() {
+  return requires(const typename F::Args &a) { F::group_align(a, 1); };
+}
+template <class F>
+__host__ __device__ constexpr bool gemv_has_store() {
+  return requires { &F::store; };
+}
+template <class F>
+__host__ __device__ int gemv_align(const typename F::Args &a, int rpw) {
+  if constexpr (gemv_has_align<F>()) return F::group_align(a, rpw);
+  else return 1;
+}
+
 // Threads per workgroup: F::WG where the format sets it (the workgroup shares one staged copy of
 // x, so a larger one stages fewer copies, each with more waves), else 256.
 template <class F>
@@ -97,10 +121,11 @@ __global__ __launch_bounds__(gemv_threads<F>()) void gemv_kernel(typename F::Arg
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int sub = lane % LPR, rg = lane / LPR;
   const int upl = (units + LPR - 1) / LPR;  // units per lane per row
-  // workgroup b of nwg owns row groups [b G / nwg, (b + 1) G / nwg); their upl unit batches per
-  // group are dealt to its waves in equal contiguous ranges [tb, te)
-  const int G = (N + RPW - 1) / RPW;
-  const int gf = (int)((long long)blockIdx.x * G / nwg), gend = (int)((long long)(blockIdx.x + 1) * G / nwg);
+  // workgroup b of nwg owns row groups [b G / nwg, (b + 1) G / nwg) (in units of GA groups);
+  // their upl unit batches per group are dealt to its waves in equal contiguous ranges [tb, te)
+  const int G = (N + RPW - 1) / RPW, GA = gemv_align<F>(args, RPW), GU = (G + GA - 1) / GA;
+  const int gf = min((int)((long long)blockIdx.x * GU / nwg) * GA, G);
+  const int gend = min((int)((long long)(blockIdx.x + 1) * GU / nwg) * GA, G);
   const int T = (gend - gf) * upl, nrows = (gend - gf) * RPW;
   const int tb = T * wave / WPG, te = T * (wave + 1) / WPG;
   const typename F::LaneC lc = F::lane(sub);
@@ -113,9 +138,15 @@ __global__ __launch_bounds__(gemv_threads<F>()) void gemv_kernel(typename F::Arg
   };
   // Batch t = (group g, slot k). A batch past the wave's last (the ring runs ahead of the consumer
   // by D - 1) loads row 0's first unit on every lane: one cache line, never consumed.
+  const auto prep = [&] {
+    if constexpr (gemv_has_prepare<F>()) return F::prepare(args, extra, xs);
+    else return 0;
+  }();
   auto load_b = [&](int t, int g, int k, typename F::Raw &r) {
     const bool live = t < te;
-    r = F::load(args, live ? min(g * RPW + rg, N - 1) : 0, live ? unit(k) : 0);
+    const int row = live ? min(g * RPW + rg, N - 1) : 0, u = live ? unit(k) : 0;
+    if constexpr (gemv_has_prepare<F>()) r = F::load(args, prep, row, u);
+    else r = F::load(args, row, u);
   };
   auto advance = [&](int &g, int &k) {
     if (++k == upl) {
@@ -141,7 +172,9 @@ __global__ __launch_bounds__(gemv_threads<F>()) void gemv_kernel(typename F::Arg
   }
 
   int im0 = 0;  // first x image of this workgroup's rows
-  if constexpr (gemv_multi_x<F>()) {
+  if constexpr (requires { F::X_ALL; }) {  // every image staged, image i at slot i
+    F::stage(args, x, xs, xsum, extra, units, pre, 0, nx - 1);
+  } else if constexpr (gemv_multi_x<F>()) {
     im0 = F::xsel(args, min(gf * RPW, N - 1));
     F::stage(args, x, xs, xsum, extra, units, pre, im0, F::xsel(args, min(max(gend * RPW - 1, gf * RPW), N - 1)));
   } else {
@@ -199,7 +232,12 @@ __global__ __launch_bounds__(gemv_threads<F>()) void gemv_kernel(typename F::Arg
     const int w0 = (WPG * (b0 + 1) - 1) / T, w1 = (WPG * (b1 + 1) - 1) / T;  // waves holding b0, b1
     float s = 0.0f;
     for (int w = w0; w <= w1; w++) s += part[w * nrows + i];
-    if (gf * RPW + i < N) y[gf * RPW + i] = f2h(s);
+    if constexpr (gemv_has_store<F>()) part[i] = s;  // only this thread reads row i's partials
+    else if (gf * RPW + i < N) y[gf * RPW + i] = f2h(s);
+  }
+  if constexpr (gemv_has_store<F>()) {
+    __syncthreads();
+    F::store(args, y, gf * RPW, min(nrows, N - gf * RPW), part);
   }
 }
 
@@ -218,20 +256,20 @@ static int launch_gemv_k(const typename F::Args &a, const void *x, void *y, hipS
   const size_t part_off = (xlds + 15) / 16 * 16;
   if (part_off > 160 * 1024) return decline("K too large for the GEMV's LDS copy of x");
   auto kern = gemv_kernel<F, LPR, F::RING, RAGGED>;
-  const int groups = (a.N + RPW - 1) / RPW;
+  const int GA = gemv_align<F>(a, RPW), groups = (a.N + RPW - 1) / RPW, units_g = (groups + GA - 1) / GA;
   const int wg_cap = std::max(F::occ(a) * 4 / WPG, 1);  // workgroups per CU the grid is sized for
   int nwg = 0;
   size_t lds = 0;
   // the rows per workgroup depend on the workgroup count, and the occupancy on the LDS: settle both
   for (int per_cu = wg_cap, it = 0; it < 3; it++) {
-    nwg = std::min(gemv_num_cu() * std::min(per_cu, wg_cap), groups);
-    const size_t rows = (size_t)(groups + nwg - 1) / nwg * RPW;
+    nwg = std::min(gemv_num_cu() * std::min(per_cu, wg_cap), units_g);
+    const size_t rows = (size_t)(units_g + nwg - 1) / nwg * GA * RPW;
     lds = part_off + WPG * rows * 4;
     if (lds > 160 * 1024) {  // very tall outputs: more workgroups, several rounds
-      const size_t room = (160 * 1024 - part_off) / (WPG * 4 * RPW);
+      const size_t room = (160 * 1024 - part_off) / (WPG * 4 * RPW * (size_t)GA);
       if (room < 1) return decline("no LDS left for the GEMV's partial sums");
-      nwg = std::min((int)((groups + room - 1) / room), groups);
-      lds = part_off + WPG * ((size_t)(groups + nwg - 1) / nwg * RPW) * 4;
+      nwg = std::min((int)((units_g + room - 1) / room), units_g);
+      lds = part_off + WPG * ((size_t)(units_g + nwg - 1) / nwg * GA * RPW) * 4;
       break;
     }
     int pc = 0;

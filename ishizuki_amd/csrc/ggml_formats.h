@@ -137,19 +137,55 @@ struct GgmlGemv {
       }
     }
   }
-  // Every slot and sum of one x image, without a pre-issued first round.
-  static DEV void stage_image(const uint16_t *x, u4 *xs, float *xsum, int units) {
-    const int ug = (units + 15) / 16, bd = blockDim.x;
-    for (int i0 = threadIdx.x; i0 < ug * 16 * D::R; i0 += U * bd) {
+  // Every slot and sum of nimg x images (image i at x + i * xstride, staged at xs + i ns and
+  // xsum + i nq): one index space over all images, so each round's slot and sum loads for every
+  // image go out together and the staging costs a memory latency per round, not per image.
+  // Threads tid0 .. tid0 + nthr - 1 take part (all of them by default).
+  static DEV void stage_images(const uint16_t *x, size_t xstride, int nimg, u4 *xs, float *xsum, int units,
+                               int tid0 = 0, int nthr = 0) {
+    const int ug = (units + 15) / 16, bd = nthr ? nthr : (int)blockDim.x, tid = (int)threadIdx.x - tid0;
+    const int ns = ug * 16 * D::R, nq = D::XSUM ? ug * 16 * D::Q : 0;
+    const int rs = (nimg * ns + U * bd - 1) / (U * bd), rq = (nimg * nq + US * bd - 1) / (US * bd);
+    for (int round = 0; round < max(rs, rq); round++) {
       u4 v[U];
-      load_slots(x, units, i0, v);
-      store_slots(xs, units, i0, v);
-    }
-    if constexpr (D::XSUM) {
-      for (int i0 = threadIdx.x; i0 < ug * 16 * D::Q; i0 += US * bd) {
-        u4 v[US][SLMAX];
-        load_sums(x, units, i0, v);
-        store_sums(xsum, units, i0, v);
+      u4 sv[US][SLMAX];
+      const int i0 = round * U * bd + tid, q0 = round * US * bd + tid;
+#pragma unroll
+      for (int j = 0; j < U; j++) {
+        const int i = min(i0 + j * bd, nimg * ns - 1), im = i / ns, ii = i % ns;
+        const int u = min((ii / (16 * D::R)) * 16 + (ii & 15), units - 1), r = (ii >> 4) % D::R;
+        v[j] = *(const u4 *)(x + im * xstride + D::slot_k(u, r));
+      }
+      if constexpr (D::XSUM) {
+        constexpr int SL = D::SUM_LEN / 8;
+#pragma unroll
+        for (int j = 0; j < US; j++) {
+          const int i = min(q0 + j * bd, nimg * nq - 1), im = i / nq, ii = i % nq;
+          const int u = min((ii / (16 * D::Q)) * 16 + (ii & 15), units - 1), q = (ii >> 4) % D::Q;
+          const u4 *p = (const u4 *)(x + im * xstride + D::sum_k(u, q));
+#pragma unroll
+          for (int h = 0; h < SL; h++) sv[j][h] = p[h];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < U; j++) {
+        const int i = i0 + j * bd, ii = i % ns;
+        if (i < nimg * ns && (ii / (16 * D::R)) * 16 + (ii & 15) < units) xs[i] = D::xperm(v[j]);
+      }
+      if constexpr (D::XSUM) {
+        constexpr int SL = D::SUM_LEN / 8;
+#pragma unroll
+        for (int j = 0; j < US; j++) {
+          const int i = q0 + j * bd, ii = i % nq;
+          if (i < nimg * nq && (ii / (16 * D::Q)) * 16 + (ii & 15) < units) {
+            float sm = 0.0f;
+#pragma unroll
+            for (int h = 0; h < SL; h++)
+#pragma unroll
+              for (int e = 0; e < 4; e++) sm = dot2(sv[j][h][e], 0x3C003C00u, sm);  // + both halves
+            xsum[i] = sm;
+          }
+        }
       }
     }
   }

@@ -332,6 +332,8 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(const uint16_t *__restri
 
 __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__restrict__ o, int H,
                                                           int T, int k, MoeRoute R, bool sorted,
+                                                          const uint16_t *__restrict__ shared,
+                                                          const uint16_t *__restrict__ shared_gate,
                                                           uint16_t *__restrict__ y) {
   const size_t total = (size_t)T * H;
   for (size_t q = blockIdx.x * (size_t)blockDim.x + threadIdx.x; q < total;
@@ -341,6 +343,10 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__rest
     for (int s = 0; s < k; s++) {
       const int q2 = sorted ? R.inv[t * k + s] : t * k + s;  // row of o holding pair (t, s)
       acc += h2f(o[(size_t)q2 * H + n]) * R.w[t * k + s];
+    }
+    if (shared) {  // the shared expert, widened and added before the one narrowing
+      const float sg = (float)(_Float16)(1.0f / (1.0f + __expf(-h2f(shared_gate[t]))));
+      acc += (float)(_Float16)(sg * h2f(shared[q]));
     }
     y[q] = f2h(acc);
   }
@@ -421,10 +427,29 @@ struct VMoeDown {
 
 // ------------------------------------------------------------------- gathered GEMV (few tokens)
 // With one or two tokens every routed (token, slot) pair is a GEMV of its own; the streaming
-// GEMV skeleton runs all of them in one launch. Pair p = t k + s (slot order) owns rows
-// p 2I .. p 2I + 2I - 1 (gate rows, then up rows) of the gate/up launch and p H .. p H + H - 1 of
-// the down launch. A row group never straddles two pairs (2I and H are multiples of 256), so the
-// expert id is wave-uniform and read with a scalar load.
+// GEMV skeleton runs all of them in two launches and nothing else runs:
+//  * gate + up + SwiGLU: pair p = t k + s (slot order) owns rows p 2I .. p 2I + 2I - 1, in blocks
+//    of eight: four gate rows, then the same four up rows (row 8b + i of the pair: gate row 4b + i,
+//    row 8b + 4 + i: up row 4b + i), and a workgroup owns whole blocks, so its final store forms
+//    h = silu(gate) * up of each of its rows with the reference's fp16 roundings (Text/MoEBlock.swift
+//    :168-171) and writes h [P][I]. Every workgroup routes the tokens itself before its first
+//    weight load (a 16-lane row per token, ids kept in LDS); workgroup 0 publishes the ids and
+//    weights for the down launch and the caller. A row group never straddles two pairs (2I is a
+//    multiple of 256), so the expert id is wave-uniform.
+//  * down + combine: rows run in blocks of four outputs of one pair, the token's k pairs' blocks
+//    of the same four outputs in turn (row j: token j / (H k), slot (j / 4) % k, output
+//    4 ((j / 4k) % (H / 4)) + j % 4), and a workgroup owns whole runs of k blocks; x is the pairs'
+//    h. Its outputs are combined in the workgroup's final store: y = sum over slots of
+//    w_s fp16(down_s), in fp32 in slot order, plus the shared expert's term, narrowed once
+//    (Text/MoEBlock.swift:143-160).
+typedef __attribute__((address_space(3))) const int32_t lds_i32;
+
+struct MoeTokens {
+  const float *logits;
+  int T, E, normalize;
+  MoeRoute R;  // ids / weights (and the caller's copies) written by workgroup 0
+};
+
 template <class F>
 struct FMoeGateUp : F {
   struct Args {
@@ -432,78 +457,121 @@ struct FMoeGateUp : F {
     size_t rb;
     int K, N;  // K = H, N = P 2I
     int I, k;
-    const int32_t *ids;
+    MoeTokens rt;
+    const uint16_t *x;  // [T][H]
   };
   struct XPre {};
+  struct Prep {
+    lds_i32 *ids;  // [T k] expert of (t, s), in LDS
+  };
   static int occ(const Args &) { return 2; }
-  static size_t extra_lds_bytes(const Args &) { return F::tab_bytes(); }
+  // LDS after the format's tables: a routing row per token, the ids, scratch for the weights
+  static size_t route_words(const Args &a) { return (size_t)a.rt.T * route_row_words(a.rt.E, a.k) + 2 * a.rt.T * a.k; }
+  static size_t extra_lds_bytes(const Args &a) { return F::tab_bytes() + route_words(a) * 4; }
   static __host__ __device__ int nx(const Args &a) { return a.N / (2 * a.I * a.k); }  // tokens
   static DEV int xsel(const Args &a, int row) { return row / (2 * a.I * a.k); }
-  static DEV auto load(const Args &a, int row, int u) {
-    const int p = __builtin_amdgcn_readfirstlane(row) / (2 * a.I);
-    const int e = a.ids[p], j = row - p * 2 * a.I;
-    const uint8_t *w = j < a.I ? a.gate + ((size_t)e * a.I + j) * a.rb : a.up + ((size_t)e * a.I + j - a.I) * a.rb;
-    return F::load_row(w, u);
-  }
-  static DEV XPre stage_load(const Args &, const uint16_t *, int) { return {}; }
-  static DEV void stage(const Args &a, const uint16_t *x, u4 *xs, float *xsum, u4 *extra, int units, const XPre &,
-                        int im0, int im1) {
-    const int ug = (units + 15) / 16;
-    for (int t = im0; t <= im1; t++)
-      F::stage_image(x + (size_t)t * a.K, xs + (t - im0) * ug * 16 * F::R, xsum + (t - im0) * ug * 16 * F::Q, units);
-    F::gemv_tables(extra);
+  static constexpr bool X_ALL = true;  // every token's x is staged (by prepare), image t at t
+  static DEV Prep prepare(const Args &a, u4 *extra, void *lds_x) {
+    uint32_t *rows = (uint32_t *)extra + F::tab_bytes() / 4;
+    const int rw = route_row_words(a.rt.E, a.k);
+    int32_t *ids = (int32_t *)(rows + a.rt.T * rw);
+    if (threadIdx.x >= 64) {  // the other waves stage every token's x meanwhile
+      u4 *xs = (u4 *)lds_x;
+      const int ug = (F::units(a.K) + 15) / 16;
+      F::stage_images(a.x, a.K, a.rt.T, xs, (float *)(xs + a.rt.T * ug * 16 * F::R), F::units(a.K), 64,
+                      blockDim.x - 64);
+    } else if ((int)threadIdx.x < 16 * a.rt.T) {  // wave 0: token t on lanes 16 t .. 16 t + 15
+      const int t = threadIdx.x >> 4;
+      MoeRoute R = a.rt.R;
+      if (blockIdx.x) {  // only workgroup 0 publishes
+        R.ids = ids + a.rt.T * a.k;
+        R.w = (float *)(ids + a.rt.T * a.k);
+        R.ids_out = nullptr;
+        R.w_out = nullptr;
+      }
+      const float *l = a.rt.logits + (size_t)t * a.rt.E;
+#define ISHZ_CALL(NPL) route_token<NPL>(l, a.rt.E, a.k, a.rt.normalize, t, rows + t * rw, R, ids)
+      ISHZ_ROUTE_NPL(a.rt.E, 256, ISHZ_CALL);
+#undef ISHZ_CALL
+    }
     __syncthreads();
+    return {(lds_i32 *)ids};
+  }
+  static __host__ __device__ int group_align(const Args &, int rpw) { return 8 / rpw; }
+  // weight row of row j' (0 .. 2I) of a pair: gate or up, and its index i
+  static DEV bool is_up(int j) { return (j >> 2) & 1; }
+  static DEV int wrow(int j) { return ((j >> 3) << 2) | (j & 3); }
+  static DEV const uint8_t *row_ptr(const Args &a, const Prep &pp, int row) {
+    const int p = __builtin_amdgcn_readfirstlane(row) / (2 * a.I);
+    const int e = pp.ids[p], j = row - p * 2 * a.I;
+    return (is_up(j) ? a.up : a.gate) + ((size_t)e * a.I + wrow(j)) * a.rb;
+  }
+  static DEV auto load(const Args &a, const Prep &pp, int row, int u) { return F::load_row(row_ptr(a, pp, row), u); }
+  static DEV XPre stage_load(const Args &, const uint16_t *, int) { return {}; }
+  static DEV void stage(const Args &, const uint16_t *, u4 *, float *, u4 *extra, int, const XPre &, int, int) {
+    F::gemv_tables(extra);  // x was staged by prepare
+    __syncthreads();
+  }
+  // rows row0 .. row0 + nrows: whole eight-row blocks; h [P][I] fp16
+  static DEV void store(const Args &a, uint16_t *h, int row0, int nrows, const float *vals) {
+    for (int q = threadIdx.x; q < nrows / 2; q += blockDim.x) {
+      const int blk = q >> 2, i4 = q & 3, j = row0 + 8 * blk;
+      const int p = j / (2 * a.I), i = wrow(j - p * 2 * a.I) + i4;
+      const float g16 = h2f(f2h(vals[8 * blk + i4])), u16 = h2f(f2h(vals[8 * blk + 4 + i4]));
+      const float sg = r16(1.0f / (1.0f + __expf(-g16)));
+      h[(size_t)p * a.I + i] = f2h(r16(g16 * sg) * u16);
+    }
   }
 };
 
-// down: x of pair p is h = silu(gate) * up of its gate/up rows (fp16 ops, as the reference's
-// elementwise SwiGLU on fp16 activations), formed while staging.
 template <class F>
 struct FMoeDown : F {
   struct Args {
     const uint8_t *down;
     size_t rb;
     int K, N;  // K = I, N = P H
-    int H;
-    const int32_t *ids;
+    int H, k;
+    const int32_t *ids;  // [T k], from the gate/up launch
+    const float *w;      // [T k] routing weights
+    const uint16_t *shared, *shared_gate;  // optional: shared expert output [T][H] and gate logit [T]
   };
   struct XPre {};
   static int occ(const Args &) { return 2; }
-  static size_t extra_lds_bytes(const Args &a) { return F::tab_bytes() + (size_t)nx(a) * a.K * 2; }
+  static size_t extra_lds_bytes(const Args &) { return F::tab_bytes(); }
   static __host__ __device__ int nx(const Args &a) { return a.N / a.H; }  // pairs
-  static DEV int xsel(const Args &a, int row) { return row / a.H; }
-  static DEV auto load(const Args &a, int row, int u) {
-    const int p = __builtin_amdgcn_readfirstlane(row) / a.H;
-    const int e = a.ids[p];
-    return F::load_row(a.down + ((size_t)e * a.H + (row - p * a.H)) * a.rb, u);
+  static __host__ __device__ int group_align(const Args &a, int rpw) { return 4 * a.k / rpw; }
+  static DEV int pair_of(const Args &a, int row) { return (row / (a.H * a.k)) * a.k + (row >> 2) % a.k; }
+  static DEV int out_of(const Args &a, int row) { return ((row >> 2) / a.k % (a.H / 4)) * 4 + (row & 3); }
+  static DEV int xsel(const Args &a, int row) { return pair_of(a, row); }
+  static DEV const uint8_t *row_ptr(const Args &a, int row) {
+    const int r0 = __builtin_amdgcn_readfirstlane(row) & ~3;  // the group's four-row block
+    const int e = a.ids[pair_of(a, r0)];
+    return a.down + ((size_t)e * a.H + out_of(a, r0) + (row & 3)) * a.rb;
   }
+  static DEV auto load(const Args &a, int row, int u) { return F::load_row(row_ptr(a, row), u); }
   static DEV XPre stage_load(const Args &, const uint16_t *, int) { return {}; }
-  // x = the gate/up outputs [P][2I]; h goes to LDS after the format's tables, then is staged.
-  static DEV void stage(const Args &a, const uint16_t *gu, u4 *xs, float *xsum, u4 *extra, int units, const XPre &,
+  // x = the pairs' h [P][I] (the gate/up launch's output)
+  static DEV void stage(const Args &a, const uint16_t *h, u4 *xs, float *xsum, u4 *extra, int units, const XPre &,
                         int im0, int im1) {
-    const int I = a.K, P = im1 - im0 + 1, ug = (units + 15) / 16;
+    F::stage_images(h + (size_t)im0 * a.K, a.K, im1 - im0 + 1, xs, xsum, units);
     F::gemv_tables(extra);
-    uint16_t *hb = (uint16_t *)(extra + F::tab_bytes() / 16);
-    for (int c = threadIdx.x; c < P * I / 8; c += blockDim.x) {
-      const int p = im0 + c / (I / 8), i = (c % (I / 8)) * 8;
-      const u4 g8 = *(const u4 *)(gu + (size_t)p * 2 * I + i), u8 = *(const u4 *)(gu + (size_t)p * 2 * I + I + i);
-      u4 h8;
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        uint32_t w = 0;
-#pragma unroll
-        for (int hh = 0; hh < 2; hh++) {
-          const float g16 = h2f(g8[q] >> (16 * hh)), u16 = h2f(u8[q] >> (16 * hh));
-          const float sg = r16(1.0f / (1.0f + __expf(-g16)));
-          w |= (uint32_t)f2h(r16(g16 * sg) * u16) << (16 * hh);
-        }
-        h8[q] = w;
+    __syncthreads();
+  }
+  // rows row0 .. row0 + nrows (whole runs of k four-row blocks): one output per four-row block
+  // position, its k slots' fp16 rows weighted in fp32 in slot order, then the shared term.
+  static DEV void store(const Args &a, uint16_t *y, int row0, int nrows, const float *vals) {
+    const int run = 4 * a.k;
+    for (int q = threadIdx.x; q < nrows / a.k; q += blockDim.x) {
+      const int blk = q >> 2, rr = q & 3, j0 = row0 + blk * run;
+      const int t = j0 / (a.H * a.k), r = out_of(a, j0) + rr;
+      float acc = 0.0f;
+      for (int s = 0; s < a.k; s++) acc += h2f(f2h(vals[blk * run + 4 * s + rr])) * a.w[t * a.k + s];
+      if (a.shared) {
+        const float sg = r16(1.0f / (1.0f + __expf(-h2f(a.shared_gate[t]))));
+        acc += r16(sg * h2f(a.shared[(size_t)t * a.H + r]));
       }
-      *(u4 *)(hb + (size_t)(p - im0) * I + i) = h8;
+      y[(size_t)t * a.H + r] = f2h(acc);
     }
-    __syncthreads();
-    for (int p = 0; p < P; p++) F::stage_image(hb + (size_t)p * I, xs + p * ug * 16 * F::R, xsum + p * ug * 16 * F::Q, units);
-    __syncthreads();
   }
 };
 
@@ -576,24 +644,22 @@ static bool gathered_gemv(int T, int H, int I, int k) {
 
 template <class F>
 static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void *gate,
-                   const void *up, const void *down, MoeRoute R, uint16_t *h, uint16_t *gu, uint16_t *o,
-                   void *y, hipStream_t st) {
+                   const void *up, const void *down, const MoeTokens &rt, uint16_t *h, uint16_t *gu, uint16_t *o,
+                   const uint16_t *shared, const uint16_t *shared_gate, void *y, hipStream_t st) {
+  const MoeRoute &R = rt.R;
   const int amax = std::min(E, T * k);
   const size_t total = (size_t)T * H;
   // one or two tokens: every (token, slot) pair is a GEMV; two launches of the streaming GEMV
+  // (routing in the first, the combine in the second)
   if (gathered_gemv(T, H, I, k)) {
     const int P = T * k;
     const typename FMoeGateUp<F>::Args ga{(const uint8_t *)gate, (const uint8_t *)up, (size_t)(H / F::BS) * F::TS,
-                                          H, P * 2 * I, I, k, R.ids};
+                                          H, P * 2 * I, I, k, rt, (const uint16_t *)x};
     int rc = launch_gemv<FMoeGateUp<F>>(ga, x, gu, st);
     if (rc) return rc;
-    const typename FMoeDown<F>::Args da{(const uint8_t *)down, (size_t)(I / F::BS) * F::TS, I, P * H, H, R.ids};
-    rc = launch_gemv<FMoeDown<F>>(da, gu, o, st);
-    if (rc) return rc;
-    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)std::min<size_t>((total + 255) / 256, 4096)), dim3(256), 0,
-                       st, o, H, T, k, R, false, (uint16_t *)y);
-    ISHZ_LAUNCH_CHECK("moe combine launch");
-    return ISHZ_OK;
+    const typename FMoeDown<F>::Args da{(const uint8_t *)down, (size_t)(I / F::BS) * F::TS, I, P * H, H, k,
+                                        R.ids, R.w, shared, shared_gate};
+    return launch_gemv<FMoeDown<F>>(da, gu, y, st);
   }
   // streaming MFMA kernels from 3 tokens up; one or two tokens (a GEMV per expert) run faster on
   // the per-block kernels below, which start streaming without staging x
@@ -625,7 +691,7 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
     ISHZ_LAUNCH_CHECK("moe down launch");
   }
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)std::min<size_t>((total + 255) / 256, 4096)), dim3(256), 0,
-                     st, o, H, T, k, R, true, (uint16_t *)y);
+                     st, o, H, T, k, R, true, shared, shared_gate, (uint16_t *)y);
   ISHZ_LAUNCH_CHECK("moe combine launch");
   return ISHZ_OK;
 }
@@ -677,10 +743,12 @@ struct FMoeGateUpA : FMoeGateUp<F> {
   struct Args : FMoeGateUp<F>::Args {
     AffPack g, u;
   };
-  static DEV auto load(const Args &a, int row, int u) {
+  using Prep = typename FMoeGateUp<F>::Prep;
+  static DEV auto load(const Args &a, const Prep &pp, int row, int u) {
+    using B = FMoeGateUp<F>;
     const int p = __builtin_amdgcn_readfirstlane(row) / (2 * a.I);
-    const int e = a.ids[p], j = row - p * 2 * a.I;
-    return F::load_unit(j < a.I ? a.g.row((size_t)e * a.I + j) : a.u.row((size_t)e * a.I + j - a.I), u);
+    const int e = pp.ids[p], j = row - p * 2 * a.I;
+    return F::load_unit((B::is_up(j) ? a.u : a.g).row((size_t)e * a.I + B::wrow(j)), u);
   }
 };
 template <class F>
@@ -689,35 +757,33 @@ struct FMoeDownA : FMoeDown<F> {
     AffPack d;
   };
   static DEV auto load(const Args &a, int row, int u) {
-    const int p = __builtin_amdgcn_readfirstlane(row) / a.H;
-    return F::load_unit(a.d.row((size_t)a.ids[p] * a.H + (row - p * a.H)), u);
+    const int r0 = __builtin_amdgcn_readfirstlane(row) & ~3;
+    const int e = a.ids[FMoeDown<F>::pair_of(a, r0)];
+    return F::load_unit(a.d.row((size_t)e * a.H + FMoeDown<F>::out_of(a, r0) + (row & 3)), u);
   }
 };
 
 template <class F>
 static int moe_ffn_affine(const void *x, int T, int H, int E, int I, int k, const AffPack &gate, const AffPack &up,
-                          const AffPack &down, MoeRoute R, uint16_t *h, uint16_t *gu, uint16_t *o, void *y,
-                          hipStream_t st) {
+                          const AffPack &down, const MoeTokens &rt, uint16_t *h, uint16_t *gu, uint16_t *o,
+                          const uint16_t *shared, const uint16_t *shared_gate, void *y, hipStream_t st) {
+  const MoeRoute &R = rt.R;
   const int amax = std::min(E, T * k);
   const size_t total = (size_t)T * H;
   if (gathered_gemv(T, H, I, k)) {  // as moe_ffn: every (token, slot) pair a GEMV, two launches
     const int P = T * k;
     typename FMoeGateUpA<F>::Args ga{};
-    static_cast<typename FMoeGateUp<F>::Args &>(ga) =
-        typename FMoeGateUp<F>::Args{nullptr, nullptr, 0, H, P * 2 * I, I, k, R.ids};
+    static_cast<typename FMoeGateUp<F>::Args &>(ga) = typename FMoeGateUp<F>::Args{nullptr, nullptr, 0, H, P * 2 * I, I, k, rt,
+                                                                                    (const uint16_t *)x};
     ga.g = gate;
     ga.u = up;
     int rc = launch_gemv<FMoeGateUpA<F>>(ga, x, gu, st);
     if (rc) return rc;
     typename FMoeDownA<F>::Args da{};
-    static_cast<typename FMoeDown<F>::Args &>(da) = typename FMoeDown<F>::Args{nullptr, 0, I, P * H, H, R.ids};
+    static_cast<typename FMoeDown<F>::Args &>(da) =
+        typename FMoeDown<F>::Args{nullptr, 0, I, P * H, H, k, R.ids, R.w, shared, shared_gate};
     da.d = down;
-    rc = launch_gemv<FMoeDownA<F>>(da, gu, o, st);
-    if (rc) return rc;
-    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)std::min<size_t>((total + 255) / 256, 4096)), dim3(256), 0,
-                       st, o, H, T, k, R, false, (uint16_t *)y);
-    ISHZ_LAUNCH_CHECK("moe combine launch");
-    return ISHZ_OK;
+    return launch_gemv<FMoeDownA<F>>(da, gu, y, st);
   }
   const int tiles_gu = 2 * ((I + 15) / 16), tiles_dn = (H + 15) / 16;
   const int act = std::min(amax, 128);
@@ -738,7 +804,7 @@ static int moe_ffn_affine(const void *x, int T, int H, int E, int I, int k, cons
   rc = moe_vgemm<F>(dn, T, E, k, I, H, amax, pick(tiles_dn, 0), st);
   if (rc) return rc;
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)std::min<size_t>((total + 255) / 256, 4096)), dim3(256), 0,
-                     st, o, H, T, k, R, true, (uint16_t *)y);
+                     st, o, H, T, k, R, true, shared, shared_gate, (uint16_t *)y);
   ISHZ_LAUNCH_CHECK("moe combine launch");
   return ISHZ_OK;
 }
@@ -763,9 +829,9 @@ extern "C" int ishz_moe_route(const float *logits, int T, int E, int topk, int n
 extern "C" int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T, int H,
                                const float *logits, int E, int topk, int normalize,
                                const void *gate, const void *up, const void *down,
-                               size_t expert_bytes, int I, void *y, int32_t *ids_out,
-                               float *weights_out, void *workspace, size_t workspace_bytes,
-                               ishz_stream_t stream) {
+                               size_t expert_bytes, int I, const void *shared, const void *shared_gate,
+                               void *y, int32_t *ids_out, float *weights_out, void *workspace,
+                               size_t workspace_bytes, ishz_stream_t stream) {
   const int bs = ishz_ggml_block_size(type);
   if (type != ISHZ_GGML_Q4_K && type != ISHZ_GGML_Q6_K && type != ISHZ_GGML_Q4_0)
     return decline("MoE experts must be Q4_0, Q4_K or Q6_K");
@@ -778,20 +844,25 @@ extern "C" int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T,
   if (expert_bytes < need || (size_t)H * (I / bs) * ishz_ggml_type_size(type) > expert_bytes)
     return decline("expert buffers too short");
   if (!x || !logits || !gate || !up || !down || !y) return einval("null pointer");
+  if (!shared != !shared_gate) return einval("the shared expert needs both its output and its gate");
   const MoeLayout L = moe_layout(T, H, E, I, topk);
   if (!workspace || workspace_bytes < L.total) return einval("workspace too small (ishz_moe_workspace_size)");
   MoeRoute R = moe_route_ptrs(workspace, L);
   R.ids_out = ids_out;
   R.w_out = weights_out;
   hipStream_t st = S(stream);
-  const int rc = moe_route_all(logits, T, E, topk, normalize, R, !gathered_gemv(T, H, I, topk), st);
-  if (rc) return rc;
+  const MoeTokens rt{logits, T, E, normalize, R};
+  if (!gathered_gemv(T, H, I, topk)) {  // (the gathered GEMVs route inside their first launch)
+    const int rc = moe_route_all(logits, T, E, topk, normalize, R, true, st);
+    if (rc) return rc;
+  }
   uint16_t *h = (uint16_t *)((uint8_t *)workspace + L.h), *o = (uint16_t *)((uint8_t *)workspace + L.o);
   uint16_t *gu = (uint16_t *)((uint8_t *)workspace + L.gu);
+  const uint16_t *sh = (const uint16_t *)shared, *sg = (const uint16_t *)shared_gate;
   switch (type) {
-  case ISHZ_GGML_Q4_K: return moe_ffn<FQ4_K>(x, T, H, E, I, topk, gate, up, down, R, h, gu, o, y, st);
-  case ISHZ_GGML_Q6_K: return moe_ffn<FQ6_K>(x, T, H, E, I, topk, gate, up, down, R, h, gu, o, y, st);
-  default: return moe_ffn<FQ4_0>(x, T, H, E, I, topk, gate, up, down, R, h, gu, o, y, st);
+  case ISHZ_GGML_Q4_K: return moe_ffn<FQ4_K>(x, T, H, E, I, topk, gate, up, down, rt, h, gu, o, sh, sg, y, st);
+  case ISHZ_GGML_Q6_K: return moe_ffn<FQ6_K>(x, T, H, E, I, topk, gate, up, down, rt, h, gu, o, sh, sg, y, st);
+  default: return moe_ffn<FQ4_0>(x, T, H, E, I, topk, gate, up, down, rt, h, gu, o, sh, sg, y, st);
   }
 }
 
@@ -801,8 +872,9 @@ extern "C" int ishz_moe_swiglu_affine(const void *x, int x_dtype, int T, int H, 
                                       const uint32_t *up_codes, const void *up_scales, const void *up_biases,
                                       const uint32_t *down_codes, const void *down_scales,
                                       const void *down_biases, int scale_dtype, int bits, int group, int I,
-                                      void *y, int32_t *ids_out, float *weights_out, void *workspace,
-                                      size_t workspace_bytes, ishz_stream_t stream) {
+                                      const void *shared, const void *shared_gate, void *y, int32_t *ids_out,
+                                      float *weights_out, void *workspace, size_t workspace_bytes,
+                                      ishz_stream_t stream) {
   if (bits != 4 && bits != 8) return decline("affine experts of 4 or 8 bits are decoded in-kernel");
   if (group != 64 && group != 128) return decline("group size must be 64 or 128");
   if (scale_dtype != ISHZ_DT_F16 && scale_dtype != ISHZ_DT_BF16) return decline("scales must be fp16 or bf16");
@@ -814,14 +886,19 @@ extern "C" int ishz_moe_swiglu_affine(const void *x, int x_dtype, int T, int H, 
   if (!x || !logits || !gate_codes || !gate_scales || !gate_biases || !up_codes || !up_scales || !up_biases ||
       !down_codes || !down_scales || !down_biases || !y)
     return einval("null pointer");
+  if (!shared != !shared_gate) return einval("the shared expert needs both its output and its gate");
   const MoeLayout L = moe_layout(T, H, E, I, topk);
   if (!workspace || workspace_bytes < L.total) return einval("workspace too small (ishz_moe_workspace_size)");
   MoeRoute R = moe_route_ptrs(workspace, L);
   R.ids_out = ids_out;
   R.w_out = weights_out;
   hipStream_t st = S(stream);
-  int rc = moe_route_all(logits, T, E, topk, normalize, R, !gathered_gemv(T, H, I, topk), st);
-  if (rc) return rc;
+  const MoeTokens rt{logits, T, E, normalize, R};
+  if (!gathered_gemv(T, H, I, topk)) {
+    const int rc = moe_route_all(logits, T, E, topk, normalize, R, true, st);
+    if (rc) return rc;
+  }
+  const uint16_t *sh = (const uint16_t *)shared, *sg = (const uint16_t *)shared_gate;
   uint16_t *h = (uint16_t *)((uint8_t *)workspace + L.h), *o = (uint16_t *)((uint8_t *)workspace + L.o);
   uint16_t *gu = (uint16_t *)((uint8_t *)workspace + L.gu);
   const AffPack gp{gate_codes, (const uint16_t *)gate_scales, (const uint16_t *)gate_biases, H * bits / 32, H / group};
@@ -829,8 +906,8 @@ extern "C" int ishz_moe_swiglu_affine(const void *x, int x_dtype, int T, int H, 
   const AffPack dp{down_codes, (const uint16_t *)down_scales, (const uint16_t *)down_biases, I * bits / 32, I / group};
   const bool bf = scale_dtype == ISHZ_DT_BF16;
 #define ISHZ_MA(B, G)                                                                                        \
-  return bf ? moe_ffn_affine<FAffineN<B, G, true>>(x, T, H, E, I, topk, gp, upk, dp, R, h, gu, o, y, st)   \
-            : moe_ffn_affine<FAffineN<B, G, false>>(x, T, H, E, I, topk, gp, upk, dp, R, h, gu, o, y, st)
+  return bf ? moe_ffn_affine<FAffineN<B, G, true>>(x, T, H, E, I, topk, gp, upk, dp, rt, h, gu, o, sh, sg, y, st) \
+            : moe_ffn_affine<FAffineN<B, G, false>>(x, T, H, E, I, topk, gp, upk, dp, rt, h, gu, o, sh, sg, y, st)
   if (bits == 4) {
     if (group == 64) ISHZ_MA(4, 64);
     ISHZ_MA(4, 128);

@@ -33,8 +33,21 @@ class GGMLExperts:
         self.expert_bytes = intermediate * ggml.row_bytes(type_, hidden)
 
 
-def swiglu(x, logits, experts, top_k=8, normalize=True, return_routing=False):
-    """y [T, H] = sum_k w_k * down_k(silu(gate_k(x)) * up_k(x)); None if declined."""
+def _shared_ptrs(x, shared, shared_gate):
+    """The shared expert's output [T, H] and gate logit [T] (x's dtype), or (None, None)."""
+    if (shared is None) != (shared_gate is None):
+        raise ValueError("the shared expert needs both its output and its gate")
+    if shared is None:
+        return None, None, ()
+    T, H = x.shape
+    shared = shared.to(x.dtype).contiguous().view(T, H)
+    shared_gate = shared_gate.to(x.dtype).contiguous().view(T)
+    return ptr(shared), ptr(shared_gate), (shared, shared_gate)
+
+
+def swiglu(x, logits, experts, top_k=8, normalize=True, return_routing=False, shared=None, shared_gate=None):
+    """y [T, H] = sum_k w_k * down_k(silu(gate_k(x)) * up_k(x)) (+ sigmoid(shared_gate) * shared,
+    the shared expert, when given); None if declined."""
     require_cuda(x, logits)
     x = x.contiguous()
     logits = logits.float().contiguous()
@@ -45,9 +58,10 @@ def swiglu(x, logits, experts, top_k=8, normalize=True, return_routing=False):
     y = torch.empty((T, H), dtype=x.dtype, device=x.device)
     ids = torch.empty((T, top_k), dtype=torch.int32, device=x.device)
     w = torch.empty((T, top_k), dtype=torch.float32, device=x.device)
+    sp, sgp, _keep = _shared_ptrs(x, shared, shared_gate)
     rc = L.ishz_moe_swiglu(ex.type, ptr(x), DTYPES.get(x.dtype, -1), T, H, ptr(logits), ex.E, top_k,
                            int(normalize), ptr(ex.gate), ptr(ex.up), ptr(ex.down), ex.expert_bytes, ex.I,
-                           ptr(y), ptr(ids), ptr(w), ptr(ws), ws.numel(), stream())
+                           sp, sgp, ptr(y), ptr(ids), ptr(w), ptr(ws), ws.numel(), stream())
     if not _lib.check(rc, "moe_swiglu"):
         return None
     return (y, ids, w) if return_routing else y
@@ -65,8 +79,9 @@ class AffineExperts:
         self.bits, self.group, self.E, self.H, self.I = bits, group, experts, hidden, intermediate
 
 
-def swiglu_affine(x, logits, experts, top_k=8, normalize=True, return_routing=False):
-    """The MoE FFN over affine stacked experts; None if declined."""
+def swiglu_affine(x, logits, experts, top_k=8, normalize=True, return_routing=False, shared=None,
+                  shared_gate=None):
+    """The MoE FFN over affine stacked experts (shared expert as in swiglu); None if declined."""
     require_cuda(x, logits)
     x = x.contiguous()
     logits = logits.float().contiguous()
@@ -78,10 +93,11 @@ def swiglu_affine(x, logits, experts, top_k=8, normalize=True, return_routing=Fa
     ids = torch.empty((T, top_k), dtype=torch.int32, device=x.device)
     w = torch.empty((T, top_k), dtype=torch.float32, device=x.device)
     (gc, gs, gb), (uc, us, ub), (dc, ds, db) = ex.gate, ex.up, ex.down
+    sp, sgp, _keep = _shared_ptrs(x, shared, shared_gate)
     rc = L.ishz_moe_swiglu_affine(ptr(x), DTYPES.get(x.dtype, -1), T, H, ptr(logits), ex.E, top_k, int(normalize),
                                   ptr(gc), ptr(gs), ptr(gb), ptr(uc), ptr(us), ptr(ub), ptr(dc), ptr(ds), ptr(db),
-                                  DTYPES.get(gs.dtype, -1), ex.bits, ex.group, ex.I, ptr(y), ptr(ids), ptr(w),
-                                  ptr(ws), ws.numel(), stream())
+                                  DTYPES.get(gs.dtype, -1), ex.bits, ex.group, ex.I, sp, sgp, ptr(y), ptr(ids),
+                                  ptr(w), ptr(ws), ws.numel(), stream())
     if not _lib.check(rc, "moe_swiglu_affine"):
         return None
     return (y, ids, w) if return_routing else y

@@ -48,7 +48,7 @@ def lib():
             "ishzo_exl3_decode": (F, [U, I]),
             "ishzo_exl3_apply": (I, [P, I, I, P, P, P, I, I, I, P, I]),
             "ishzo_moe_route": (None, [P, I, I, I, I, P, P]),
-            "ishzo_moe_swiglu": (I, [U, P, I, I, P, P, I, P, P, P, I, I, P, I]),
+            "ishzo_moe_swiglu": (I, [U, P, I, I, P, P, I, P, P, P, I, I, P, P, P, I]),
             "ishzo_bench_affine_linear": (ctypes.c_double, [P, I, P, I, P, P, P, I, I, I, I, I, P]),
         }
         for name, (res, args) in sig.items():
@@ -171,15 +171,18 @@ def moe_route(logits, topk, normalize=True):
     return ids, w
 
 
-def moe_swiglu(type_, x, ids, weights, gate, up, down, E, I, threads=0):
+def moe_swiglu(type_, x, ids, weights, gate, up, down, E, I, threads=0, shared=None, shared_gate=None):
+    """shared [T][H] / shared_gate [T]: the shared expert's output and gate logit (fp16 values)."""
     x = _c(np.atleast_2d(x), np.float32)
     T, H = x.shape
     ids = _c(ids, np.int32)
     topk = ids.shape[1]
     y = np.empty((T, H), np.float32)
+    sh = None if shared is None else _c(np.reshape(shared, (T, H)), np.float32)
+    sg = None if shared_gate is None else _c(np.reshape(shared_gate, (T,)), np.float32)
     rc = lib().ishzo_moe_swiglu(type_, _p(x), T, H, _p(ids), _p(_c(weights, np.float32)), topk,
                                 _p(_c(gate, np.uint8)), _p(_c(up, np.uint8)), _p(_c(down, np.uint8)),
-                                E, I, _p(y), threads)
+                                E, I, None if sh is None else _p(sh), None if sg is None else _p(sg), _p(y), threads)
     if rc:
         raise ValueError(f"moe oracle failed {rc}")
     return y

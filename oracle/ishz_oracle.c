@@ -744,7 +744,8 @@ void ishzo_moe_route(const float *logits, int T, int E, int topk, int normalize,
    up are fp16 elementwise ops, the weighted sum over slots is fp32 and narrows once. */
 int ishzo_moe_swiglu(uint32_t type, const float *x, int T, int H, const int32_t *ids,
                      const float *weights, int topk, const uint8_t *gate, const uint8_t *up,
-                     const uint8_t *down, int E, int I, float *y, int threads) {
+                     const uint8_t *down, int E, int I, const float *shared, const float *shared_gate,
+                     float *y, int threads) {
   int bs = ishzo_block_size(type), ts = ishzo_type_size(type);
   if (!bs || H % bs || I % bs) return -1;
   size_t gate_bytes = (size_t)I * (H / bs) * ts, down_bytes = (size_t)H * (I / bs) * ts;
@@ -782,6 +783,10 @@ int ishzo_moe_swiglu(uint32_t type, const float *x, int T, int H, const int32_t 
     for (int j = 0; j < H; j++) {
       float acc = 0.0f;
       for (int s = 0; s < topk; s++) acc += o[((size_t)t * topk + s) * H + j] * weights[(size_t)t * topk + s];
+      /* shared expert (Text/MoEBlock.swift:158-160): sigmoid(sharedGate(x)) in x.dtype, times
+         shared(x) in x.dtype, widened and added in fp32 before the one narrowing */
+      if (shared && shared_gate)
+        acc += round16(round16(1.0f / (1.0f + expf(-shared_gate[t]))) * shared[(size_t)t * H + j]);
       y[(size_t)t * H + j] = round16(acc);
     }
   free(h);

@@ -88,10 +88,13 @@ void ishzo_moe_route(const float *logits, int T, int E, int topk, int normalize,
 
 /* Expert SwiGLU over Q4_K (or any GGML type) experts, fp16 activations. gate/up blocks are
    [E][I][H], down [E][H][I]. Emulates the reference's fp16 intermediates
-   (ResidentExperts.swiglu, Text/MoEBlock.swift:168-171; weighting :147-149). y [T][H]. */
+   (ResidentExperts.swiglu, Text/MoEBlock.swift:168-171; weighting :147-149). With shared
+   ([T][H]) and shared_gate ([T]), both fp16 values as floats, the shared expert's
+   sigmoid(gate) * shared term is added in fp32 before the cast (:158-160). y [T][H]. */
 int ishzo_moe_swiglu(uint32_t type, const float *x, int T, int H, const int32_t *ids,
                      const float *weights, int topk, const uint8_t *gate, const uint8_t *up,
-                     const uint8_t *down, int E, int I, float *y, int threads);
+                     const uint8_t *down, int E, int I, const float *shared, const float *shared_gate,
+                     float *y, int threads);
 
 #ifdef __cplusplus
 }

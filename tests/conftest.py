@@ -96,7 +96,7 @@ def golden_exl3():
 MOE_ELEM = 2.0 ** -9
 
 
-def moe_reference(type_, x, ids, weights, gate, up, down, E, I):
+def moe_reference(type_, x, ids, weights, gate, up, down, E, I, shared=None, shared_gate=None):
     """(ref, bound) for the expert-gathered SwiGLU FFN: ref is the oracle's loop-per-token
     restatement; bound_t = sum_s w_s |W_down[e_s]| @ |h_s|, the magnitudes forming each output.
     Check with elem=MOE_ELEM: an fp16 intermediate (a projection output, silu, h) computed in
@@ -105,7 +105,7 @@ def moe_reference(type_, x, ids, weights, gate, up, down, E, I):
     import oracle
     x = np.asarray(x, np.float32)
     T, H = x.shape
-    ref = oracle.moe_swiglu(type_, x, ids, weights, gate, up, down, E, I)
+    ref = oracle.moe_swiglu(type_, x, ids, weights, gate, up, down, E, I, shared=shared, shared_gate=shared_gate)
     bs, ts = oracle.block_size(type_), oracle.type_size(type_)
     gb = I * (H // bs) * ts
     db = H * (I // bs) * ts
@@ -126,4 +126,6 @@ def moe_reference(type_, x, ids, weights, gate, up, down, E, I):
             gv = g @ x[t]
             h = gv / (1.0 + np.exp(-gv.astype(np.float64))) * (u @ x[t])
             bound[t] += float(weights[t, s]) * (ad @ np.abs(h))
+    if shared is not None:
+        bound += np.abs(np.asarray(shared, np.float64))
     return ref, bound

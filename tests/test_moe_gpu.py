@@ -126,7 +126,7 @@ def affine_experts(E, H, I, bits, group, seed, scale):
     return packs, moe.AffineExperts(tens[0], tens[1], tens[2], bits, group, E, H, I)
 
 
-def affine_moe_reference(x, rid, rw, packs, E, H, I, bits, group):
+def affine_moe_reference(x, rid, rw, packs, E, H, I, bits, group, shared=None, shared_gate=None):
     """The oracle's MoE formula (ishzo_moe_swiglu: fp16 projection outputs, fp16 SwiGLU ops, fp32
     weighted sum in slot order, narrowed once) over affine weights from the oracle's dequantizer."""
     r16 = lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
@@ -145,8 +145,32 @@ def affine_moe_reference(x, rid, rw, packs, E, H, I, bits, group):
             h = r16(r16(g * sg) * u)
             o = r16(Wd[e] @ h)
             acc = (acc + o * np.float32(rw[t, s])).astype(np.float32)
+        if shared is not None:
+            acc = (acc + r16(r16(1.0 / (1.0 + np.exp(-np.float32(shared_gate[t])))) * shared[t])).astype(np.float32)
         y[t] = r16(acc)
     return y
+
+
+@pytest.mark.parametrize("T,type_", [(1, ggml.Q4_K), (2, ggml.Q6_K), (8, ggml.Q4_K), (3, ggml.Q4_0)])
+def test_swiglu_shared_expert(T, type_):
+    """The shared expert's sigmoid(gate) * output, added in fp32 before the one narrowing
+    (Text/MoEBlock.swift:158-160): in the two-launch gathered path (T <= 2, combined in the down
+    projection's store) and in the streaming path's combine kernel."""
+    E, H, I, k = 16, 512, 256, 4
+    (g, u, d), ex = experts(E, H, I, type_, seed=T + 40)
+    x = synth.fp16_normal((T, H), seed=T + 41)
+    logits = np.random.default_rng(T + 42).standard_normal((T, E)).astype(np.float32)
+    sh = (synth.fp16_normal((T, H), seed=T + 43).astype(np.float32) * 0.05).astype(np.float16)
+    sg = synth.fp16_normal((T,), seed=T + 44)
+    y = moe.swiglu(torch.from_numpy(x).to(DEV), torch.from_numpy(logits).to(DEV), ex, top_k=k,
+                   shared=torch.from_numpy(sh).to(DEV), shared_gate=torch.from_numpy(sg).to(DEV))
+    rid, rw = oracle.moe_route(logits, k)
+    ref, bd = moe_reference(type_, x.astype(np.float32), rid, rw, g, u, d, E, I, shared=sh.astype(np.float32),
+                            shared_gate=sg.astype(np.float32))
+    assert_close(y.float().cpu().numpy(), ref, bound=bd, elem=MOE_ELEM, what=f"moe shared T={T}")
+    with pytest.raises(ValueError):
+        moe.swiglu(torch.from_numpy(x).to(DEV), torch.from_numpy(logits).to(DEV), ex, top_k=k,
+                   shared=torch.from_numpy(sh).to(DEV))
 
 
 @pytest.mark.parametrize("bits,group,T", [(4, 64, 1), (8, 128, 2), (4, 128, 5), (8, 64, 3), (4, 64, 20)])
@@ -164,3 +188,19 @@ def test_swiglu_affine_experts(bits, group, T):
     ref = affine_moe_reference(x.astype(np.float32), rid, rw, packs, E, H, I, bits, group)
     assert np.isfinite(ref).all()
     assert_close(y.float().cpu().numpy(), ref, what=f"moe affine bits={bits} g={group} T={T}")
+
+
+@pytest.mark.parametrize("T", [1, 5])
+def test_swiglu_affine_shared_expert(T):
+    E, H, I, k, bits, group = 16, 512, 256, 4, 4, 64
+    packs, ex = affine_experts(E, H, I, bits, group, seed=90 + T, scale=0.01)
+    x = synth.fp16_normal((T, H), seed=T + 91)
+    logits = np.random.default_rng(T + 92).standard_normal((T, E)).astype(np.float32)
+    sh = (synth.fp16_normal((T, H), seed=T + 93).astype(np.float32) * 0.05).astype(np.float16)
+    sg = synth.fp16_normal((T,), seed=T + 94)
+    y = moe.swiglu_affine(torch.from_numpy(x).to(DEV), torch.from_numpy(logits).to(DEV), ex, top_k=k,
+                          shared=torch.from_numpy(sh).to(DEV), shared_gate=torch.from_numpy(sg).to(DEV))
+    rid, rw = oracle.moe_route(logits, k)
+    ref = affine_moe_reference(x.astype(np.float32), rid, rw, packs, E, H, I, bits, group,
+                               shared=sh.astype(np.float32), shared_gate=sg.astype(np.float32))
+    assert_close(y.float().cpu().numpy(), ref, what=f"moe affine shared T={T}")

@@ -206,7 +206,7 @@ def test_affine_matmul_pinned(bits, group):
     assert np.array_equal(w32, W.astype(np.float32))
 
 
-def _moe_loop_reference(x, logits, gate, up, down, t_, E, H, I, k):
+def _moe_loop_reference(x, logits, gate, up, down, t_, E, H, I, k, shared=None, shared_gate=None):
     """MoEBlockTests.reference (Tests/IshizukiKitTests/MoEBlockTests.swift:94-126) written out per
     token with numpy: softmax, top-k by sorting (ties to the lower index), renormalised weights,
     one SwiGLU per chosen expert with the fp16 activations of an fp16 model (each projection's
@@ -232,6 +232,9 @@ def _moe_loop_reference(x, logits, gate, up, down, t_, E, H, I, k):
             o = r16(Wd[e] @ h)
             acc = (acc + (o * w[s]).astype(np.float32)).astype(np.float32)
             bound[t] += w[s] * (np.abs(Wd[e]) @ np.abs(h))
+        if shared is not None:  # Text/MoEBlock.swift:158-160: sigmoid(gate) * shared in x.dtype, added in fp32
+            term = r16(r16(1.0 / (1.0 + np.exp(-np.float64(shared_gate[t])))) * shared[t].astype(np.float64))
+            acc = (acc + term.astype(np.float32)).astype(np.float32)
         y[t] = r16(acc)
     return y, bound, order
 
@@ -260,6 +263,29 @@ def test_moe_swiglu_pinned():
     w2[:, -1] = 0
     y2 = oracle.moe_swiglu(t_, x, ids, w2, gate, up, down, E, I)
     assert not np.all(np.abs(y2 - want) <= 2.0 ** -10 * bound + 2.0 ** -11 * np.abs(want) + 2.0 ** -24)
+
+
+def test_moe_swiglu_shared_expert_pinned():
+    """The shared-expert term (sigmoid of its gate logit, times its output, both fp16, added in
+    fp32 before the one narrowing) against the loop reference; dropping the term or taking the
+    gate's sigmoid with the wrong sign is caught."""
+    from ishizuki_amd import synth
+    E, H, I, k, T, t_ = 16, 512, 256, 4, 2, 12
+    gate = synth.ggml_blocks(t_, E * I, H, seed=11, scale=4e-4)
+    up = synth.ggml_blocks(t_, E * I, H, seed=12, scale=4e-4)
+    down = synth.ggml_blocks(t_, E * H, I, seed=13, scale=4e-4)
+    x = synth.fp16_normal((T, H), seed=14).astype(np.float32)
+    logits = np.random.default_rng(15).standard_normal((T, E)).astype(np.float32)
+    sh = (synth.fp16_normal((T, H), seed=16).astype(np.float32) * 0.05).astype(np.float16).astype(np.float32)
+    sg = synth.fp16_normal((T,), seed=17).astype(np.float32)
+    ids, w = oracle.moe_route(logits, k)
+    y = oracle.moe_swiglu(t_, x, ids, w, gate, up, down, E, I, shared=sh, shared_gate=sg)
+    want, bound, _ = _moe_loop_reference(x, logits, gate, up, down, t_, E, H, I, k, shared=sh, shared_gate=sg)
+    tol = 2.0 ** -10 * bound + 2.0 ** -11 * np.abs(want) + 2.0 ** -24
+    assert np.all(np.abs(y - want) <= tol)
+    assert not np.all(np.abs(oracle.moe_swiglu(t_, x, ids, w, gate, up, down, E, I) - want) <= tol)
+    assert not np.all(np.abs(oracle.moe_swiglu(t_, x, ids, w, gate, up, down, E, I, shared=sh, shared_gate=-sg)
+                             - want) <= tol)
 
 
 def test_cpu_baseline_matches_the_oracle():
