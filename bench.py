@@ -203,8 +203,10 @@ def main():
         y = torch.empty((M, N), dtype=torch.float16, device=dev)
         L = ggml._lib.lib()
         from ishizuki_amd._torch import ptr
-        calls = [lambda w=w: L.ishz_ggml_matvec(t, ptr(x), 1, M, K, ptr(w), nb, N, ptr(y),
-                                                torch.cuda.current_stream().cuda_stream) for w in ws]
+        wsb = L.ishz_ggml_workspace_size(t, M, K, N)  # K-split parts for narrow outputs (M >= 2)
+        wsp = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+        calls = [lambda w=w: L.ishz_ggml_matvec_ws(t, ptr(x), 1, M, K, ptr(w), nb, N, ptr(y), ptr(wsp), wsb,
+                                                   torch.cuda.current_stream().cuda_stream) for w in ws]
         return calls, nb, nb + 2 * M * (K + N)
 
     def affine_case(N, K, M, seed=2):

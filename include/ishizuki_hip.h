@@ -70,6 +70,17 @@ int ishz_ggml_type_size(uint32_t type);
 int ishz_ggml_matvec(uint32_t type, const void *x, int x_dtype, int M, int K, const void *blocks,
                      size_t blocks_bytes, int N, void *y, ishz_stream_t stream);
 
+/* ishz_ggml_matvec with a caller workspace of ishz_ggml_workspace_size(type, M, K, N) bytes (0:
+   none is used): for outputs too narrow to give every CU its own tiles, the M >= 2 product is
+   split along K into parts written as fp32 partials [S][M][N] and summed in part order, narrowed
+   once -- the reference's split-K verify (Core/VerifyMatmul.swift:91-107: outputs [split, m, n]
+   in fp32, then sum(axis: 0) and the cast). With a NULL or short workspace it is
+   ishz_ggml_matvec. */
+size_t ishz_ggml_workspace_size(uint32_t type, int M, int K, int N);
+int ishz_ggml_matvec_ws(uint32_t type, const void *x, int x_dtype, int M, int K, const void *blocks,
+                        size_t blocks_bytes, int N, void *y, void *workspace, size_t workspace_bytes,
+                        ishz_stream_t stream);
+
 /* GGMLKernels.matmulFew (Core/GGMLKernels.swift:219-253): the same product for M in 2..8
    (matmulFewRows, :217), 256-element block types only, as the reference. Each weight is decoded
    once into MFMA operand registers and multiplied against every row. row_blocks is accepted for

@@ -21,6 +21,8 @@ _SIGS = {
     "ishz_ggml_block_size": (I, [U32]),
     "ishz_ggml_type_size": (I, [U32]),
     "ishz_ggml_matvec": (I, [U32, P, I, I, I, P, SZ, I, P, P]),
+    "ishz_ggml_workspace_size": (SZ, [U32, I, I, I]),
+    "ishz_ggml_matvec_ws": (I, [U32, P, I, I, I, P, SZ, I, P, P, SZ, P]),
     "ishz_ggml_matmul_few": (I, [U32, P, I, I, I, P, SZ, I, I, P, P]),
     "ishz_ggml_dequant": (I, [U32, P, SZ, SZ, P, I, P]),
     "ishz_ggml_gather": (I, [U32, P, I, P, SZ, I, I, P, I, P]),

@@ -314,7 +314,8 @@ static int num_cu() {
 int gemv_num_cu() { return num_cu(); }
 
 template <class F>
-static int verify(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st);
+static int verify(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st, void *ws = nullptr,
+                  size_t ws_bytes = 0);
 
 template <class F>
 static int gemv(const void *x, int K, const void *w, int N, void *y, hipStream_t st) {
@@ -337,8 +338,9 @@ static int launch_verify(const void *x, int M, int K, const void *w, int N, void
 }
 
 template <class F>
-static int verify(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st) {
-  if (M >= 2 && K % 256 == 0) return vgemm<F>(x, M, K, w, N, y, st);
+static int verify(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st, void *ws,
+                  size_t ws_bytes) {
+  if (M >= 2 && K % 256 == 0) return vgemm<F>(x, M, K, w, N, y, st, ws, ws_bytes);
   if (N >= 4096) return launch_verify<F, 2>(x, M, K, w, N, y, st);
   return launch_verify<F, 1>(x, M, K, w, N, y, st);
 }
@@ -346,12 +348,22 @@ static int verify(const void *x, int M, int K, const void *w, int N, void *y, hi
 // The quarter-block formats: K is always a multiple of 256 (their block), so M = 1 is the
 // streaming GEMV and M >= 2 the streaming MFMA kernel.
 template <class F>
-static int quarter(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st) {
+static int quarter(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st, void *ws = nullptr,
+                   size_t ws_bytes = 0) {
   if (M == 1) {
     const typename F::Args a{(const uint8_t *)w, (size_t)(K / F::BS) * F::TS, K, N};
     return launch_gemv<F>(a, x, y, st);
   }
-  return vgemm<F>(x, M, K, w, N, y, st);
+  return vgemm<F>(x, M, K, w, N, y, st, ws, ws_bytes);
+}
+
+__global__ __launch_bounds__(256) void vgemm_sum_kernel(const float *__restrict__ part, int S, size_t n,
+                                                        uint16_t *__restrict__ y) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    float s = 0.0f;
+    for (int k = 0; k < S; k++) s += part[(size_t)k * n + i];
+    y[i] = f2h(s);
+  }
 }
 
 static int check_matmul(uint32_t type, int x_dtype, int M, int lo, int hi, int K,
@@ -374,9 +386,14 @@ using namespace ishz;
 extern "C" int ishz_ggml_block_size(uint32_t type) { return block_size(type); }
 extern "C" int ishz_ggml_type_size(uint32_t type) { return type_size(type); }
 
-extern "C" int ishz_ggml_matvec(uint32_t type, const void *x, int x_dtype, int M, int K,
-                                const void *blocks, size_t blocks_bytes, int N, void *y,
-                                ishz_stream_t stream) {
+extern "C" size_t ishz_ggml_workspace_size(uint32_t type, int M, int K, int N) {
+  if (!block_size(type) || M < 2 || M > 16 || K <= 0 || N <= 0 || K % 256) return 0;
+  return vgemm_workspace(M, K, N, num_cu());
+}
+
+extern "C" int ishz_ggml_matvec_ws(uint32_t type, const void *x, int x_dtype, int M, int K, const void *blocks,
+                                   size_t blocks_bytes, int N, void *y, void *workspace, size_t workspace_bytes,
+                                   ishz_stream_t stream) {
   int rc = check_matmul(type, x_dtype, M, 1, 16, K, blocks_bytes, N, x, blocks, y);
   if (rc) return rc;
   hipStream_t st = S(stream);
@@ -388,16 +405,24 @@ extern "C" int ishz_ggml_matvec(uint32_t type, const void *x, int x_dtype, int M
     case ISHZ_GGML_IQ2_XS: return gemv<FIQ2_XS>(x, K, blocks, N, y, st);
     }
   }
+  void *ws = workspace;
+  const size_t wb = workspace_bytes;
   switch (type) {
-  case ISHZ_GGML_Q4_0: return verify<FQ4_0>(x, M, K, blocks, N, y, st);
-  case ISHZ_GGML_Q4_K: return verify<FQ4_K>(x, M, K, blocks, N, y, st);
-  case ISHZ_GGML_Q6_K: return verify<FQ6_K>(x, M, K, blocks, N, y, st);
-  case ISHZ_GGML_IQ2_XS: return verify<FIQ2_XS>(x, M, K, blocks, N, y, st);
-#define X(T, F) case T: return quarter<F>(x, M, K, blocks, N, y, st);
+  case ISHZ_GGML_Q4_0: return verify<FQ4_0>(x, M, K, blocks, N, y, st, ws, wb);
+  case ISHZ_GGML_Q4_K: return verify<FQ4_K>(x, M, K, blocks, N, y, st, ws, wb);
+  case ISHZ_GGML_Q6_K: return verify<FQ6_K>(x, M, K, blocks, N, y, st, ws, wb);
+  case ISHZ_GGML_IQ2_XS: return verify<FIQ2_XS>(x, M, K, blocks, N, y, st, ws, wb);
+#define X(T, F) case T: return quarter<F>(x, M, K, blocks, N, y, st, ws, wb);
     ISHZ_GGML_QUARTER_FORMATS(X)
 #undef X
   }
   return decline("unsupported GGML type");
+}
+
+extern "C" int ishz_ggml_matvec(uint32_t type, const void *x, int x_dtype, int M, int K,
+                                const void *blocks, size_t blocks_bytes, int N, void *y,
+                                ishz_stream_t stream) {
+  return ishz_ggml_matvec_ws(type, x, x_dtype, M, K, blocks, blocks_bytes, N, y, nullptr, 0, stream);
 }
 
 extern "C" int ishz_ggml_matmul_few(uint32_t type, const void *x, int x_dtype, int M, int K,

@@ -43,10 +43,12 @@ namespace ishz {
 //   void finish(g, c0, M, tb, te, out)   write tokens c0 .. c0 + M - 1 of tiles tb .. te - 1;
 //                                 out[(tile - tb) * 256 + tk * 16 + n] is row 16 tile + n
 //   PAIRS                         tiles_per_wg must be even and start even (SwiGLU pairs)
-// Work split: a workgroup owns tiles tb .. te - 1 of its group; the (tile, step) items go to its
-// waves round-robin (item i to wave i % NW), so short K still uses every wave.
+// Work split: a workgroup owns tiles tb .. te - 1 of its group and, with S > 1 (K split: the
+// problem's finish then writes fp32 partials), the S-th part blockIdx.x % S of the K steps; the
+// (tile, step) items go to its waves round-robin (item i to wave i % NW), so short K still uses
+// every wave.
 template <class F, class P, int NQ, int D, int NW>
-__global__ __launch_bounds__(64 * NW) void vgemm_kernel(P p, int K, int Kc, int tiles_per_wg) {
+__global__ __launch_bounds__(64 * NW) void vgemm_kernel(P p, int K, int Kc, int tiles_per_wg, int S) {
   constexpr int NS = F::VNS, MPS = 8 / NS;  // MFMAs per sub-unit
   constexpr int MT = 4 * NQ;                // tokens per pass, padded to whole quads
   typedef typename P::Group Group;
@@ -56,8 +58,10 @@ __global__ __launch_bounds__(64 * NW) void vgemm_kernel(P p, int K, int Kc, int 
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int n = lane & 15, G = lane >> 4;
   const int N = p.rows(gp), ntiles = (N + 15) / 16;
-  const int tb = blockIdx.x * tiles_per_wg, te = min(tb + tiles_per_wg, ntiles);
+  const int tb = (blockIdx.x / S) * tiles_per_wg, te = min(tb + tiles_per_wg, ntiles);
   if (tb >= te) return;
+  const int split = blockIdx.x % S, ksteps = K / 256;
+  const int kb = split * ksteps / S * 256, ke = (split + 1) * ksteps / S * 256;  // this part of K
   const int ntl = te - tb;
   const int cs = Kc / 256;                    // steps per chunk
   const int IW = cs * 32 + 1;                 // token image stride (16-byte words, padded)
@@ -81,8 +85,8 @@ __global__ __launch_bounds__(64 * NW) void vgemm_kernel(P p, int K, int Kc, int 
       for (int i = threadIdx.x; i < ntl * 256; i += blockDim.x) outb[i] = 0.0f;
     else
       for (int i = threadIdx.x; i < NW * tiles_per_wg * NQ * 64; i += blockDim.x) accb[i] = 0.0f;
-    for (int kc0 = 0; kc0 < K; kc0 += Kc) {
-      const int steps = min(Kc, K - kc0) / 256;
+    for (int kc0 = kb; kc0 < ke; kc0 += Kc) {
+      const int steps = min(Kc, ke - kc0) / 256;
       // ---- stage every token's x for this chunk
       for (int it = threadIdx.x; it < MT * steps * 4 * NS; it += blockDim.x) {
         const int s = it % NS, g = (it / NS) % 4, j = (it / (NS * 4)) % steps, tk = it / (NS * 4 * steps);
@@ -213,30 +217,33 @@ static size_t vgemm_lds(int Kc, int T) {
          (T >= NW ? 0 : (size_t)NW * T * NQ * 64 * 4) + (size_t)T * 256 * 4 + F::tab_bytes();
 }
 
-// Launch over `groups` groups of (up to) `rows` weight rows each; T tiles per workgroup.
+// Launch over `groups` groups of (up to) `rows` weight rows each; T tiles per workgroup, K in S parts.
 template <class F, class P, int NQ>
-static int launch_vgemm_p(const P &p, int K, int rows, int groups, int T, hipStream_t st) {
+static int launch_vgemm_p(const P &p, int K, int rows, int groups, int T, hipStream_t st, int S = 1) {
   constexpr int NW = 8;
   constexpr int D = F::VDEPTH;  // ring depth: what fits the registers with the format's raw
   const int ntiles = (rows + 15) / 16;
   const size_t budget = 150 * 1024;
-  int Kc = K;
+  int Kc = (K / 256 + S - 1) / S * 256;  // one part of K
   while (Kc > 256 && vgemm_lds<F, NQ, NW>(Kc, T) > budget) Kc -= 256;
   if (vgemm_lds<F, NQ, NW>(Kc, T) > budget) return decline("verify x does not fit in LDS");
   const size_t lds = vgemm_lds<F, NQ, NW>(Kc, T);
-  hipLaunchKernelGGL((vgemm_kernel<F, P, NQ, D, NW>), dim3((ntiles + T - 1) / T, groups), dim3(64 * NW), lds, st, p,
-                     K, Kc, T);
+  hipLaunchKernelGGL((vgemm_kernel<F, P, NQ, D, NW>), dim3((ntiles + T - 1) / T * S, groups), dim3(64 * NW), lds, st,
+                     p, K, Kc, T, S);
   ISHZ_LAUNCH_CHECK("vgemm launch");
   return ISHZ_OK;
 }
 
-// The plain problem: y[M][N] = x[M][K] . W^T for 2..16 tokens.
+// The plain problem: y[M][N] = x[M][K] . W^T for 2..16 tokens; with a K split, part [S][M][N]
+// fp32 receives each part's partial product instead (summed by vgemm_sum_kernel).
 struct VPlain {
   const uint16_t *x;
   const uint8_t *w;
   size_t rb;
   int M, K, N;
   uint16_t *y;
+  float *part;
+  int S;
   struct Group {};
   DEV bool group(int, Group &) const { return true; }
   DEV int count(const Group &) const { return M; }
@@ -244,24 +251,67 @@ struct VPlain {
   DEV const uint16_t *xrow(const Group &, int tk) const { return x + (size_t)tk * K; }
   DEV const uint8_t *wrow(const Group &, int row) const { return w + (size_t)row * rb; }
   DEV void finish(const Group &, int c0, int m, int tb, int te, const float *out) const {
+    float *pp = part ? part + (size_t)(blockIdx.x % S) * M * N : nullptr;
     for (int o = threadIdx.x; o < (te - tb) * 256; o += blockDim.x) {
       const int tk = (o >> 4) & 15, row = (tb + (o >> 8)) * 16 + (o & 15);
-      if (tk < m && row < N) y[(size_t)(c0 + tk) * N + row] = f2h(out[o]);
+      if (tk < m && row < N) {
+        if (pp) pp[(size_t)(c0 + tk) * N + row] = out[o];
+        else y[(size_t)(c0 + tk) * N + row] = f2h(out[o]);
+      }
     }
   }
 };
 
+// y = the S parts' partial products summed in part order, narrowed once.
+__global__ __launch_bounds__(256) void vgemm_sum_kernel(const float *__restrict__ part, int S, size_t n,
+                                                        uint16_t *__restrict__ y);
+
+// K split for long K (>= 32 steps of 256: x no longer fits one workgroup's LDS and is restaged in
+// chunks) and outputs too narrow to give every CU two workgroups' tiles: up to 8 tiles per
+// workgroup (x is staged once per workgroup, so more tiles per workgroup stage it fewer times in
+// all) and enough parts of K for one round of workgroups, each part at least 4 steps. Measured at
+// 5120x25600, M = 8: Q4_K 57 -> 34 us; at K = 4096 the extra sum launch costs more than it saves.
+// 1: no split.
+inline int vgemm_splits(int M, int K, int N, int cus, int &T) {
+  const int ntiles = (N + 15) / 16, steps = K / 256;
+  T = (ntiles + cus - 1) / cus;  // tiles per workgroup without a split: one round of CUs
+  if (M < 2 || ntiles >= 2 * cus || steps < 32) return 1;
+  const int t8 = std::min(8, ntiles), runs = (ntiles + t8 - 1) / t8;
+  const int S = std::min(std::max(cus / runs, 1), steps / 4);
+  if (S < 2) return 1;
+  T = t8;
+  return S;
+}
+inline size_t vgemm_workspace(int M, int K, int N, int cus) {
+  int T;
+  const int S = vgemm_splits(M, K, N, cus, T);
+  return S > 1 ? (size_t)S * M * N * 4 : 0;
+}
+
 template <class F>
-static int vgemm(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st) {
-  const VPlain p{(const uint16_t *)x, (const uint8_t *)w, (size_t)(K / F::BS) * F::TS, M, K, N, (uint16_t *)y};
-  const int ntiles = (N + 15) / 16;
-  const int T = (ntiles + gemv_num_cu() - 1) / gemv_num_cu();  // tiles per workgroup: one round of CUs
-  switch ((M + 3) / 4) {
-    case 1: return launch_vgemm_p<F, VPlain, 1>(p, K, N, 1, T, st);
-    case 2: return launch_vgemm_p<F, VPlain, 2>(p, K, N, 1, T, st);
-    case 3: return launch_vgemm_p<F, VPlain, 3>(p, K, N, 1, T, st);
-    default: return launch_vgemm_p<F, VPlain, 4>(p, K, N, 1, T, st);
+static int vgemm(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st, void *ws = nullptr,
+                 size_t ws_bytes = 0) {
+  int T;
+  int S = vgemm_splits(M, K, N, gemv_num_cu(), T);
+  if (S > 1 && (!ws || ws_bytes < (size_t)S * M * N * 4)) {  // no room for the parts: unsplit
+    S = 1;
+    T = ((N + 15) / 16 + gemv_num_cu() - 1) / gemv_num_cu();
   }
+  const VPlain p{(const uint16_t *)x, (const uint8_t *)w, (size_t)(K / F::BS) * F::TS, M, K, N, (uint16_t *)y,
+                 S > 1 ? (float *)ws : nullptr, S};
+  int rc;
+  switch ((M + 3) / 4) {
+    case 1: rc = launch_vgemm_p<F, VPlain, 1>(p, K, N, 1, T, st, S); break;
+    case 2: rc = launch_vgemm_p<F, VPlain, 2>(p, K, N, 1, T, st, S); break;
+    case 3: rc = launch_vgemm_p<F, VPlain, 3>(p, K, N, 1, T, st, S); break;
+    default: rc = launch_vgemm_p<F, VPlain, 4>(p, K, N, 1, T, st, S); break;
+  }
+  if (rc || S == 1) return rc;
+  const size_t n = (size_t)M * N;
+  hipLaunchKernelGGL(vgemm_sum_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 2048)), dim3(256), 0, st,
+                     (const float *)ws, S, n, (uint16_t *)y);
+  ISHZ_LAUNCH_CHECK("vgemm sum launch");
+  return ISHZ_OK;
 }
 
 }  // namespace ishz

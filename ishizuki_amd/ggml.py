@@ -33,16 +33,21 @@ def row_bytes(t, K):
 
 
 def matvec(x, blocks, type_, output_dim):
-    """GGMLKernels.matvec (Core/GGMLKernels.swift:177): x [M, K] -> [M, N] in x.dtype."""
+    """GGMLKernels.matvec (Core/GGMLKernels.swift:177): x [M, K] -> [M, N] in x.dtype. A narrow
+    output with M >= 2 is split along K into a temporary fp32 workspace, as the reference's
+    split-K verify returns [split, m, n] fp32 parts and sums them."""
     require_cuda(x, blocks)
     if x.dim() != 2:
         return None
     x = x.contiguous()
     M, K = x.shape
+    L = _lib.lib()
     y = torch.empty((M, output_dim), dtype=x.dtype, device=x.device)
-    rc = _lib.lib().ishz_ggml_matvec(type_, ptr(x), DTYPES.get(x.dtype, -1), M, K, ptr(blocks),
-                                     blocks.numel() * blocks.element_size(), output_dim, ptr(y),
-                                     stream())
+    wsb = L.ishz_ggml_workspace_size(type_, M, K, output_dim)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=x.device) if wsb else None
+    rc = L.ishz_ggml_matvec_ws(type_, ptr(x), DTYPES.get(x.dtype, -1), M, K, ptr(blocks),
+                               blocks.numel() * blocks.element_size(), output_dim, ptr(y),
+                               ptr(ws) if ws is not None else None, wsb, stream())
     return y if _lib.check(rc, "ggml_matvec") else None
 
 

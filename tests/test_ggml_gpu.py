@@ -152,3 +152,32 @@ def test_apply_row_policy(rows):
     y = ggml.apply(torch.from_numpy(x).to(DEV), torch.from_numpy(blk).to(DEV), ggml.Q4_K, N)
     assert y is not None and y.shape == (rows, N)
     assert_close(y.float().cpu().numpy(), ref, bound=bd, what=f"ggml apply rows={rows}")
+
+
+@pytest.mark.parametrize("t", [ggml.Q4_0, ggml.Q4_K, ggml.Q6_K, ggml.IQ2_XS, ggml.IQ3_S])
+@pytest.mark.parametrize("M", [2, 9])
+def test_verify_k_split_matches_unsplit(t, M):
+    """A narrow output (33 tiles) with a workspace takes the K split (fp32 parts summed in part
+    order); without one, the unsplit kernel. Both against the oracle, per element."""
+    from ishizuki_amd import _lib
+    from ishizuki_amd._torch import ptr, stream
+    N, K = 520, 8192
+    L = _lib.lib()
+    wsb = L.ishz_ggml_workspace_size(t, M, K, N)
+    assert wsb > 0, "this shape should be split"
+    assert L.ishz_ggml_workspace_size(t, M, K, 17408) == 0  # wide outputs are not
+    assert L.ishz_ggml_workspace_size(t, 1, K, N) == 0      # nor the GEMV
+    blocks = synth.ggml_blocks(t, N, K, seed=M + 3 * t)
+    x = synth.fp16_normal((M, K), seed=M + 7)
+    wb, xd = torch.from_numpy(blocks).to(DEV), torch.from_numpy(x).to(DEV)
+    ys = []
+    for ws_bytes in (wsb, 0):
+        y = torch.empty((M, N), dtype=torch.float16, device=DEV)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
+        print(f"k-split t={t} M={M} ws={ws_bytes}", flush=True)
+        assert L.ishz_ggml_matvec_ws(t, ptr(xd), _lib.DT_F16, M, K, ptr(wb), blocks.nbytes, N, ptr(y),
+                                     ptr(ws) if ws_bytes else None, ws_bytes, stream()) == _lib.OK
+        ys.append(y.float().cpu().numpy())
+    ref, bd = ggml_reference(t, x.astype(np.float32), blocks, N)
+    for y, what in zip(ys, ("split", "unsplit")):
+        assert_close(y, ref, bound=bd, what=f"{what} t={t} M={M}")
