@@ -16,7 +16,7 @@ Also printed (same JSON line, "families"), every BASELINE config at its own shap
   cfg4  MoE FFN, 128 Q4_K experts, H 2048, I 768, top-8, T = 1, 8, 64
 and the north-star shape 17408x5120 for Q4_0, Q4_K, Q6_K and IQ2_XS at M = 1 and 8. With --all,
 also the other GGUF formats (Q2_K, IQ4_XS, IQ2_XXS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_S, IQ1_M), the
-4- and 8-bit affine packs and the MoE over affine experts. cpu_baseline: the CPU restatement
+3- to 8-bit affine packs and the MoE over affine experts. cpu_baseline: the CPU restatement
 (oracle/ishz_oracle.c, timed in C: rotate, then dequantize-then-dot; and the fused decode-dot)
 on the full headline matrix, OpenMP on the host's cores, median of 10.
 """
@@ -387,7 +387,7 @@ def main():
         for M in (1, 8):
             add("northstar", nm, lambda t=t, M=M: ggml_case(t, NS, KS, M), M, f"{NS}x{KS}", nk=(NS, KS))
     if args.all:
-        for bits in (4, 8):
+        for bits in (3, 4, 5, 6, 8):
             for M in (1, 8):
                 add("extra", f"affine{bits}_g64", lambda M=M, bits=bits: affine_nbit_case(NS, KS, M, bits), M,
                     f"{NS}x{KS}", nk=(NS, KS))

@@ -109,13 +109,13 @@ int ishz_hadamard(const void *x, int dtype, int rows, int width, int block, cons
                   int inverse, void *y, ishz_stream_t stream);
 
 /* MLX affine quantized matmul: y[M][N] = x[M][K] . W^T, W[n][k] = s[n][k/group] * q + b[...].
-   codes u32 [N][K*bits/32], bits 2, 4 or 8 (code k at bits bits*(k%(32/bits)) of word
-   k/(32/bits): MLX's pack, Quantize/WeightedAffineQuantizer.swift:142-153), scales/biases
+   codes u32 [N][K*bits/32], bits 2..8 (code k at bit k*bits of the row's little-endian u32
+   stream: MLX's pack, Quantize/WeightedAffineQuantizer.swift:142-153), scales/biases
    [N][K/group] in scale_dtype (fp16 or bf16). x and y fp16. M = 1 is the streaming GEMV (MLX
    quantizedMM's qmv, called at Core/Hadamard.swift:228-230); M = 2..16 the MFMA verify kernel
-   (VerifyMatmul.applyAny, Core/VerifyMatmul.swift:73-120, whose fast path takes the same three
-   widths, :89). Declines: other widths, group not 64/128, K % 128 (and K % 256 for 4/8-bit
-   verify rows), other dtypes. */
+   (VerifyMatmul.applyAny, Core/VerifyMatmul.swift:73-120: its fast path takes 2, 4 and 8 bits,
+   :89, its generic path the other widths, :273-290). Declines: group not 64/128, K % 128 (and
+   K % 256 for verify rows of packs other than 2-bit), other dtypes. */
 int ishz_affine_matmul(const void *x, int x_dtype, int M, int K, const uint32_t *codes,
                        const void *scales, const void *biases, int scale_dtype, int N, int bits,
                        int group, void *y, ishz_stream_t stream);

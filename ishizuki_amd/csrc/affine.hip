@@ -468,7 +468,7 @@ static int check_affine(const void *x, int x_dtype, int M, int K, const void *co
                         const void *scales, const void *biases, int scale_dtype, int N, int bits,
                         int group, const void *y) {
   if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
-  if (bits != 2 && bits != 4 && bits != 8) return decline("packs of 2, 4 or 8 bits are decoded in-kernel");
+  if (bits < 2 || bits > 8) return decline("packs of 2 to 8 bits are decoded in-kernel");
   if (group != 64 && group != 128) return decline("group size must be 64 or 128");
   if (scale_dtype != ISHZ_DT_F16 && scale_dtype != ISHZ_DT_BF16) return decline("scales must be fp16 or bf16");
   if (M < 1 || M > 16) return decline("row count outside 1..16");
@@ -477,19 +477,26 @@ static int check_affine(const void *x, int x_dtype, int M, int K, const void *co
   return ISHZ_OK;
 }
 
-// 4- and 8-bit packs (x already rotated when the layer rotates).
+// Packs of 3 to 8 bits (x already rotated when the layer rotates).
 static int affine_nbit_dispatch(const void *x, int M, int K, const uint32_t *codes, const void *scales,
                                 const void *biases, int bf16s, int N, int bits, int group, void *y, hipStream_t st) {
-#define ISHZ_NB(B, G)                                                                              \
-  return bf16s ? affine_nbit<B, G, true>(x, M, K, codes, scales, biases, N, y, st)              \
-               : affine_nbit<B, G, false>(x, M, K, codes, scales, biases, N, y, st)
-  if (bits == 4) {
-    if (group == 64) ISHZ_NB(4, 64);
-    ISHZ_NB(4, 128);
+#define ISHZ_NB(B)                                                                                      \
+  case B:                                                                                              \
+    if (group == 64)                                                                                   \
+      return bf16s ? affine_nbit<B, 64, true>(x, M, K, codes, scales, biases, N, y, st)                \
+                   : affine_nbit<B, 64, false>(x, M, K, codes, scales, biases, N, y, st);              \
+    return bf16s ? affine_nbit<B, 128, true>(x, M, K, codes, scales, biases, N, y, st)                 \
+                 : affine_nbit<B, 128, false>(x, M, K, codes, scales, biases, N, y, st);
+  switch (bits) {
+    ISHZ_NB(3)
+    ISHZ_NB(4)
+    ISHZ_NB(5)
+    ISHZ_NB(6)
+    ISHZ_NB(7)
+    ISHZ_NB(8)
   }
-  if (group == 64) ISHZ_NB(8, 64);
-  ISHZ_NB(8, 128);
 #undef ISHZ_NB
+  return decline("packs of 2 to 8 bits are decoded in-kernel");
 }
 
 static int affine_dispatch(const void *x, int M, int K, const float *signs, int block,
@@ -556,7 +563,7 @@ extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, cons
   if (block > 0 && (!pow2(block) || block > 4096 || K % block)) return decline("bad Hadamard block");
   const int bf16s = scale_dtype == ISHZ_DT_BF16;
   hipStream_t st = S(stream);
-  if (bits != 2) {  // 4- and 8-bit packs: rotate x once into the workspace, then the matmul
+  if (bits != 2) {  // 3- to 8-bit packs: rotate x once into the workspace, then the matmul
     if (block == 0) return affine_nbit_dispatch(x, M, K, codes, scales, biases, bf16s, N, bits, group, y, st);
     if (!workspace || workspace_bytes < ishz_affine_workspace_size(M, K))
       return einval("workspace too small (ishz_affine_workspace_size)");

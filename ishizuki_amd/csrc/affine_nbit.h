@@ -1,7 +1,8 @@
-// MLX affine packs of 4 or 8 bits per weight (VerifyMatmul.applyAny's other fast-path widths,
-// Core/VerifyMatmul.swift:83-89; pack layout Quantize/WeightedAffineQuantizer.swift:142-153):
-// w[n][k] = s[n][k/gs] * q + b[n][k/gs], q the bits-wide field k of the row's little-endian u32
-// stream, so a word holds 8 (4-bit) or 4 (8-bit) consecutive codes.
+// MLX affine packs of 3 to 8 bits per weight (VerifyMatmul.applyAny: the 4- and 8-bit fast paths
+// and the generic one for 3, 5, 6 and 7 bits, Core/VerifyMatmul.swift:83-89,
+// 273-290; pack layout Quantize/WeightedAffineQuantizer.swift:142-153): w[n][k] = s[n][k/gs] * q +
+// b[n][k/gs], q the bits-wide field k of the row's little-endian u32 stream, so a word holds 8
+// (4-bit) or 4 (8-bit) consecutive codes and 64 codes of any width fill 2 * bits whole words.
 //
 // One format serves both skeletons: a "unit" / verify quarter is 64 weights of one group (group
 // size 64 or 128), 32 or 64 bytes of codes plus the group's scale and bias. Codes are masked in
@@ -9,7 +10,9 @@
 // pairs; the offset and the bias come back through the sum of x over the unit:
 //   sum_k w_k x_k = s * (sum (1024 + q_k) x_k - 1024 X) + b * X.
 // Pair orders: 4-bit word >> 4j masked with 0x000F000F gives codes (j, j + 4); 8-bit word (>> 8)
-// masked with 0x00FF00FF gives (0, 2) and (1, 3). x is staged in the same pair order.
+// masked with 0x00FF00FF gives (0, 2) and (1, 3). x is staged in the same pair order. 3, 5, 6
+// and 7 bits: codes (2j, 2j + 1) are the low 2 * bits of one funnel shift of the unit's words (a
+// compile-time offset into the stream), masked and shifted into a pair; x in natural order.
 #pragma once
 #include "ggml_formats.h"
 #include "vgemm.h"
@@ -55,7 +58,7 @@ struct VAffineN {
 
 template <int BITS, int GS, bool BF16S>
 struct FAffineN : GgmlGemv<FAffineN<BITS, GS, BF16S>> {
-  static_assert(BITS == 4 || BITS == 8, "4- or 8-bit packs");
+  static_assert(BITS >= 3 && BITS <= 8, "3- to 8-bit packs");
   using Base = GgmlGemv<FAffineN<BITS, GS, BF16S>>;
   struct Args {
     const uint32_t *codes;
@@ -67,23 +70,29 @@ struct FAffineN : GgmlGemv<FAffineN<BITS, GS, BF16S>> {
   static constexpr int RING = 5;
   static constexpr int R = 8, Q = 2, SUM_LEN = 32;
   static constexpr bool XSUM = true, GRID = false, VGRID = false, XPERM = BITS == 8;
-  static DEV u4 xperm(u4 v) { return BITS == 4 ? perm04(v) : perm0213(v); }
+  static constexpr bool MASKED = BITS == 4 || BITS == 8;  // whole codes per word: masked in place
+  static DEV u4 xperm(u4 v) {
+    if constexpr (BITS == 4) return perm04(v);
+    else if constexpr (BITS == 8) return perm0213(v);
+    else return v;
+  }
   static __host__ __device__ int units(int K) { return K / 64; }
   static int occ(const Args &) { return 2; }
   static size_t extra_lds_bytes(const Args &) { return 0; }
   static DEV int slot_k(int u, int r) { return 64 * u + 8 * r; }
   static DEV int sum_k(int u, int q) { return 64 * u + 32 * q; }
   struct Raw {
-    u4 q[WPU / 4];
+    u2 q[WPU / 2];
     uint32_t s, b;
   };
+  static DEV uint32_t word(const Raw &r, int i) { return r.q[i >> 1][i & 1]; }
   static DEV float ld_s(uint32_t v) { return BF16S ? __builtin_bit_cast(float, v << 16) : h2f(v); }
   // Unit u of a row: its codes and its group's scale and bias.
   static DEV Raw load_unit(const AffRow &w, int u) {
     Raw r;
-    const u4 *c = (const u4 *)(w.codes + (size_t)u * WPU);
+    const u2 *c = (const u2 *)(w.codes + (size_t)u * WPU);  // 8-byte aligned: rows are K * BITS / 8 bytes
 #pragma unroll
-    for (int i = 0; i < WPU / 4; i++) r.q[i] = c[i];
+    for (int i = 0; i < WPU / 2; i++) r.q[i] = c[i];
     r.s = w.scales[u * 64 / GS];
     r.b = w.biases[u * 64 / GS];
     return r;
@@ -99,13 +108,22 @@ struct FAffineN : GgmlGemv<FAffineN<BITS, GS, BF16S>> {
 #pragma unroll
     for (int t = 0; t < 8; t++) {
       if constexpr (BITS == 4) {
-        const uint32_t w = r.q[t >> 2][t & 3];
+        const uint32_t w = word(r, t);
         B[t] = u4{and_or(w, 0x000F000Fu, mg), and_or(w >> 4, 0x000F000Fu, mg), and_or(w >> 8, 0x000F000Fu, mg),
                   and_or(w >> 12, 0x000F000Fu, mg)};
-      } else {
-        const uint32_t w0 = r.q[(2 * t) >> 2][(2 * t) & 3], w1 = r.q[(2 * t + 1) >> 2][(2 * t + 1) & 3];
+      } else if constexpr (BITS == 8) {
+        const uint32_t w0 = word(r, 2 * t), w1 = word(r, 2 * t + 1);
         B[t] = u4{and_or(w0, 0x00FF00FFu, mg), and_or(w0 >> 8, 0x00FF00FFu, mg), and_or(w1, 0x00FF00FFu, mg),
                   and_or(w1 >> 8, 0x00FF00FFu, mg)};
+      } else {
+        constexpr uint32_t MASK = (1u << BITS) - 1;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int p = (8 * t + 2 * i) * BITS, wi = p >> 5, o = p & 31;  // codes 8t + 2i, + 1
+          const uint32_t lo = word(r, wi);
+          const uint32_t win = o + 2 * BITS <= 32 ? lo >> o : __builtin_amdgcn_alignbit(word(r, wi + 1), lo, o);
+          B[t][i] = (((win >> BITS) & MASK) << 16) | and_or(win, MASK, mg);
+        }
       }
     }
   }
@@ -137,7 +155,7 @@ struct FAffineN : GgmlGemv<FAffineN<BITS, GS, BF16S>> {
 
   // Streaming MFMA verify: quarter g of step j is unit 4j + g of the chunk; one scale group per
   // quarter (VNS = 1, eight MFMAs).
-  static constexpr int VNS = 1, VSTEP_BYTES = 0, VDEPTH = BITS == 4 ? 3 : 2;
+  static constexpr int VNS = 1, VSTEP_BYTES = 0, VDEPTH = BITS <= 4 ? 3 : 2;
   typedef Raw VRaw;
   // Any problem whose rows are affine rows: P::arow(group, row) or, with one group, P::arow(row).
   template <class P>
@@ -166,7 +184,7 @@ struct FAffineN : GgmlGemv<FAffineN<BITS, GS, BF16S>> {
   }
 };
 
-// y[M][N] = x . W^T for a 4- or 8-bit pack: the streaming GEMV at M = 1, the streaming MFMA
+// y[M][N] = x . W^T for a 3- to 8-bit pack: the streaming GEMV at M = 1, the streaming MFMA
 // kernel for M = 2..16 (K a multiple of 256 there; declined otherwise).
 template <int BITS, int GS, bool BF16S>
 static int affine_nbit(const void *x, int M, int K, const uint32_t *codes, const void *scales, const void *biases,
@@ -177,7 +195,7 @@ static int affine_nbit(const void *x, int M, int K, const uint32_t *codes, const
     const typename F::Args a{codes, (const uint16_t *)scales, (const uint16_t *)biases, K, N};
     return launch_gemv<F>(a, x, y, st);
   }
-  if (K % 256) return decline("verify rows need K a multiple of 256 for 4- and 8-bit packs");
+  if (K % 256) return decline("verify rows need K a multiple of 256 for packs other than 2-bit");
   const VAffineN p{(const uint16_t *)x, codes, (const uint16_t *)scales, (const uint16_t *)biases, M, K, N,
                    (uint16_t *)y, K * BITS / 32, K / GS};
   const int ntiles = (N + 15) / 16;

@@ -64,20 +64,27 @@ def affine_pack(N, K, group=64, bits=2, seed=0, scale=0.02, probs=(0.3, 0.4, 0.3
     return codes, s, b
 
 
-def affine_pack_bits(N, K, bits, group=64, seed=0, scale=0.02):
-    """MLX affine pack of `bits` in {4, 8}: uniform random codes (value k at bits (k % (32/bits)) *
-    bits of word k / (32/bits)), scales |N|*scale and biases -s * 2^(bits-1) (fp16), so weights
-    are centred on zero."""
-    assert bits in (4, 8)
+def affine_pack_bits(N, K, bits, group=64, seed=0, scale=0.02, return_codes=False):
+    """MLX affine pack of `bits` in 2..8: uniform random codes, code k at bit k * bits of the row's
+    little-endian u32 stream (for bits dividing 32: bits (k % (32/bits)) * bits of word
+    k / (32/bits)), scales |N|*scale and biases -s * 2^(bits-1) (fp16), so weights are centred
+    on zero. return_codes: also the codes themselves [N, K]."""
+    assert 2 <= bits <= 8 and (K * bits) % 32 == 0
     r = rng(seed)
-    per = 32 // bits
-    q = r.integers(0, 1 << bits, size=(N, K // per, per), dtype=np.uint64)
-    codes = np.zeros((N, K // per), np.uint64)
-    for i in range(per):
-        codes |= q[:, :, i] << np.uint64(bits * i)
+    q = r.integers(0, 1 << bits, size=(N, K), dtype=np.uint64)
+    pos = np.arange(K, dtype=np.uint64) * np.uint64(bits)
+    word, off = (pos // np.uint64(32)).astype(np.int64), pos % np.uint64(32)
+    acc = np.zeros((N, K * bits // 32 + 1), np.uint64)  # 64-bit words: a code may spill into the next
+    np.add.at(acc, (slice(None), word), q << off)       # disjoint bits: the sum is the OR
+    lo = acc & np.uint64(0xFFFFFFFF)
+    codes = lo.copy()
+    codes[:, 1:] += acc[:, :-1] >> np.uint64(32)         # the spill of word w lands in word w + 1
+    codes = codes[:, :K * bits // 32].astype(np.uint32)
     s = fp16_absnormal(r, N * (K // group), scale).reshape(N, K // group)
     b = (-s.astype(np.float32) * (1 << (bits - 1))).astype(np.float16)
-    return codes.astype(np.uint32), s, b
+    if return_codes:
+        return codes, s, b, q.astype(np.uint32)
+    return codes, s, b
 
 
 def exl3_pack(K, N, bits2=4, seed=0, scale=0.02):

@@ -69,12 +69,13 @@ def test_affine_matmul(M, group):
     assert_close(y.float().cpu().numpy(), ref, bound=bd, what=f"affine M={M} g={group}")
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("M", [1, 2, 5, 8, 16])
 @pytest.mark.parametrize("group,bf16", [(64, False), (128, True)])
 def test_affine_wide_bits(bits, M, group, bf16):
-    """4- and 8-bit packs (VerifyMatmul.applyAny's other fast-path widths): the GEMV at M = 1,
-    the streaming MFMA kernel above."""
+    """3- to 8-bit packs (VerifyMatmul.applyAny's 4- and 8-bit fast paths and its generic one for
+    the other widths, Core/VerifyMatmul.swift:83-89, 273-290): the GEMV at M = 1, the streaming
+    MFMA kernel above."""
     N, K = 1000, 1024
     codes, s, b = synth.affine_pack_bits(N, K, bits, group=group, seed=bits + M)
     x = synth.fp16_normal((M, K), seed=M + 40)
@@ -93,18 +94,17 @@ def test_affine_wide_bits(bits, M, group, bf16):
 def _ref_bf16(x, codes, sd, bd, N, K, bits, group):
     """Reference with bf16 scales: dequantize through the oracle with unit scale / zero bias, then
     apply the bf16 values (exact in fp32)."""
-    per = 32 // bits
-    q = np.stack([(codes[:, k // per] >> np.uint32(bits * (k % per))) & np.uint32((1 << bits) - 1)
-                  for k in range(K)], 1).astype(np.float32)
+    one = np.full((N, K // group), 0x3C00, np.uint16)  # the codes themselves: scale 1, bias 0
+    q = oracle.affine_dequant(codes, one, np.zeros_like(one), N, K, bits, group)
     s = np.repeat(sd.float().cpu().numpy(), group, 1)
     b = np.repeat(bd.float().cpu().numpy(), group, 1)
     w = (s * q + b).astype(np.float32)
     return x.astype(np.float32) @ w.T
 
 
-@pytest.mark.parametrize("bits,M", [(4, 1), (4, 8), (8, 3)])
+@pytest.mark.parametrize("bits,M", [(4, 1), (4, 8), (8, 3), (3, 1), (5, 8), (6, 2)])
 def test_affine_wide_bits_rotated_linear(bits, M):
-    """PackedLinear's rotated forward with a 4- or 8-bit pack: x rotated once, then the matmul."""
+    """PackedLinear's rotated forward with a 3- to 8-bit pack: x rotated once, then the matmul."""
     N, K = 300, 1024
     codes, s, b = synth.affine_pack_bits(N, K, bits, group=64, seed=bits * 3 + M)
     x = synth.fp16_normal((M, K), seed=M + 50)

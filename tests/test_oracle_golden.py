@@ -149,6 +149,22 @@ def test_affine_closed_form_wide(bits):
     assert q.max() == (1 << bits) - 1 and q.min() == 0
 
 
+@pytest.mark.parametrize("bits", [3, 5, 6, 7, 4])
+def test_affine_closed_form_stream(bits):
+    """Any width: codes packed by numpy into the little-endian u32 stream (code k at bit k * bits,
+    spilling into the next word), read back by the oracle's C decoder, give s * q + b for the
+    codes that were packed."""
+    from ishizuki_amd import synth
+    N, K, g = 4, 256, 64
+    codes, s, b, q = synth.affine_pack_bits(N, K, bits, group=g, seed=bits, return_codes=True)
+    assert codes.shape == (N, K * bits // 32)
+    w = oracle.affine_dequant(codes, s.view(np.uint16), b.view(np.uint16), N, K, bits, g)
+    sf = np.repeat(s.astype(np.float32), g, 1)
+    bf = np.repeat(b.astype(np.float32), g, 1)
+    assert np.array_equal(w, (sf * q.astype(np.float32) + bf).astype(np.float32))
+    assert q.max() == (1 << bits) - 1 and q.min() == 0
+
+
 def test_matmul_fused_agrees_with_expanded():
     from ishizuki_amd import synth
     for t, K in ((2, 512), (12, 512), (14, 512), (17, 512)):
