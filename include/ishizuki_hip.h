@@ -26,7 +26,14 @@ typedef void *ishz_stream_t; /* hipStream_t */
 
 enum { ISHZ_OK = 0, ISHZ_DECLINED = 1, ISHZ_EINVAL = 2, ISHZ_EHIP = 3 };
 
-/* Element types of activations and outputs. */
+/* Element types of activations and outputs. The matmuls take x in any of them and write y in
+   x's dtype, as the reference's kernels templated on the activation type do. Their kernels
+   stage fp16: bf16 / fp32 x is first converted into an fp16 image with a power-of-two factor
+   per row (the row's largest value lands in [0.5, 1); outputs are multiplied back, exactly,
+   before their one narrowing to x's dtype). bf16 values convert exactly down to 2^-17 of their
+   row's largest; fp32 values round to fp16. The image lives in the call's workspace where the
+   entry point takes one, else in a stream-ordered temporary (hipMallocAsync). The MoE FFN takes
+   fp16 x only. */
 enum { ISHZ_DT_F32 = 0, ISHZ_DT_F16 = 1, ISHZ_DT_BF16 = 2 };
 
 /* GGML storage types, numbered as GGMLType's raw values (Config/GGUFFile.swift:13-43). */
@@ -63,7 +70,8 @@ int ishz_ggml_block_size(uint32_t type);
 int ishz_ggml_type_size(uint32_t type);
 
 /* GGMLKernels.matvec (Core/GGMLKernels.swift:177-213): y[M][N] = x[M][K] . W[N][K]^T with W
-   the GGML blocks of `type`, rows of W contiguous, never expanded. x and y are fp16; M in
+   the GGML blocks of `type`, rows of W contiguous, never expanded. x fp16, bf16 or fp32, y in
+   x's dtype; M in
    1..16 (matvecBatch, :146). M = 1 runs the streaming GEMV, M >= 2 the MFMA verify kernel.
    Declines (ISHZ_DECLINED) for an unsupported type or dtype, M outside 1..16, K not a whole
    number of blocks, N < 1, or blocks_bytes < N * rowBytes (:181-189). */
@@ -111,7 +119,8 @@ int ishz_hadamard(const void *x, int dtype, int rows, int width, int block, cons
 /* MLX affine quantized matmul: y[M][N] = x[M][K] . W^T, W[n][k] = s[n][k/group] * q + b[...].
    codes u32 [N][K*bits/32], bits 2..8 (code k at bit k*bits of the row's little-endian u32
    stream: MLX's pack, Quantize/WeightedAffineQuantizer.swift:142-153), scales/biases
-   [N][K/group] in scale_dtype (fp16 or bf16). x and y fp16. M = 1 is the streaming GEMV (MLX
+   [N][K/group] in scale_dtype (fp16 or bf16). x fp16, bf16 or fp32, y in x's dtype. M = 1 is
+   the streaming GEMV (MLX
    quantizedMM's qmv, called at Core/Hadamard.swift:228-230); M = 2..16 the MFMA verify kernel
    (VerifyMatmul.applyAny, Core/VerifyMatmul.swift:73-120: its fast path takes 2, 4 and 8 bits,
    :89, its generic path the other widths, :273-290). Declines: group not 64/128, K % 128 (and
@@ -121,9 +130,10 @@ int ishz_affine_matmul(const void *x, int x_dtype, int M, int K, const uint32_t 
                        int group, void *y, ishz_stream_t stream);
 
 /* The rotated PackedLinear forward (Core/Hadamard.swift:180-231): hadamardRotate(x, block,
-   signs) rounded to fp16, then ishz_affine_matmul. block = 0 means no rotation. For M = 1 the
-   rotation runs inside the GEMV (x is rotated while it is staged into LDS); for M >= 2 it is a
-   separate kernel into `workspace` (ishz_affine_workspace_size bytes). */
+   signs) rounded to x's dtype, then ishz_affine_matmul. block = 0 means no rotation. For fp16
+   x and M = 1 the rotation runs inside the GEMV (x is rotated while it is staged into LDS);
+   otherwise it is a separate kernel into `workspace` (ishz_affine_workspace_size bytes, which
+   bf16 / fp32 x always needs). */
 size_t ishz_affine_workspace_size(int M, int K);
 int ishz_affine_linear(const void *x, int x_dtype, int M, int K, const float *signs, int block,
                        const uint32_t *codes, const void *scales, const void *biases,
@@ -141,17 +151,19 @@ int ishz_exl3_dequant(const int16_t *trellis, int K, int N, int bits2, int codeb
 
 /* EXL3Kernels.rotate (Core/EXL3.swift:102-124, kernel :219-265): per 128-block of each row,
    (x * scales if before) -> WHT / sqrt(128) -> (* scales if not before), fp32 math, output in
-   out_dtype (fp32 or fp16). scales fp16 [width] (the suh / svh vectors). */
+   out_dtype; in and out fp32, fp16 or bf16. scales fp16 [width] (the suh / svh vectors). */
 int ishz_exl3_rotate(const void *x, int in_dtype, int rows, int width, const uint16_t *scales,
                      int before, void *y, int out_dtype, ishz_stream_t stream);
 
 /* EXL3Kernels.matvec (Core/EXL3.swift:149-164, kernel :286-330): yh[M][N] (fp32) = xh[M][K]
-   (fp16) . W, W decoded in-kernel. M in 1..16 (the reference: 1..8, 9..16 as two launches). */
+   (fp16, bf16 or fp32) . W, W decoded in-kernel. M in 1..16 (the reference: 1..8, 9..16 as two
+   launches). */
 int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const int16_t *trellis, int N,
                      int bits2, int codebook, float *yh, ishz_stream_t stream);
 
-/* EXL3Kernels.apply (Core/EXL3.swift:82-100): y = fp16(rotate_out(xh . W)) with
-   xh = fp16(rotate_in(x)). Needs ishz_exl3_workspace_size(M, K, N) bytes of device workspace. */
+/* EXL3Kernels.apply (Core/EXL3.swift:82-100): y = dt(rotate_out(xh . W)) with
+   xh = dt(rotate_in(x)), dt = x's dtype (fp16, bf16 or fp32). Needs
+   ishz_exl3_workspace_size(M, K, N) bytes of device workspace. */
 size_t ishz_exl3_workspace_size(int M, int K, int N);
 int ishz_exl3_apply(const void *x, int x_dtype, int M, int K, const int16_t *trellis,
                     const uint16_t *suh, const uint16_t *svh, int N, int bits2, int codebook,

@@ -20,23 +20,6 @@
 #include "gemv.h"
 
 namespace ishz {
-DEV float load_act(const void *x, size_t i, int dt) {
-  if (dt == ISHZ_DT_F32) return ((const float *)x)[i];
-  const uint16_t b = ((const uint16_t *)x)[i];
-  return dt == ISHZ_DT_F16 ? h2f(b) : __builtin_bit_cast(float, (uint32_t)b << 16);
-}
-DEV void store_act(void *y, size_t i, int dt, float v) {
-  if (dt == ISHZ_DT_F32) {
-    ((float *)y)[i] = v;
-  } else if (dt == ISHZ_DT_F16) {
-    ((uint16_t *)y)[i] = f2h(v);
-  } else {
-    uint32_t u = __builtin_bit_cast(uint32_t, v);
-    u = ((u & 0x7fffffffu) > 0x7f800000u) ? (u | 0x400000u) : u + 0x7fffu + ((u >> 16) & 1u);
-    ((uint16_t *)y)[i] = (uint16_t)(u >> 16);
-  }
-}
-
 // hadamardRotate as a kernel. Blocks up to 128: one wave per 128 contiguous values, two per
 // lane, butterflies across lanes by shuffles (stages above the block size skipped). Larger
 // blocks: one workgroup per block, in LDS. fp32 math, output in `out_dt`.
@@ -100,7 +83,7 @@ __global__ __launch_bounds__(1024) void affine_verify(const uint16_t *__restrict
                                                       const uint32_t *__restrict__ codes,
                                                       const uint16_t *__restrict__ scales,
                                                       const uint16_t *__restrict__ biases,
-                                                      int bf16s, int N, uint16_t *__restrict__ y) {
+                                                      int bf16s, int N, Out y) {
   extern __shared__ __align__(16) float red[];
   const int lane = threadIdx.x & 63, wave = wave_id(), KS = blockDim.x >> 6;
   const int j = lane & 15, g = lane >> 4;
@@ -166,7 +149,7 @@ __global__ __launch_bounds__(1024) void affine_verify(const uint16_t *__restrict
     float s = 0.0f;
     for (int v = 0; v < KS; v++) s += red[((v * T + t) * 4 + r) * 64 + l];
     const int tk = 4 * (l >> 4) + r, n = n0 + 16 * t + (l & 15);
-    if (tk < M && n < N) y[(size_t)tk * N + n] = f2h(s);
+    if (tk < M && n < N) y.put((size_t)tk * N + n, tk, s);
   }
 }
 
@@ -187,7 +170,7 @@ __global__ __launch_bounds__(512) void affine_vgemm(const uint16_t *__restrict__
                                                     const uint32_t *__restrict__ codes,
                                                     const uint16_t *__restrict__ scales,
                                                     const uint16_t *__restrict__ biases, int N,
-                                                    uint16_t *__restrict__ y, int Kc, int tiles_per_wg,
+                                                    Out y, int Kc, int tiles_per_wg,
                                                     const float *__restrict__ signs, int block,
                                                     const u4 *__restrict__ img) {
   using F = FAffine<GS, BF16S>;
@@ -363,7 +346,7 @@ __global__ __launch_bounds__(512) void affine_vgemm(const uint16_t *__restrict__
     float s = 0.0f;
     for (int w = 0; w < nw; w++) s += accb[((w * tiles_per_wg + tl) * NQ + q) * 64 + l];
     const int tk = 4 * q + (l >> 4), row = (tb + tl) * 16 + (l & 15);
-    if (tk < M && row < N) y[(size_t)tk * N + row] = f2h(s);
+    if (tk < M && row < N) y.put((size_t)tk * N + row, tk, s);
   }
 }
 
@@ -396,19 +379,19 @@ __global__ __launch_bounds__(64) void affine_prestage_kernel(FAffine<64, false>:
 
 template <int GS>
 static int affine_gemv(const void *x, const float *signs, int block, const uint32_t *codes,
-                       const void *scales, const void *biases, int bf16s, int K, int N, void *y,
+                       const void *scales, const void *biases, int bf16s, int K, int N, const Out &y,
                        hipStream_t st) {
   if (bf16s) {
     const typename FAffine<GS, true>::Args a{codes, (const uint16_t *)scales, (const uint16_t *)biases, signs, block, K, N};
-    return launch_gemv<FAffine<GS, true>>(a, x, y, st);
+    return launch_gemv<FAffine<GS, true>>(a, x, y.y, st, y.dt, y.rs);
   }
   const typename FAffine<GS, false>::Args a{codes, (const uint16_t *)scales, (const uint16_t *)biases, signs, block, K, N};
-  return launch_gemv<FAffine<GS, false>>(a, x, y, st);
+  return launch_gemv<FAffine<GS, false>>(a, x, y.y, st, y.dt, y.rs);
 }
 
 template <int GS, bool BF16S, int NQ>
 static int affine_vgemm_launch(const void *x, int M, int K, const uint32_t *codes, const void *scales,
-                               const void *biases, int N, void *y, hipStream_t st, const float *signs,
+                               const void *biases, int N, const Out &y, hipStream_t st, const float *signs,
                                int block, const u4 *img) {
   using F = FAffine<GS, BF16S>;
   constexpr int D = 4;
@@ -427,7 +410,7 @@ static int affine_vgemm_launch(const void *x, int M, int K, const uint32_t *code
   if (need(Kc) > budget) return decline("verify workspace does not fit in LDS");
   const size_t lds = need(Kc);
   hipLaunchKernelGGL((affine_vgemm<GS, BF16S, NQ, D>), dim3(wgs), dim3(64 * NW), lds, st, (const uint16_t *)x, M, K,
-                     codes, (const uint16_t *)scales, (const uint16_t *)biases, N, (uint16_t *)y, Kc, T, signs,
+                     codes, (const uint16_t *)scales, (const uint16_t *)biases, N, y, Kc, T, signs,
                      block, img);
   ISHZ_LAUNCH_CHECK("affine verify launch");
   return ISHZ_OK;
@@ -435,7 +418,7 @@ static int affine_vgemm_launch(const void *x, int M, int K, const uint32_t *code
 
 template <int GS, bool BF16S>
 static int affine_vgemm_nq(const void *x, int M, int K, const uint32_t *codes, const void *scales,
-                           const void *biases, int N, void *y, hipStream_t st, const float *signs = nullptr,
+                           const void *biases, int N, const Out &y, hipStream_t st, const float *signs = nullptr,
                            int block = 0, const u4 *img = nullptr) {
   switch ((M + 3) / 4) {
     case 1: return affine_vgemm_launch<GS, BF16S, 1>(x, M, K, codes, scales, biases, N, y, st, signs, block, img);
@@ -447,7 +430,7 @@ static int affine_vgemm_nq(const void *x, int M, int K, const uint32_t *codes, c
 
 template <int GS>
 static int affine_verify_launch(const void *x, int M, int K, const uint32_t *codes,
-                                const void *scales, const void *biases, int bf16s, int N, void *y,
+                                const void *scales, const void *biases, int bf16s, int N, const Out &y,
                                 hipStream_t st) {
   if (K % 256 == 0)
     return bf16s ? affine_vgemm_nq<GS, true>(x, M, K, codes, scales, biases, N, y, st)
@@ -459,7 +442,7 @@ static int affine_verify_launch(const void *x, int M, int K, const uint32_t *cod
   while (ks < 16 && ks < groups && wgs * ks < num_cu_aff() * 16) ks *= 2;
   hipLaunchKernelGGL((affine_verify<GS, T>), dim3(wgs), dim3(64 * ks), (size_t)ks * T * 256 * 4, st,
                      (const uint16_t *)x, M, K, codes, (const uint16_t *)scales,
-                     (const uint16_t *)biases, bf16s, N, (uint16_t *)y);
+                     (const uint16_t *)biases, bf16s, N, y);
   ISHZ_LAUNCH_CHECK("affine verify launch");
   return ISHZ_OK;
 }
@@ -467,7 +450,8 @@ static int affine_verify_launch(const void *x, int M, int K, const uint32_t *cod
 static int check_affine(const void *x, int x_dtype, int M, int K, const void *codes,
                         const void *scales, const void *biases, int scale_dtype, int N, int bits,
                         int group, const void *y) {
-  if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
+  if (x_dtype != ISHZ_DT_F16 && x_dtype != ISHZ_DT_BF16 && x_dtype != ISHZ_DT_F32)
+    return decline("activations must be fp16, bf16 or fp32");
   if (bits < 2 || bits > 8) return decline("packs of 2 to 8 bits are decoded in-kernel");
   if (group != 64 && group != 128) return decline("group size must be 64 or 128");
   if (scale_dtype != ISHZ_DT_F16 && scale_dtype != ISHZ_DT_BF16) return decline("scales must be fp16 or bf16");
@@ -479,7 +463,8 @@ static int check_affine(const void *x, int x_dtype, int M, int K, const void *co
 
 // Packs of 3 to 8 bits (x already rotated when the layer rotates).
 static int affine_nbit_dispatch(const void *x, int M, int K, const uint32_t *codes, const void *scales,
-                                const void *biases, int bf16s, int N, int bits, int group, void *y, hipStream_t st) {
+                                const void *biases, int bf16s, int N, int bits, int group, const Out &y,
+                                hipStream_t st) {
 #define ISHZ_NB(B)                                                                                      \
   case B:                                                                                              \
     if (group == 64)                                                                                   \
@@ -501,7 +486,7 @@ static int affine_nbit_dispatch(const void *x, int M, int K, const uint32_t *cod
 
 static int affine_dispatch(const void *x, int M, int K, const float *signs, int block,
                            const uint32_t *codes, const void *scales, const void *biases,
-                           int bf16s, int N, int group, void *y, hipStream_t st) {
+                           int bf16s, int N, int group, const Out &y, hipStream_t st) {
   if (M == 1) {
     return group == 64 ? affine_gemv<64>(x, signs, block, codes, scales, biases, bf16s, K, N, y, st)
                        : affine_gemv<128>(x, signs, block, codes, scales, biases, bf16s, K, N, y, st);
@@ -538,19 +523,26 @@ extern "C" int ishz_affine_matmul(const void *x, int x_dtype, int M, int K, cons
                                   int bits, int group, void *y, ishz_stream_t stream) {
   int rc = check_affine(x, x_dtype, M, K, codes, scales, biases, scale_dtype, N, bits, group, y);
   if (rc) return rc;
+  hipStream_t st = S(stream);
+  StreamTemp tmp(st);  // bf16 / fp32 activations: their fp16 image
+  if (x_dtype != ISHZ_DT_F16 && (rc = tmp.get(act_image_bytes(M, K)))) return rc;
+  const uint16_t *xh;
+  const float *rs;
+  if ((rc = act_prepare(x, x_dtype, M, K, tmp.p, st, &xh, &rs))) return rc;
+  const Out o{y, x_dtype, rs};
   if (bits != 2)
-    return affine_nbit_dispatch(x, M, K, codes, scales, biases, scale_dtype == ISHZ_DT_BF16, N, bits, group, y,
-                                S(stream));
-  return affine_dispatch(x, M, K, nullptr, 0, codes, scales, biases, scale_dtype == ISHZ_DT_BF16, N,
-                         group, y, S(stream));
+    return affine_nbit_dispatch(xh, M, K, codes, scales, biases, scale_dtype == ISHZ_DT_BF16, N, bits, group, o, st);
+  return affine_dispatch(xh, M, K, nullptr, 0, codes, scales, biases, scale_dtype == ISHZ_DT_BF16, N, group, o, st);
 }
 
 // Room for the rotated activations (fp16, general path) or every row's staged x image (what the
-// verify workgroups copy; a null or smaller workspace stages x in every workgroup). One row needs
-// none: the GEMV rotates and stages x in each workgroup.
+// verify workgroups copy; a null or smaller workspace stages x in every workgroup); bf16 / fp32
+// activations: x rotated in its own dtype (up to 4 bytes a value), then its fp16 image. One fp16
+// row needs none: the GEMV rotates and stages x in each workgroup.
 extern "C" size_t ishz_affine_workspace_size(int M, int K) {
   if (K <= 0 || M <= 0) return 0;
-  return std::max((size_t)M * K * 2, (size_t)M * FAffine<64, false>::img_words(K) * 16);
+  const size_t f16 = std::max((size_t)M * K * 2, (size_t)M * FAffine<64, false>::img_words(K) * 16);
+  return std::max(f16, (size_t)M * K * 4 + act_image_bytes(M, K));
 }
 
 extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, const float *signs,
@@ -563,16 +555,36 @@ extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, cons
   if (block > 0 && (!pow2(block) || block > 4096 || K % block)) return decline("bad Hadamard block");
   const int bf16s = scale_dtype == ISHZ_DT_BF16;
   hipStream_t st = S(stream);
+  if (x_dtype != ISHZ_DT_F16) {
+    // hadamardRotate in x's own dtype (Core/Hadamard.swift:8-23, the rotated activation the
+    // reference multiplies), then its fp16 image and the unrotated product
+    if (!workspace || workspace_bytes < ishz_affine_workspace_size(M, K))
+      return einval("workspace too small (ishz_affine_workspace_size)");
+    const void *xr = x;
+    void *img = workspace;
+    if (block > 0) {
+      if ((rc = ishz_hadamard(x, x_dtype, M, K, block, signs, 0, workspace, stream))) return rc;
+      xr = workspace;
+      img = (char *)workspace + (size_t)M * K * 4;
+    }
+    const uint16_t *xh;
+    const float *rs;
+    if ((rc = act_prepare(xr, x_dtype, M, K, img, st, &xh, &rs))) return rc;
+    const Out o{y, x_dtype, rs};
+    if (bits != 2) return affine_nbit_dispatch(xh, M, K, codes, scales, biases, bf16s, N, bits, group, o, st);
+    return affine_dispatch(xh, M, K, nullptr, 0, codes, scales, biases, bf16s, N, group, o, st);
+  }
+  const Out o{y, ISHZ_DT_F16, nullptr};
   if (bits != 2) {  // 3- to 8-bit packs: rotate x once into the workspace, then the matmul
-    if (block == 0) return affine_nbit_dispatch(x, M, K, codes, scales, biases, bf16s, N, bits, group, y, st);
+    if (block == 0) return affine_nbit_dispatch(x, M, K, codes, scales, biases, bf16s, N, bits, group, o, st);
     if (!workspace || workspace_bytes < ishz_affine_workspace_size(M, K))
       return einval("workspace too small (ishz_affine_workspace_size)");
     rc = ishz_hadamard(x, ISHZ_DT_F16, M, K, block, signs, 0, workspace, stream);
     if (rc) return rc;
-    return affine_nbit_dispatch(workspace, M, K, codes, scales, biases, bf16s, N, bits, group, y, st);
+    return affine_nbit_dispatch(workspace, M, K, codes, scales, biases, bf16s, N, bits, group, o, st);
   }
   if (block == 0 || M == 1)
-    return affine_dispatch(x, M, K, signs, block, codes, scales, biases, bf16s, N, group, y, st);
+    return affine_dispatch(x, M, K, signs, block, codes, scales, biases, bf16s, N, group, o, st);
   if (block <= 128 && K % 256 == 0) {
     // x rotated and staged once into the workspace (every token's image), else the rotation is
     // fused into each workgroup's staging
@@ -585,14 +597,14 @@ extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, cons
       img = (const u4 *)workspace;
     }
     if (group == 64)
-      return bf16s ? affine_vgemm_nq<64, true>(x, M, K, codes, scales, biases, N, y, st, signs, block, img)
-                   : affine_vgemm_nq<64, false>(x, M, K, codes, scales, biases, N, y, st, signs, block, img);
-    return bf16s ? affine_vgemm_nq<128, true>(x, M, K, codes, scales, biases, N, y, st, signs, block, img)
-                 : affine_vgemm_nq<128, false>(x, M, K, codes, scales, biases, N, y, st, signs, block, img);
+      return bf16s ? affine_vgemm_nq<64, true>(x, M, K, codes, scales, biases, N, o, st, signs, block, img)
+                   : affine_vgemm_nq<64, false>(x, M, K, codes, scales, biases, N, o, st, signs, block, img);
+    return bf16s ? affine_vgemm_nq<128, true>(x, M, K, codes, scales, biases, N, o, st, signs, block, img)
+                 : affine_vgemm_nq<128, false>(x, M, K, codes, scales, biases, N, o, st, signs, block, img);
   }
   if (!workspace || workspace_bytes < ishz_affine_workspace_size(M, K))
     return einval("workspace too small (ishz_affine_workspace_size)");
   rc = ishz_hadamard(x, ISHZ_DT_F16, M, K, block, signs, 0, workspace, stream);
   if (rc) return rc;
-  return affine_dispatch(workspace, M, K, nullptr, 0, codes, scales, biases, bf16s, N, group, y, st);
+  return affine_dispatch(workspace, M, K, nullptr, 0, codes, scales, biases, bf16s, N, group, o, st);
 }

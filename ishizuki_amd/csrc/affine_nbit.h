@@ -37,7 +37,7 @@ struct VAffineN {
   const uint32_t *codes;
   const uint16_t *scales, *biases;
   int M, K, N;
-  uint16_t *y;
+  Out y;
   int wpr, gpr;  // code words and scale groups per row
   DEV AffRow arow(int row) const {
     return {codes + (size_t)row * wpr, scales + (size_t)row * gpr, biases + (size_t)row * gpr};
@@ -51,7 +51,7 @@ struct VAffineN {
   DEV void finish(const Group &, int c0, int m, int tb, int te, const float *out) const {
     for (int o = threadIdx.x; o < (te - tb) * 256; o += blockDim.x) {
       const int tk = (o >> 4) & 15, row = (tb + (o >> 8)) * 16 + (o & 15);
-      if (tk < m && row < N) y[(size_t)(c0 + tk) * N + row] = f2h(out[o]);
+      if (tk < m && row < N) y.put((size_t)(c0 + tk) * N + row, c0 + tk, out[o]);
     }
   }
 };
@@ -188,16 +188,16 @@ struct FAffineN : GgmlGemv<FAffineN<BITS, GS, BF16S>> {
 // kernel for M = 2..16 (K a multiple of 256 there; declined otherwise).
 template <int BITS, int GS, bool BF16S>
 static int affine_nbit(const void *x, int M, int K, const uint32_t *codes, const void *scales, const void *biases,
-                       int N, void *y, hipStream_t st) {
+                       int N, const Out &y, hipStream_t st) {
   using F = FAffineN<BITS, GS, BF16S>;
   if (K % 64) return decline("K must be a multiple of 64");
   if (M == 1) {
     const typename F::Args a{codes, (const uint16_t *)scales, (const uint16_t *)biases, K, N};
-    return launch_gemv<F>(a, x, y, st);
+    return launch_gemv<F>(a, x, y.y, st, y.dt, y.rs);
   }
   if (K % 256) return decline("verify rows need K a multiple of 256 for packs other than 2-bit");
   const VAffineN p{(const uint16_t *)x, codes, (const uint16_t *)scales, (const uint16_t *)biases, M, K, N,
-                   (uint16_t *)y, K * BITS / 32, K / GS};
+                   y, K * BITS / 32, K / GS};
   const int ntiles = (N + 15) / 16;
   const int T = (ntiles + gemv_num_cu() - 1) / gemv_num_cu();
   switch ((M + 3) / 4) {

@@ -118,6 +118,36 @@ DEV uint32_t quad_bcast(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, K * 0x55, 0xf, 0xf, false);
 }
 
+// ---------------------------------------------------------------- activations and outputs
+DEV float load_act(const void *x, size_t i, int dt) {
+  if (dt == ISHZ_DT_F32) return ((const float *)x)[i];
+  const uint16_t b = ((const uint16_t *)x)[i];
+  return dt == ISHZ_DT_F16 ? h2f(b) : __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+// v narrowed to dt (fp32 as is; fp16 and bf16 round to nearest even, NaN stays NaN).
+DEV void store_act(void *y, size_t i, int dt, float v) {
+  if (dt == ISHZ_DT_F32) {
+    ((float *)y)[i] = v;
+  } else if (dt == ISHZ_DT_F16) {
+    ((uint16_t *)y)[i] = f2h(v);
+  } else {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    u = ((u & 0x7fffffffu) > 0x7f800000u) ? (u | 0x400000u) : u + 0x7fffu + ((u >> 16) & 1u);
+    ((uint16_t *)y)[i] = (uint16_t)(u >> 16);
+  }
+}
+// Where a kernel's outputs go: dtype, and the per-token-row factor 2^e of rescaled activations
+// (null: none; see act_prepare). Output i of token row t is v * rs[t] narrowed to dt.
+struct Out {
+  void *y;
+  int dt;
+  const float *rs;
+  DEV void put(size_t i, int t, float v) const {
+    if (dt == ISHZ_DT_F16 && !rs) ((uint16_t *)y)[i] = f2h(v);
+    else store_act(y, i, dt, rs ? v * rs[t] : v);
+  }
+};
+
 // ---------------------------------------------------------------- MFMA
 // C[i][j] += sum_k A[i][k] B[k][j], 16x16 fp32 tile. Lane l holds A row l%16 and B column l%16
 // (k slots chosen by l/16; any consistent k order works) and C rows 4*(l/16)+r, column l%16.
@@ -133,6 +163,30 @@ int fail(const char *what, hipError_t e);
 int decline(const std::string &why);
 int einval(const std::string &why);
 inline hipStream_t S(ishz_stream_t s) { return (hipStream_t)s; }
+
+// Activations other than fp16 (bf16, fp32) are converted once per call into an fp16 image with a
+// power-of-two factor per row, and every kernel stages that image as it stages fp16 x:
+//   xh[m][k] = fp16(x[m][k] * 2^-e_m),  2^(e_m - 1) <= max_k |x[m][k]| < 2^e_m,
+// outputs multiplied back by rs[m] = 2^e_m (exact) in fp32 before their one narrowing to x's
+// dtype. bf16 values (8 significant bits) land exactly down to 2^-17 of their row's largest
+// (fp16 subnormals below 2^-14 still hold 8 bits there); smaller ones within 2^-25 of it. fp32
+// values round to fp16 (2^-11 relative). The image: act_image_bytes(M, K) bytes of a workspace.
+size_t act_image_bytes(int M, int K);
+int act_prepare(const void *x, int dt, int M, int K, void *image, hipStream_t st, const uint16_t **xh,
+                const float **rs);
+// A stream-ordered temporary (hipMallocAsync / hipFreeAsync) for calls without a workspace.
+struct StreamTemp {
+  void *p = nullptr;
+  hipStream_t st;
+  explicit StreamTemp(hipStream_t s) : st(s) {}
+  int get(size_t bytes) {
+    const hipError_t e = hipMallocAsync(&p, bytes, st);
+    return e == hipSuccess ? ISHZ_OK : fail("temporary allocation", e);
+  }
+  ~StreamTemp() {
+    if (p) (void)hipFreeAsync(p, st);
+  }
+};
 }  // namespace ishz
 
 #define ISHZ_LAUNCH_CHECK(what)                     \

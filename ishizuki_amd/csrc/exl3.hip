@@ -502,7 +502,7 @@ __global__ __launch_bounds__(256) void exl3_rotate_kernel(const void *__restrict
                                                           size_t blocks, int width,
                                                           const uint16_t *__restrict__ scales,
                                                           int before, void *__restrict__ y,
-                                                          int out_dt, int nsum) {
+                                                          int out_dt, int nsum, const float *__restrict__ rs) {
   const size_t blk = (size_t)blockIdx.x * 4 + wave_id();
   if (blk >= blocks) return;
   const int lane = threadIdx.x & 63;
@@ -525,8 +525,8 @@ __global__ __launch_bounds__(256) void exl3_rotate_kernel(const void *__restrict
       }
     }
   } else {
-    v0 = h2f(((const uint16_t *)x)[base]);
-    v1 = h2f(((const uint16_t *)x)[base + 1]);
+    v0 = load_act(x, base, in_dt);
+    v1 = load_act(x, base + 1, in_dt);
   }
   if (before) {
     v0 *= h2f(scales[col]);
@@ -537,13 +537,20 @@ __global__ __launch_bounds__(256) void exl3_rotate_kernel(const void *__restrict
     v0 *= h2f(scales[col]);
     v1 *= h2f(scales[col + 1]);
   }
-  if (out_dt == ISHZ_DT_F32) {
-    ((float *)y)[base] = v0;
-    ((float *)y)[base + 1] = v1;
-  } else {
-    ((uint16_t *)y)[base] = f2h(v0);
-    ((uint16_t *)y)[base + 1] = f2h(v1);
+  if (rs) {  // outputs of a rescaled activation image: its row's factor back
+    const float f = rs[(blk * 128) / width];
+    v0 *= f;
+    v1 *= f;
   }
+  store_act(y, base, out_dt, v0);
+  store_act(y, base + 1, out_dt, v1);
+}
+
+// yh[m][n] *= rs[m] (the matvec's outputs for a rescaled activation image).
+__global__ __launch_bounds__(256) void exl3_scale_rows_kernel(float *__restrict__ yh, size_t n, int N,
+                                                              const float *__restrict__ rs) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    yh[i] *= rs[i / N];
 }
 
 // ------------------------------------------------------------------- host
@@ -607,14 +614,13 @@ extern "C" int ishz_exl3_dequant(const int16_t *trellis, int K, int N, int bits2
 extern "C" int ishz_exl3_rotate(const void *x, int in_dtype, int rows, int width,
                                 const uint16_t *scales, int before, void *y, int out_dtype,
                                 ishz_stream_t stream) {
-  if ((in_dtype != ISHZ_DT_F32 && in_dtype != ISHZ_DT_F16) ||
-      (out_dtype != ISHZ_DT_F32 && out_dtype != ISHZ_DT_F16))
-    return decline("rotation takes fp32 or fp16");
+  if (in_dtype < ISHZ_DT_F32 || in_dtype > ISHZ_DT_BF16 || out_dtype < ISHZ_DT_F32 || out_dtype > ISHZ_DT_BF16)
+    return decline("rotation takes fp32, fp16 or bf16");
   if (rows <= 0 || width <= 0 || width % 128) return einval("width must be a multiple of 128");
   if (!x || !y || !scales) return einval("null pointer");
   const size_t blocks = (size_t)rows * (width / 128);
   hipLaunchKernelGGL(exl3_rotate_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, S(stream), x,
-                     in_dtype, blocks, width, scales, before, y, out_dtype, 1);
+                     in_dtype, blocks, width, scales, before, y, out_dtype, 1, nullptr);
   ISHZ_LAUNCH_CHECK("exl3 rotate launch");
   return ISHZ_OK;
 }
@@ -709,11 +715,24 @@ extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const
                                 int N, int bits2, int codebook, float *yh, ishz_stream_t stream) {
   int rc = check_exl3(K, N, bits2, codebook);
   if (rc) return rc;
-  if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
+  if (x_dtype < ISHZ_DT_F32 || x_dtype > ISHZ_DT_BF16) return decline("activations must be fp16, bf16 or fp32");
   if (M < 1 || M > 16) return decline("row count outside 1..16");
   if (!xh || !trellis || !yh) return einval("null pointer");
+  hipStream_t st = S(stream);
+  StreamTemp tmp(st);  // bf16 / fp32 activations: their fp16 image
+  if (x_dtype != ISHZ_DT_F16 && (rc = tmp.get(act_image_bytes(M, K)))) return rc;
+  const uint16_t *x16;
+  const float *rs;
+  if ((rc = act_prepare(xh, x_dtype, M, K, tmp.p, st, &x16, &rs))) return rc;
   int np;
-  return exl3_matvec_core(xh, M, K, trellis, N, bits2, codebook, yh, nullptr, &np, S(stream));
+  if ((rc = exl3_matvec_core(x16, M, K, trellis, N, bits2, codebook, yh, nullptr, &np, st))) return rc;
+  if (rs) {
+    const size_t n = (size_t)M * N;
+    hipLaunchKernelGGL(exl3_scale_rows_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 1024)), dim3(256), 0,
+                       st, yh, n, N, rs);
+    ISHZ_LAUNCH_CHECK("exl3 scale launch");
+  }
+  return ISHZ_OK;
 }
 
 // Whether exl3_matvec_core takes the wide-step kernel, which can rotate x itself, and the
@@ -729,11 +748,13 @@ static bool exl3_fused_rotation(int M, int K, int N, int bits2) {
   return own + (size_t)M * (per * 16 + 256) * 2 <= 120 * 1024;
 }
 
-// x rotated (fp16), then the matvec's K-split partials (fp32 [splits][M][N], splits bounded by
-// the widest column step of any rate, 32 tiles).
+// x rotated (in x's dtype, up to 4 bytes a value), the fp16 image of bf16 / fp32 rotated
+// activations, then the matvec's K-split partials (fp32 [splits][M][N], splits bounded by the
+// widest column step of any rate, 32 tiles).
+static size_t exl3_rot_bytes(int M, int K) { return ((size_t)M * K * 4 + 255) / 256 * 256; }
 extern "C" size_t ishz_exl3_workspace_size(int M, int K, int N) {
   const int most = std::max(1, exl3_splits(M, K, std::max(1, N / 16 / 32)));
-  return ((size_t)M * K * 2 + 255) / 256 * 256 + (size_t)most * M * N * 4;
+  return exl3_rot_bytes(M, K) + act_image_bytes(M, K) + (size_t)most * M * N * 4;
 }
 
 // Device scratch of ishz_exl3_apply_static: every GPU the library runs on holds its own copy
@@ -773,23 +794,29 @@ extern "C" int ishz_exl3_apply(const void *x, int x_dtype, int M, int K, const i
                                ishz_stream_t stream) {
   int rc = check_exl3(K, N, bits2, codebook);
   if (rc) return rc;
-  if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
+  if (x_dtype < ISHZ_DT_F32 || x_dtype > ISHZ_DT_BF16) return decline("activations must be fp16, bf16 or fp32");
   if (M < 1 || M > 16) return decline("row count outside 1..16");
   if (!x || !trellis || !suh || !svh || !y) return einval("null pointer");
   if (!workspace || workspace_bytes < ishz_exl3_workspace_size(M, K, N))
     return einval("workspace too small (ishz_exl3_workspace_size)");
-  uint16_t *xh = (uint16_t *)workspace;
-  float *yh = (float *)((uint8_t *)workspace + ((size_t)M * K * 2 + 255) / 256 * 256);
+  hipStream_t st = S(stream);
+  uint8_t *xr = (uint8_t *)workspace, *img = xr + exl3_rot_bytes(M, K);
+  float *yh = (float *)(img + act_image_bytes(M, K));
   int np = 1;
-  if (exl3_fused_rotation(M, K, N, bits2)) {  // the matvec rotates its own K range of x
-    if ((rc = exl3_matvec_core(x, M, K, trellis, N, bits2, codebook, yh, yh, &np, S(stream), suh))) return rc;
+  const float *rs = nullptr;
+  if (x_dtype == ISHZ_DT_F16 && exl3_fused_rotation(M, K, N, bits2)) {  // the matvec rotates its own K range of x
+    if ((rc = exl3_matvec_core(x, M, K, trellis, N, bits2, codebook, yh, yh, &np, st, suh))) return rc;
   } else {
-    if ((rc = ishz_exl3_rotate(x, ISHZ_DT_F16, M, K, suh, 1, xh, ISHZ_DT_F16, stream))) return rc;
-    if ((rc = exl3_matvec_core(xh, M, K, trellis, N, bits2, codebook, yh, yh, &np, S(stream)))) return rc;
+    // rotated into x's dtype (EXL3Kernels.apply rotates `to: x.dtype`, Core/EXL3.swift:85), then
+    // (bf16 / fp32) its fp16 image
+    if ((rc = ishz_exl3_rotate(x, x_dtype, M, K, suh, 1, xr, x_dtype, stream))) return rc;
+    const uint16_t *x16;
+    if ((rc = act_prepare(xr, x_dtype, M, K, img, st, &x16, &rs))) return rc;
+    if ((rc = exl3_matvec_core(x16, M, K, trellis, N, bits2, codebook, yh, yh, &np, st))) return rc;
   }
   const size_t blocks = (size_t)M * (N / 128);  // output rotation, summing the K-split partials
-  hipLaunchKernelGGL(exl3_rotate_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, S(stream), yh,
-                     ISHZ_DT_F32, blocks, N, svh, 0, y, ISHZ_DT_F16, np);
+  hipLaunchKernelGGL(exl3_rotate_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, st, yh,
+                     ISHZ_DT_F32, blocks, N, svh, 0, y, x_dtype, np, rs);
   ISHZ_LAUNCH_CHECK("exl3 rotate launch");
   return ISHZ_OK;
 }
@@ -801,7 +828,7 @@ extern "C" int ishz_exl3_apply_static(const void *x, int x_dtype, int M, int K, 
                                       void *y, ishz_stream_t stream) {
   int rc = check_exl3(K, N, bits2, codebook);
   if (rc) return rc;
-  if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
+  if (x_dtype < ISHZ_DT_F32 || x_dtype > ISHZ_DT_BF16) return decline("activations must be fp16, bf16 or fp32");
   if (M < 1 || M > 16) return decline("row count outside 1..16");
   const size_t need = ishz_exl3_workspace_size(M, K, N);
   if (need > ISHZ_EXL3_STATIC_SCRATCH_BYTES)

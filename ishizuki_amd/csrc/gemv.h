@@ -105,7 +105,7 @@ __host__ __device__ constexpr int gemv_threads() {
 
 template <class F, int LPR, int D, bool RAGGED>
 __global__ __launch_bounds__(gemv_threads<F>()) void gemv_kernel(typename F::Args args, const uint16_t *__restrict__ x,
-                                                   uint16_t *__restrict__ y, int nwg, int part_off) {
+                                                   Out out, int nwg, int part_off) {
   static_assert(LPR % 16 == 0, "lanes per row must be a multiple of 16");
   extern __shared__ __align__(16) uint32_t smem[];
   const int K = args.K, N = args.N;
@@ -233,11 +233,11 @@ __global__ __launch_bounds__(gemv_threads<F>()) void gemv_kernel(typename F::Arg
     float s = 0.0f;
     for (int w = w0; w <= w1; w++) s += part[w * nrows + i];
     if constexpr (gemv_has_store<F>()) part[i] = s;  // only this thread reads row i's partials
-    else if (gf * RPW + i < N) y[gf * RPW + i] = f2h(s);
+    else if (gf * RPW + i < N) out.put(gf * RPW + i, 0, s);
   }
   if constexpr (gemv_has_store<F>()) {
     __syncthreads();
-    F::store(args, y, gf * RPW, min(nrows, N - gf * RPW), part);
+    F::store(args, (uint16_t *)out.y, gf * RPW, min(nrows, N - gf * RPW), part);
   }
 }
 
@@ -247,7 +247,7 @@ int gemv_num_cu();
 // launch's LDS allow), each an equal share of row groups. LDS: the staged x images and sums, the
 // format's tables, then the waves' partial dots for the workgroup's rows.
 template <class F, int LPR, bool RAGGED>
-static int launch_gemv_k(const typename F::Args &a, const void *x, void *y, hipStream_t st) {
+static int launch_gemv_k(const typename F::Args &a, const void *x, const Out &o, hipStream_t st) {
   constexpr int RPW = 64 / LPR;
   constexpr int NT = gemv_threads<F>(), WPG = NT / 64;
   const int units = F::units(a.K);
@@ -277,19 +277,22 @@ static int launch_gemv_k(const typename F::Args &a, const void *x, void *y, hipS
     if (pc >= per_cu || pc >= wg_cap) break;
     per_cu = pc;
   }
-  hipLaunchKernelGGL(kern, dim3(nwg), dim3(NT), lds, st, a, (const uint16_t *)x, (uint16_t *)y, nwg, (int)part_off);
+  hipLaunchKernelGGL(kern, dim3(nwg), dim3(NT), lds, st, a, (const uint16_t *)x, o, nwg, (int)part_off);
   ISHZ_LAUNCH_CHECK("gemv launch");
   return ISHZ_OK;
 }
 
 // Lanes per row: 16 for rows of up to 160 units, 32 up to 384, else 64. RAGGED: the row's units
-// are not a whole number of every lane's slots.
+// are not a whole number of every lane's slots. x is fp16 (or an activation image, with its row
+// factor in rs); y in dtype odt.
 template <class F>
-static int launch_gemv(const typename F::Args &a, const void *x, void *y, hipStream_t st) {
+static int launch_gemv(const typename F::Args &a, const void *x, void *y, hipStream_t st, int odt = ISHZ_DT_F16,
+                       const float *rs = nullptr) {
   const int units = F::units(a.K);
-  if (units <= 160) return units % 16 ? launch_gemv_k<F, 16, true>(a, x, y, st) : launch_gemv_k<F, 16, false>(a, x, y, st);
-  if (units <= 384) return units % 32 ? launch_gemv_k<F, 32, true>(a, x, y, st) : launch_gemv_k<F, 32, false>(a, x, y, st);
-  return units % 64 ? launch_gemv_k<F, 64, true>(a, x, y, st) : launch_gemv_k<F, 64, false>(a, x, y, st);
+  const Out o{y, odt, rs};
+  if (units <= 160) return units % 16 ? launch_gemv_k<F, 16, true>(a, x, o, st) : launch_gemv_k<F, 16, false>(a, x, o, st);
+  if (units <= 384) return units % 32 ? launch_gemv_k<F, 32, true>(a, x, o, st) : launch_gemv_k<F, 32, false>(a, x, o, st);
+  return units % 64 ? launch_gemv_k<F, 64, true>(a, x, o, st) : launch_gemv_k<F, 64, false>(a, x, o, st);
 }
 
 }  // namespace ishz

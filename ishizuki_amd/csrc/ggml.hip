@@ -45,8 +45,7 @@ DEV void build_iq2xs_tables_nat(u4 *grid, u4 *sgn) { build_iq2xs_tables<false>(g
 // and their partial 16x16 C tiles are summed through LDS at the end.
 template <class F, int T>
 __global__ __launch_bounds__(1024) void verify_kernel(const uint16_t *__restrict__ x, int M, int K,
-                                                      const uint8_t *__restrict__ w, int N,
-                                                      uint16_t *__restrict__ y) {
+                                                      const uint8_t *__restrict__ w, int N, Out y) {
   extern __shared__ __align__(16) uint32_t vsm[];
   const int lane = threadIdx.x & 63, wave = wave_id(), KS = blockDim.x >> 6;
   const int j = lane & 15, g = lane >> 4;
@@ -86,7 +85,7 @@ __global__ __launch_bounds__(1024) void verify_kernel(const uint16_t *__restrict
     float s = 0.0f;
     for (int v = 0; v < KS; v++) s += red[((v * T + t) * 4 + r) * 64 + l];
     const int tk = 4 * (l >> 4) + r, n = n0 + 16 * t + (l & 15);
-    if (tk < M && n < N) y[(size_t)tk * N + n] = f2h(s);
+    if (tk < M && n < N) y.put((size_t)tk * N + n, tk, s);
   }
 }
 
@@ -314,31 +313,31 @@ static int num_cu() {
 int gemv_num_cu() { return num_cu(); }
 
 template <class F>
-static int verify(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st, void *ws = nullptr,
+static int verify(const void *x, int M, int K, const void *w, int N, const Out &y, hipStream_t st, void *ws = nullptr,
                   size_t ws_bytes = 0);
 
 template <class F>
-static int gemv(const void *x, int K, const void *w, int N, void *y, hipStream_t st) {
+static int gemv(const void *x, int K, const void *w, int N, const Out &y, hipStream_t st) {
   if (K % F::GEMV_K_MULT) return verify<F>(x, 1, K, w, N, y, st);
   const typename F::Args a{(const uint8_t *)w, (size_t)(K / F::BS) * F::TS, K, N};
-  return launch_gemv<F>(a, x, y, st);
+  return launch_gemv<F>(a, x, y.y, st, y.dt, y.rs);
 }
 
 template <class F, int T>
-static int launch_verify(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st) {
+static int launch_verify(const void *x, int M, int K, const void *w, int N, const Out &y, hipStream_t st) {
   const int wgs = (N + 16 * T - 1) / (16 * T);
   const int nblk = K / F::BS;
   int ks = 1;
   while (ks < 16 && ks < nblk && wgs * ks < num_cu() * 16) ks *= 2;
   const size_t lds = (F::GRID ? (512 + 128) * 16 : 0) + (size_t)ks * T * 256 * 4;
   hipLaunchKernelGGL((verify_kernel<F, T>), dim3(wgs), dim3(64 * ks), lds, st, (const uint16_t *)x,
-                     M, K, (const uint8_t *)w, N, (uint16_t *)y);
+                     M, K, (const uint8_t *)w, N, y);
   ISHZ_LAUNCH_CHECK("verify launch");
   return ISHZ_OK;
 }
 
 template <class F>
-static int verify(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st, void *ws,
+static int verify(const void *x, int M, int K, const void *w, int N, const Out &y, hipStream_t st, void *ws,
                   size_t ws_bytes) {
   if (M >= 2 && K % 256 == 0) return vgemm<F>(x, M, K, w, N, y, st, ws, ws_bytes);
   if (N >= 4096) return launch_verify<F, 2>(x, M, K, w, N, y, st);
@@ -348,21 +347,20 @@ static int verify(const void *x, int M, int K, const void *w, int N, void *y, hi
 // The quarter-block formats: K is always a multiple of 256 (their block), so M = 1 is the
 // streaming GEMV and M >= 2 the streaming MFMA kernel.
 template <class F>
-static int quarter(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st, void *ws = nullptr,
+static int quarter(const void *x, int M, int K, const void *w, int N, const Out &y, hipStream_t st, void *ws = nullptr,
                    size_t ws_bytes = 0) {
   if (M == 1) {
     const typename F::Args a{(const uint8_t *)w, (size_t)(K / F::BS) * F::TS, K, N};
-    return launch_gemv<F>(a, x, y, st);
+    return launch_gemv<F>(a, x, y.y, st, y.dt, y.rs);
   }
   return vgemm<F>(x, M, K, w, N, y, st, ws, ws_bytes);
 }
 
-__global__ __launch_bounds__(256) void vgemm_sum_kernel(const float *__restrict__ part, int S, size_t n,
-                                                        uint16_t *__restrict__ y) {
+__global__ __launch_bounds__(256) void vgemm_sum_kernel(const float *__restrict__ part, int S, size_t n, int N, Out y) {
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
     float s = 0.0f;
     for (int k = 0; k < S; k++) s += part[(size_t)k * n + i];
-    y[i] = f2h(s);
+    y.put(i, (int)(i / N), s);
   }
 }
 
@@ -370,7 +368,8 @@ static int check_matmul(uint32_t type, int x_dtype, int M, int lo, int hi, int K
                         size_t blocks_bytes, int N, const void *x, const void *w, const void *y) {
   const int bs = block_size(type);
   if (!bs) return decline("unsupported GGML type " + std::to_string(type));
-  if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
+  if (x_dtype != ISHZ_DT_F16 && x_dtype != ISHZ_DT_BF16 && x_dtype != ISHZ_DT_F32)
+    return decline("activations must be fp16, bf16 or fp32");
   if (M < lo || M > hi) return decline("row count outside the kernel's range");
   if (K <= 0 || K % bs) return decline("K is not a whole number of blocks");
   if (N <= 0) return decline("N must be positive");
@@ -386,9 +385,57 @@ using namespace ishz;
 extern "C" int ishz_ggml_block_size(uint32_t type) { return block_size(type); }
 extern "C" int ishz_ggml_type_size(uint32_t type) { return type_size(type); }
 
+// Workspace: the activation image (bf16 / fp32 x), then the K split's fp32 parts.
 extern "C" size_t ishz_ggml_workspace_size(uint32_t type, int M, int K, int N) {
-  if (!block_size(type) || M < 2 || M > 16 || K <= 0 || N <= 0 || K % 256) return 0;
-  return vgemm_workspace(M, K, N, num_cu());
+  if (!block_size(type) || M < 1 || M > 16 || K <= 0 || N <= 0) return 0;
+  return act_image_bytes(M, K) + (K % 256 ? 0 : vgemm_workspace(M, K, N, num_cu()));
+}
+
+// x (any activation dtype) -> fp16 image; then the product with outputs in x's dtype.
+static int ggml_call(uint32_t type, const void *x, int x_dtype, int M, int K, const void *blocks, int N, void *y,
+                     void *workspace, size_t workspace_bytes, hipStream_t st, bool few) {
+  StreamTemp tmp(st);
+  void *img = workspace;
+  size_t left = workspace_bytes;
+  const size_t ib = act_image_bytes(M, K);
+  if (x_dtype != ISHZ_DT_F16) {
+    if (!workspace || workspace_bytes < ib) {  // no room for the image: a temporary of its own
+      int rc = tmp.get(ib);
+      if (rc) return rc;
+      img = tmp.p;
+    } else {
+      workspace = (char *)workspace + ib;
+      left -= ib;
+    }
+  } else if (workspace && workspace_bytes >= ib) {
+    workspace = (char *)workspace + ib;
+    left -= ib;
+  }
+  const uint16_t *xh;
+  const float *rs;
+  int rc = act_prepare(x, x_dtype, M, K, img, st, &xh, &rs);
+  if (rc) return rc;
+  const Out o{y, x_dtype, rs};
+  void *ws = workspace;
+  const size_t wb = ws ? left : 0;
+  if (M == 1 && !few) {
+    switch (type) {
+    case ISHZ_GGML_Q4_0: return gemv<FQ4_0>(xh, K, blocks, N, o, st);
+    case ISHZ_GGML_Q4_K: return gemv<FQ4_K>(xh, K, blocks, N, o, st);
+    case ISHZ_GGML_Q6_K: return gemv<FQ6_K>(xh, K, blocks, N, o, st);
+    case ISHZ_GGML_IQ2_XS: return gemv<FIQ2_XS>(xh, K, blocks, N, o, st);
+    }
+  }
+  switch (type) {
+  case ISHZ_GGML_Q4_0: return verify<FQ4_0>(xh, M, K, blocks, N, o, st, ws, wb);
+  case ISHZ_GGML_Q4_K: return verify<FQ4_K>(xh, M, K, blocks, N, o, st, ws, wb);
+  case ISHZ_GGML_Q6_K: return verify<FQ6_K>(xh, M, K, blocks, N, o, st, ws, wb);
+  case ISHZ_GGML_IQ2_XS: return verify<FIQ2_XS>(xh, M, K, blocks, N, o, st, ws, wb);
+#define X(T, F) case T: return quarter<F>(xh, M, K, blocks, N, o, st, ws, wb);
+    ISHZ_GGML_QUARTER_FORMATS(X)
+#undef X
+  }
+  return decline("unsupported GGML type");
 }
 
 extern "C" int ishz_ggml_matvec_ws(uint32_t type, const void *x, int x_dtype, int M, int K, const void *blocks,
@@ -396,27 +443,7 @@ extern "C" int ishz_ggml_matvec_ws(uint32_t type, const void *x, int x_dtype, in
                                    ishz_stream_t stream) {
   int rc = check_matmul(type, x_dtype, M, 1, 16, K, blocks_bytes, N, x, blocks, y);
   if (rc) return rc;
-  hipStream_t st = S(stream);
-  if (M == 1) {
-    switch (type) {
-    case ISHZ_GGML_Q4_0: return gemv<FQ4_0>(x, K, blocks, N, y, st);
-    case ISHZ_GGML_Q4_K: return gemv<FQ4_K>(x, K, blocks, N, y, st);
-    case ISHZ_GGML_Q6_K: return gemv<FQ6_K>(x, K, blocks, N, y, st);
-    case ISHZ_GGML_IQ2_XS: return gemv<FIQ2_XS>(x, K, blocks, N, y, st);
-    }
-  }
-  void *ws = workspace;
-  const size_t wb = workspace_bytes;
-  switch (type) {
-  case ISHZ_GGML_Q4_0: return verify<FQ4_0>(x, M, K, blocks, N, y, st, ws, wb);
-  case ISHZ_GGML_Q4_K: return verify<FQ4_K>(x, M, K, blocks, N, y, st, ws, wb);
-  case ISHZ_GGML_Q6_K: return verify<FQ6_K>(x, M, K, blocks, N, y, st, ws, wb);
-  case ISHZ_GGML_IQ2_XS: return verify<FIQ2_XS>(x, M, K, blocks, N, y, st, ws, wb);
-#define X(T, F) case T: return quarter<F>(x, M, K, blocks, N, y, st, ws, wb);
-    ISHZ_GGML_QUARTER_FORMATS(X)
-#undef X
-  }
-  return decline("unsupported GGML type");
+  return ggml_call(type, x, x_dtype, M, K, blocks, N, y, workspace, workspace_bytes, S(stream), false);
 }
 
 extern "C" int ishz_ggml_matvec(uint32_t type, const void *x, int x_dtype, int M, int K,
@@ -432,16 +459,7 @@ extern "C" int ishz_ggml_matmul_few(uint32_t type, const void *x, int x_dtype, i
   if (block_size(type) != 256) return decline("matmulFew takes 256-element block types only");
   int rc = check_matmul(type, x_dtype, M, 2, 8, K, blocks_bytes, N, x, blocks, y);
   if (rc) return rc;
-  hipStream_t st = S(stream);
-  switch (type) {
-  case ISHZ_GGML_Q4_K: return verify<FQ4_K>(x, M, K, blocks, N, y, st);
-  case ISHZ_GGML_Q6_K: return verify<FQ6_K>(x, M, K, blocks, N, y, st);
-  case ISHZ_GGML_IQ2_XS: return verify<FIQ2_XS>(x, M, K, blocks, N, y, st);
-#define X(T, F) case T: return quarter<F>(x, M, K, blocks, N, y, st);
-    ISHZ_GGML_QUARTER_FORMATS(X)
-#undef X
-  }
-  return decline("unsupported GGML type");
+  return ggml_call(type, x, x_dtype, M, K, blocks, N, y, nullptr, 0, S(stream), true);
 }
 
 template <uint32_t TYPE, int BS, int TS>

@@ -22,6 +22,45 @@ int einval(const std::string &why) {
   set_error("invalid argument: " + why);
   return ISHZ_EINVAL;
 }
+
+// One workgroup per row: the row's largest magnitude (a max over the block), then every value
+// times 2^-e rounded to fp16.
+__global__ __launch_bounds__(256) void act_half_kernel(const void *__restrict__ x, int dt, int K,
+                                                       uint16_t *__restrict__ xh, float *__restrict__ rs) {
+  __shared__ float wmax[4];
+  const size_t row = (size_t)blockIdx.x * K;
+  float m = 0.0f;
+  for (int k = threadIdx.x; k < K; k += blockDim.x) m = fmaxf(m, fabsf(load_act(x, row + k, dt)));
+  for (int o = 32; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  int e = 0;
+  if (m > 0.0f && m <= 3.0e38f) (void)frexpf(m, &e);  // m = f 2^e, f in [0.5, 1)
+  const float down = ldexpf(1.0f, -e);
+  for (int k = threadIdx.x; k < K; k += blockDim.x) xh[row + k] = f2h(load_act(x, row + k, dt) * down);
+  if (threadIdx.x == 0) rs[blockIdx.x] = ldexpf(1.0f, e);
+}
+
+size_t act_image_bytes(int M, int K) { return ((size_t)M * K * 2 + 255) / 256 * 256 + ((size_t)M * 4 + 255) / 256 * 256; }
+
+int act_prepare(const void *x, int dt, int M, int K, void *image, hipStream_t st, const uint16_t **xh,
+                const float **rs) {
+  if (dt == ISHZ_DT_F16) {
+    *xh = (const uint16_t *)x;
+    *rs = nullptr;
+    return ISHZ_OK;
+  }
+  if (dt != ISHZ_DT_BF16 && dt != ISHZ_DT_F32) return decline("activations must be fp16, bf16 or fp32");
+  if (!image) return einval("bf16 / fp32 activations need a workspace");
+  uint16_t *h = (uint16_t *)image;
+  float *r = (float *)((char *)image + ((size_t)M * K * 2 + 255) / 256 * 256);
+  hipLaunchKernelGGL(act_half_kernel, dim3(M), dim3(256), 0, st, x, dt, K, h, r);
+  ISHZ_LAUNCH_CHECK("activation image launch");
+  *xh = h;
+  *rs = r;
+  return ISHZ_OK;
+}
 }  // namespace ishz
 
 extern "C" const char *ishz_last_error(void) { return ishz::t_last_error.c_str(); }

@@ -241,7 +241,7 @@ struct VPlain {
   const uint8_t *w;
   size_t rb;
   int M, K, N;
-  uint16_t *y;
+  Out y;
   float *part;
   int S;
   struct Group {};
@@ -256,15 +256,14 @@ struct VPlain {
       const int tk = (o >> 4) & 15, row = (tb + (o >> 8)) * 16 + (o & 15);
       if (tk < m && row < N) {
         if (pp) pp[(size_t)(c0 + tk) * N + row] = out[o];
-        else y[(size_t)(c0 + tk) * N + row] = f2h(out[o]);
+        else y.put((size_t)(c0 + tk) * N + row, c0 + tk, out[o]);
       }
     }
   }
 };
 
-// y = the S parts' partial products summed in part order, narrowed once.
-__global__ __launch_bounds__(256) void vgemm_sum_kernel(const float *__restrict__ part, int S, size_t n,
-                                                        uint16_t *__restrict__ y);
+// y = the S parts' partial products summed in part order, narrowed once (rows of N outputs).
+__global__ __launch_bounds__(256) void vgemm_sum_kernel(const float *__restrict__ part, int S, size_t n, int N, Out y);
 
 // K split for long K (>= 32 steps of 256: x no longer fits one workgroup's LDS and is restaged in
 // chunks) and outputs too narrow to give every CU two workgroups' tiles: up to 8 tiles per
@@ -289,7 +288,7 @@ inline size_t vgemm_workspace(int M, int K, int N, int cus) {
 }
 
 template <class F>
-static int vgemm(const void *x, int M, int K, const void *w, int N, void *y, hipStream_t st, void *ws = nullptr,
+static int vgemm(const void *x, int M, int K, const void *w, int N, const Out &y, hipStream_t st, void *ws = nullptr,
                  size_t ws_bytes = 0) {
   int T;
   int S = vgemm_splits(M, K, N, gemv_num_cu(), T);
@@ -297,7 +296,7 @@ static int vgemm(const void *x, int M, int K, const void *w, int N, void *y, hip
     S = 1;
     T = ((N + 15) / 16 + gemv_num_cu() - 1) / gemv_num_cu();
   }
-  const VPlain p{(const uint16_t *)x, (const uint8_t *)w, (size_t)(K / F::BS) * F::TS, M, K, N, (uint16_t *)y,
+  const VPlain p{(const uint16_t *)x, (const uint8_t *)w, (size_t)(K / F::BS) * F::TS, M, K, N, y,
                  S > 1 ? (float *)ws : nullptr, S};
   int rc;
   switch ((M + 3) / 4) {
@@ -309,7 +308,7 @@ static int vgemm(const void *x, int M, int K, const void *w, int N, void *y, hip
   if (rc || S == 1) return rc;
   const size_t n = (size_t)M * N;
   hipLaunchKernelGGL(vgemm_sum_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 2048)), dim3(256), 0, st,
-                     (const float *)ws, S, n, (uint16_t *)y);
+                     (const float *)ws, S, n, N, y);
   ISHZ_LAUNCH_CHECK("vgemm sum launch");
   return ISHZ_OK;
 }

@@ -194,5 +194,5 @@ def test_affine_declines():
     w = torch.zeros((4, 16), dtype=torch.int32, device=DEV)
     s = torch.zeros((4, 8), dtype=torch.float16, device=DEV)
     assert affine.quantized_matmul(x, w, s, s, group_size=32) is None        # group 32
-    assert affine.quantized_matmul(x.float(), w, s, s, group_size=64) is None  # fp32 x
+    assert affine.quantized_matmul(x.to(torch.int16), w, s, s, group_size=64) is None  # integer x
     assert affine.verify_apply(torch.zeros((1, 256), dtype=torch.float16, device=DEV), w, s, s) is None
