@@ -246,7 +246,9 @@ __global__ __launch_bounds__(512) void affine_vgemm(const uint16_t *__restrict__
 
     // ---- stream: this wave's (tile, step) sequence, steps wave, wave + nw, ... of each tile.
     // Load and consume cursors (tile, step) advance in step; loads past the end re-read the
-    // wave's last step (always in range) and are dropped.
+    // wave's last step (always in range) and are dropped. Ring of D steps: the main loop consumes
+    // D steps per pass and loads as many, with no exit in between, so the waits are for the step
+    // being consumed; the last (total % D) steps are already in the ring.
     struct Raw {
       u4 q;
       uint32_t s[2], b[2];
@@ -275,6 +277,7 @@ __global__ __launch_bounds__(512) void affine_vgemm(const uint16_t *__restrict__
     };
     Raw ring[D];
     int lt = tb, lj = wave;
+    const int total = active ? (te - tb) * ((j_last - wave) / nw + 1) : 0;
     if (active) {
 #pragma unroll
       for (int d = 0; d < D - 1; d++) {
@@ -284,60 +287,65 @@ __global__ __launch_bounds__(512) void affine_vgemm(const uint16_t *__restrict__
     }
     float acc[NQ];
     int ct = tb, cj = wave;
-    while (active && ct < te) {
+    auto consume = [&](const Raw &r) {
+      const int tl = ct - tb, j = cj;
+      if (j == wave) {
+#pragma unroll
+        for (int q = 0; q < NQ; q++) acc[q] = accb[((wave * tiles_per_wg + tl) * NQ + q) * 64 + lane];
+      }
+      // B operands: slot r2 of the unit (word r2 / 2, pairs 4 (r2 % 2) .. + 3)
+      u4 B[8];
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const uint32_t w = r.q[t], w10 = w >> 10;
+        B[2 * t] = u4{and_or(w, 0x00030003u, mg), and_or(w, 0x000C000Cu, mg), and_or(w, 0x00300030u, mg),
+                      and_or(w, 0x00C000C0u, mg)};
+        B[2 * t + 1] = u4{and_or(w, 0x03000300u, mg), and_or(w10, 0x00030003u, mg),
+                          and_or(w10, 0x000C000Cu, mg), and_or(w10, 0x00300030u, mg)};
+      }
+      const int ua = 4 * j + gg;  // chunk-relative unit of this lane's A row
+      float sc[4], bi[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint32_t sv = GS == 64 ? (r.s[e >> 1] >> (16 * (e & 1))) : (r.s[0] >> (16 * (e >> 1)));
+        const uint32_t bv = GS == 64 ? (r.b[e >> 1] >> (16 * (e & 1))) : (r.b[0] >> (16 * (e >> 1)));
+        sc[e] = F::ld_s(sv & 0xffffu);
+        bi[e] = F::ld_s(bv & 0xffffu);
+      }
+#pragma unroll
+      for (int q = 0; q < NQ; q++) {
+        const int tka = 4 * q + tt;  // token of this lane's A row
+        const u4 *ab = (gg == G && tka < M) ? vlds + tka * IW + (ua >> 4) * 16 * R + (ua & 15) : zero;
+        f4 C = f4{0, 0, 0, 0};
+#pragma unroll
+        for (int r2 = 0; r2 < 8; r2++) C = mfma32(as_h8(ab[16 * r2]), as_h8(B[r2]), C);
+        // lane (n, G): token 4q + G, units 4j .. 4j + 3 of row n
+        const int tkc = min(4 * q + G, M - 1);
+        const float *sm = (const float *)(vlds + tkc * IW + ugc * 16 * R) + ((4 * j) >> 4) * 32 + ((4 * j) & 15);
+        const f4 off = *(const f4 *)sm, X = *(const f4 *)(sm + 16);
+        float a = acc[q];
+#pragma unroll
+        for (int e = 0; e < 4; e++) a += sc[e] * (C[e] - off[e]) + bi[e] * X[e];
+        acc[q] = a;
+      }
+      if (j == j_last) {
+#pragma unroll
+        for (int q = 0; q < NQ; q++) accb[((wave * tiles_per_wg + tl) * NQ + q) * 64 + lane] = acc[q];
+      }
+      advance(ct, cj);
+    };
+    int c = 0;
+    for (; c + D <= total; c += D) {
 #pragma unroll
       for (int d = 0; d < D; d++) {
         load(lt, lj, ring[(d + D - 1) % D]);
         advance(lt, lj);
-        if (ct >= te) break;
-        const int tl = ct - tb, j = cj;
-        if (j == wave) {
-#pragma unroll
-          for (int q = 0; q < NQ; q++) acc[q] = accb[((wave * tiles_per_wg + tl) * NQ + q) * 64 + lane];
-        }
-        const Raw &r = ring[d];
-        // B operands: slot r2 of the unit (word r2 / 2, pairs 4 (r2 % 2) .. + 3)
-        u4 B[8];
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-          const uint32_t w = r.q[t], w10 = w >> 10;
-          B[2 * t] = u4{and_or(w, 0x00030003u, mg), and_or(w, 0x000C000Cu, mg), and_or(w, 0x00300030u, mg),
-                        and_or(w, 0x00C000C0u, mg)};
-          B[2 * t + 1] = u4{and_or(w, 0x03000300u, mg), and_or(w10, 0x00030003u, mg),
-                            and_or(w10, 0x000C000Cu, mg), and_or(w10, 0x00300030u, mg)};
-        }
-        const int ua = 4 * j + gg;  // chunk-relative unit of this lane's A row
-        float sc[4], bi[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const uint32_t sv = GS == 64 ? (r.s[e >> 1] >> (16 * (e & 1))) : (r.s[0] >> (16 * (e >> 1)));
-          const uint32_t bv = GS == 64 ? (r.b[e >> 1] >> (16 * (e & 1))) : (r.b[0] >> (16 * (e >> 1)));
-          sc[e] = F::ld_s(sv & 0xffffu);
-          bi[e] = F::ld_s(bv & 0xffffu);
-        }
-#pragma unroll
-        for (int q = 0; q < NQ; q++) {
-          const int tka = 4 * q + tt;  // token of this lane's A row
-          const u4 *ab = (gg == G && tka < M) ? vlds + tka * IW + (ua >> 4) * 16 * R + (ua & 15) : zero;
-          f4 C = f4{0, 0, 0, 0};
-#pragma unroll
-          for (int r2 = 0; r2 < 8; r2++) C = mfma32(as_h8(ab[16 * r2]), as_h8(B[r2]), C);
-          // lane (n, G): token 4q + G, units 4j .. 4j + 3 of row n
-          const int tkc = min(4 * q + G, M - 1);
-          const float *sm = (const float *)(vlds + tkc * IW + ugc * 16 * R) + ((4 * j) >> 4) * 32 + ((4 * j) & 15);
-          const f4 off = *(const f4 *)sm, X = *(const f4 *)(sm + 16);
-          float a = acc[q];
-#pragma unroll
-          for (int e = 0; e < 4; e++) a += sc[e] * (C[e] - off[e]) + bi[e] * X[e];
-          acc[q] = a;
-        }
-        if (j == j_last) {
-#pragma unroll
-          for (int q = 0; q < NQ; q++) accb[((wave * tiles_per_wg + tl) * NQ + q) * 64 + lane] = acc[q];
-        }
-        advance(ct, cj);
+        consume(ring[d]);
       }
     }
+#pragma unroll
+    for (int d = 0; d < D - 1; d++)
+      if (c + d < total) consume(ring[d]);
     __syncthreads();  // partials written; x image free for the next chunk
   }
   // ---- sum the waves' partials and write y
@@ -394,7 +402,7 @@ static int affine_vgemm_launch(const void *x, int M, int K, const uint32_t *code
                                const void *biases, int N, const Out &y, hipStream_t st, const float *signs,
                                int block, const u4 *img) {
   using F = FAffine<GS, BF16S>;
-  constexpr int D = 4;
+  constexpr int D = NQ == 1 ? 6 : 4;  // ring depth, measured best per token-quad count on MI355X
   const int ntiles = (N + 15) / 16;
   // tiles per workgroup: one round of CUs, at most 16 / NQ (the waves' per-tile partials live in
   // LDS: a very wide output, such as a vocabulary head, takes several rounds instead)

@@ -75,7 +75,8 @@ __host__ __device__ int gemv_nx(const typename F::Args &a) {
 // value handed to every load(args, prep, row, u) (the gathered-expert formats route their tokens
 // there, so the loads know which expert a row reads). group_align(args, RPW): workgroup row
 // ranges start on multiples of this many row groups. store(args, y, row0, nrows, vals): writes
-// the workgroup's outputs from their final dots in LDS (vals[i] is row row0 + i). X_ALL: every x
+// the workgroup's outputs from their final dots in LDS (vals[i] is row row0 + i), with prepare's
+// value as a sixth argument where the format takes one. X_ALL: every x
 // image is staged (image i at slot i), not only those of the workgroup's rows.
 template <class F>
 __host__ __device__ constexpr bool gemv_has_prepare() {
@@ -237,7 +238,10 @@ __global__ __launch_bounds__(gemv_threads<F>()) void gemv_kernel(typename F::Arg
   }
   if constexpr (gemv_has_store<F>()) {
     __syncthreads();
-    F::store(args, (uint16_t *)out.y, gf * RPW, min(nrows, N - gf * RPW), part);
+    if constexpr (requires { F::store(args, (uint16_t *)out.y, 0, 0, part, prep); })
+      F::store(args, (uint16_t *)out.y, gf * RPW, min(nrows, N - gf * RPW), part, prep);
+    else
+      F::store(args, (uint16_t *)out.y, gf * RPW, min(nrows, N - gf * RPW), part);
   }
 }
 

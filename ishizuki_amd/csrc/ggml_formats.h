@@ -666,12 +666,13 @@ struct FQ6_K : GgmlGemv<FQ6_K> {
 // l < 2, hi otherwise.
 // IQ2_XS sign masks of one ksigns index (7 bits; the eighth sign is their parity) in the GEMV's
 // pair order (x0,x2 | x1,x3 | x4,x6 | x5,x7), sign bits at 15 and 31 of each word, computed in
-// registers instead of read from an LDS table. Word w is s * (2^a + 2^b): the two shifted copies
-// of the 8-bit s occupy disjoint bits, so the product is their OR, and bits 15 and 31 are signs
-// (0, 2), (1, 3), (4, 6), (5, 7); the caller keeps only those bits (mask 0x80008000).
+// registers instead of read from an LDS table. With t = s << 7, word w is t * (2^a + 2^b), a
+// 24-bit by 24-bit product (full-rate v_mul_u32_u24): the two shifted copies of the pattern occupy
+// disjoint bits, so the product is their OR, and bits 15 and 31 are signs (0, 2), (1, 3), (4, 6),
+// (5, 7); the caller keeps only those bits (mask 0x80008000).
 DEV u4 iq2xs_sign_words(uint32_t idx) {
-  const uint32_t s = idx | (__builtin_popcount(idx) & 1u) << 7;
-  return u4{s * 0x20008000u, s * 0x10004000u, s * 0x02000800u, s * 0x01000400u};
+  const uint32_t t = (idx | (__builtin_popcount(idx) & 1u) << 7) << 7;
+  return u4{mul24(t, 0x400100u), mul24(t, 0x200080u), mul24(t, 0x040010u), mul24(t, 0x020008u)};
 }
 
 struct FIQ2_XS : GgmlGemv<FIQ2_XS> {
@@ -684,6 +685,10 @@ struct FIQ2_XS : GgmlGemv<FIQ2_XS> {
   static DEV int slot_k(int u, int r) { return (u >> 2) * 256 + (u & 3) * 64 + 8 * r; }
   static DEV int sum_k(int u, int q) { return 0; }
   static constexpr int SUM_LEN = 16;
+  // sc: the dword ending with the unit's two scale bytes (bits 16..31); d: the dword starting with
+  // the block's fp16 d (bits 0..15). Whole-dword loads: a 2-byte load's zero extension, kept as a
+  // mask on the ring's registers, made the compiler wait for every load in flight at the loop's
+  // back edge.
   struct Raw {
     u4 q;
     uint32_t sc, d;
@@ -691,26 +696,32 @@ struct FIQ2_XS : GgmlGemv<FIQ2_XS> {
   static DEV Raw load_row(const uint8_t *row, int u) {
     const uint8_t *p = row + (size_t)(u >> 2) * TS;
     const int pp = u & 3;
-    return {ld16<2>(p + 2 + 16 * pp), ld2(p + 66 + 2 * pp), ld2(p)};
+    return {ld16<2>(p + 2 + 16 * pp), ld4<2>(p + 64 + 2 * pp), ld4<2>(p)};
   }
   struct LaneC {};
   static DEV LaneC lane(int sub) { return {}; }
   static DEV float dot(const Raw &r, const UnitX &s, const LaneC &) {
-    const float d = h2f(r.d);
+    // entries 2j, 2j + 1 (16 weights) share nibble j of the unit's scale bytes:
+    // d * (0.5 + nib) * 0.25 = (d / 4) * nib + d / 8, exact scalings of d
+    const float d = h2f(r.d & 0xffffu), dq = 0.25f * d, dh = 0.125f * d;
     const u4 QS = r.q;
     float acc = 0.0f;
 #pragma unroll
-    for (int l = 0; l < 8; l++) {
-      const uint32_t q = (QS[l >> 1] >> (16 * (l & 1))) & 0xffffu;
-      const u4 G = s.grid[q & 511], M = iq2xs_sign_words(q >> 9);
-      const u4 X = s.slot(l);
-      constexpr uint32_t SB = 0x80008000u;
-      float e = dot2(G.x ^ (M.x & SB), X.x, 0.0f);
-      e = dot2(G.y ^ (M.y & SB), X.y, e);
-      e = dot2(G.z ^ (M.z & SB), X.z, e);
-      e = dot2(G.w ^ (M.w & SB), X.w, e);
-      const uint32_t nib = (r.sc >> (8 * (l >> 2) + 4 * ((l >> 1) & 1))) & 15;
-      acc += (d * (0.5f + (float)nib) * 0.25f) * e;
+    for (int j = 0; j < 4; j++) {
+      float e = 0.0f;
+#pragma unroll
+      for (int l = 2 * j; l < 2 * j + 2; l++) {
+        const uint32_t q = (QS[j] >> (16 * (l & 1))) & 0xffffu;
+        const u4 G = s.grid[q & 511], M = iq2xs_sign_words(q >> 9);
+        const u4 X = s.slot(l);
+        constexpr uint32_t SB = 0x80008000u;
+        e = dot2(G.x ^ (M.x & SB), X.x, e);
+        e = dot2(G.y ^ (M.y & SB), X.y, e);
+        e = dot2(G.z ^ (M.z & SB), X.z, e);
+        e = dot2(G.w ^ (M.w & SB), X.w, e);
+      }
+      const float nib = (float)__builtin_amdgcn_ubfe(r.sc, 16 + 4 * j, 4);
+      acc = fmaf(fmaf(dq, nib, dh), e, acc);
     }
     return acc;
   }

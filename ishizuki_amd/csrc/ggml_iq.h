@@ -47,12 +47,15 @@ DEV void tab_grid4(const uint32_t *g, int n, u2 *dst) {
   }
 }
 // Sign masks, computed in registers: bit j of the 8-bit pattern s flips the fp16 sign of weight j
-// (natural pair order). Word w is s * (2^(15-2w) + 2^(30-2w)),
-// whose two shifted copies of the 8-bit pattern occupy disjoint bits, so bits 15 and 31 hold signs
-// 2w and 2w + 1; everything else is masked off.
+// (natural pair order). With t = s << 7 (bits 7..14), word w is t * (2^(8-2w) + 2^(23-2w)): both
+// multiplier and t fit 24 bits, so this is one full-rate v_mul_u32_u24 (a 32-bit v_mul_lo_u32 is
+// quarter rate), and the two shifted copies of the pattern occupy disjoint bits, so bits 15 and 31
+// hold signs 2w and 2w + 1; everything else is masked off.
 DEV u4 sign_words(uint32_t s) {
   constexpr uint32_t SB = 0x80008000u;
-  return u4{s * 0x40008000u & SB, s * 0x10002000u & SB, s * 0x04000800u & SB, s * 0x01000200u & SB};
+  const uint32_t t = s << 7;
+  return u4{mul24(t, 0x800100u) & SB, mul24(t, 0x200040u) & SB, mul24(t, 0x080010u) & SB,
+            mul24(t, 0x020004u) & SB};
 }
 DEV uint32_t ksigns_pattern(uint32_t idx) { return idx | (__builtin_popcount(idx) & 1u) << 7; }
 
@@ -276,12 +279,14 @@ struct FIQ2_S : GgmlQuarter<FIQ2_S> {
   static DEV int xk(int g, int r) { return 64 * g + 8 * r; }
   static DEV VRaw vload(const uint8_t *row, int j, int g) {
     const uint8_t *p = row + (size_t)j * TS;
-    return {ld8<2>(p + 2 + 8 * g), ld8<2>(p + 34 + 8 * g), ld2(p + 66 + 2 * g), ld2(p + 74 + 2 * g), ld2(p)};
+    // qh, sc: the dwords ending with the quarter's two bytes (bits 16..31); d: bits 0..15 of the
+    // block's first dword (dword loads: see FIQ2_XS::Raw)
+    return {ld8<2>(p + 2 + 8 * g), ld8<2>(p + 34 + 8 * g), ld4<2>(p + 64 + 2 * g), ld4<2>(p + 72 + 2 * g), ld4<2>(p)};
   }
   static DEV void vdecode(const VRaw &r, u4 *B, uint32_t, const u4 *t, const u4 *) {
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-      const uint32_t qh = byte_of(r.qh, h);
+      const uint32_t qh = byte_of(r.qh, 2 + h);
 #pragma unroll
       for (int l = 0; l < 4; l++) {
         const uint32_t idx = byte_of(r.qs[h], l) | ((qh << (8 - 2 * l)) & 0x300u);
@@ -290,8 +295,8 @@ struct FIQ2_S : GgmlQuarter<FIQ2_S> {
     }
   }
   static DEV void vscale(const VRaw &r, int, int s, float &sc, float &mn) {
-    const uint32_t nib = (r.sc >> (4 * s)) & 15;  // s = 2 h + (l >= 2): byte h, nibble s & 1
-    sc = h2f(r.d) * (0.5f + (float)nib) * 0.25f;
+    const uint32_t nib = (r.sc >> (16 + 4 * s)) & 15;  // s = 2 h + (l >= 2): byte h, nibble s & 1
+    sc = h2f(r.d & 0xffffu) * (0.5f + (float)nib) * 0.25f;
     mn = 0.0f;
   }
 };
@@ -353,14 +358,16 @@ struct FIQ3_S : GgmlQuarter<FIQ3_S> {
   static DEV int xk(int g, int r) { return 64 * g + 8 * r; }
   static DEV VRaw vload(const uint8_t *row, int j, int g) {
     const uint8_t *p = row + (size_t)j * TS;
-    return {ld16<2>(p + 2 + 16 * g), ld8<2>(p + 74 + 8 * g), ld2(p + 66 + 2 * g), (uint32_t)p[106 + g], ld2(p)};
+    // qh: the dword ending with the quarter's two bytes (bits 16..31); sc: the dword ending with its
+    // scale byte (bits 24..31); d: bits 0..15 of the block's first dword (see FIQ2_XS::Raw)
+    return {ld16<2>(p + 2 + 16 * g), ld8<2>(p + 74 + 8 * g), ld4<2>(p + 64 + 2 * g), ld4<1>(p + 103 + g), ld4<2>(p)};
   }
   // Index 2l of sub-block ib takes its 9th bit from bit 2l of qh[ib], index 2l + 1 from bit 2l + 1.
   static DEV void vdecode(const VRaw &r, u4 *B, uint32_t, const u4 *t, const u4 *) {
     const u2 *grid = (const u2 *)t;
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-      const uint32_t qh = byte_of(r.qh, h);
+      const uint32_t qh = byte_of(r.qh, 2 + h);
 #pragma unroll
       for (int l = 0; l < 4; l++) {
         const uint32_t w = r.q[2 * h + (l >> 1)];
@@ -372,7 +379,7 @@ struct FIQ3_S : GgmlQuarter<FIQ3_S> {
     }
   }
   static DEV void vscale(const VRaw &r, int, int s, float &sc, float &mn) {
-    sc = h2f(r.d) * (float)(1 + 2 * (int)((r.sc >> (4 * s)) & 15));
+    sc = h2f(r.d & 0xffffu) * (float)(1 + 2 * (int)((r.sc >> (24 + 4 * s)) & 15));
     mn = 0.0f;
   }
 };

@@ -443,12 +443,24 @@ struct VMoeDown {
 //    w_s fp16(down_s), in fp32 in slot order, plus the shared expert's term, narrowed once
 //    (Text/MoEBlock.swift:143-160).
 typedef __attribute__((address_space(3))) const int32_t lds_i32;
+typedef __attribute__((address_space(3))) const float lds_f32;
 
 struct MoeTokens {
   const float *logits;
   int T, E, normalize;
   MoeRoute R;  // ids / weights (and the caller's copies) written by workgroup 0
 };
+
+// a, or b when c (wave-uniform): a plus an offset that is either zero or b - a. Written as a
+// plain select of two argument fields, the compiler loads the field from the kernel arguments at a
+// computed offset, a memory load every weight batch would then depend on; an offset kept opaque
+// keeps both fields in registers, and a's address space (global loads, not flat).
+template <class T>
+DEV T *pick_ptr(bool c, T *a, T *b) {
+  int64_t d = (const char *)b - (const char *)a;
+  asm("" : "+s"(d));
+  return (T *)((const char *)a + (c ? d : 0));
+}
 
 template <class F>
 struct FMoeGateUp : F {
@@ -502,9 +514,10 @@ struct FMoeGateUp : F {
   static DEV bool is_up(int j) { return (j >> 2) & 1; }
   static DEV int wrow(int j) { return ((j >> 3) << 2) | (j & 3); }
   static DEV const uint8_t *row_ptr(const Args &a, const Prep &pp, int row) {
-    const int p = __builtin_amdgcn_readfirstlane(row) / (2 * a.I);
+    const int r0 = __builtin_amdgcn_readfirstlane(row);  // a batch's rows share pair and gate/up
+    const int p = r0 / (2 * a.I);
     const int e = pp.ids[p], j = row - p * 2 * a.I;
-    return (is_up(j) ? a.up : a.gate) + ((size_t)e * a.I + wrow(j)) * a.rb;
+    return pick_ptr(is_up(r0 - p * 2 * a.I), a.gate, a.up) + ((size_t)e * a.I + wrow(j)) * a.rb;
   }
   static DEV auto load(const Args &a, const Prep &pp, int row, int u) { return F::load_row(row_ptr(a, pp, row), u); }
   static DEV XPre stage_load(const Args &, const uint16_t *, int) { return {}; }
@@ -534,38 +547,68 @@ struct FMoeDown : F {
     const int32_t *ids;  // [T k], from the gate/up launch
     const float *w;      // [T k] routing weights
     const uint16_t *shared, *shared_gate;  // optional: shared expert output [T][H] and gate logit [T]
+    const uint16_t *h;   // [P][I] SwiGLU outputs of the gate/up launch: the x images
   };
   struct XPre {};
+  struct Prep {
+    lds_i32 *ids;  // [P] expert of each pair, in LDS before the first weight load
+    lds_f32 *w;    // [P] routing weight of each pair
+  };
   static int occ(const Args &) { return 2; }
-  static size_t extra_lds_bytes(const Args &) { return F::tab_bytes(); }
+  static size_t extra_lds_bytes(const Args &a) { return F::tab_bytes() + ((size_t)nx(a) * 8 + 15) / 16 * 16; }
   static __host__ __device__ int nx(const Args &a) { return a.N / a.H; }  // pairs
+  static constexpr bool X_ALL = true;  // every pair's h is staged (by prepare), image p at p
+  // The loads of ids and weights go out first, then the staging of every pair's h (which waits
+  // for its own loads); both arrive in the same memory round trip, before the first weight load
+  // (whose rows the ids select) is issued.
+  static DEV Prep prepare(const Args &a, u4 *extra, void *lds_x) {
+    const int P = nx(a), tid = threadIdx.x;
+    int32_t *ids = (int32_t *)((char *)extra + F::tab_bytes());
+    float *w = (float *)(ids + P);
+    int32_t id = 0;
+    float wv = 0.0f;
+    if (tid < P) {
+      id = a.ids[tid];
+      wv = a.w[tid];
+    }
+    u4 *xs = (u4 *)lds_x;
+    const int units = F::units(a.K), ug = (units + 15) / 16;
+    F::stage_images(a.h, a.K, P, xs, (float *)(xs + P * ug * 16 * F::R), units);
+    if (tid < P) {
+      ids[tid] = id;
+      w[tid] = wv;
+    }
+    for (int i = tid + blockDim.x; i < P; i += blockDim.x) {
+      ids[i] = a.ids[i];
+      w[i] = a.w[i];
+    }
+    __syncthreads();
+    return {(lds_i32 *)ids, (lds_f32 *)w};
+  }
   static __host__ __device__ int group_align(const Args &a, int rpw) { return 4 * a.k / rpw; }
   static DEV int pair_of(const Args &a, int row) { return (row / (a.H * a.k)) * a.k + (row >> 2) % a.k; }
   static DEV int out_of(const Args &a, int row) { return ((row >> 2) / a.k % (a.H / 4)) * 4 + (row & 3); }
   static DEV int xsel(const Args &a, int row) { return pair_of(a, row); }
-  static DEV const uint8_t *row_ptr(const Args &a, int row) {
+  static DEV const uint8_t *row_ptr(const Args &a, const Prep &pp, int row) {
     const int r0 = __builtin_amdgcn_readfirstlane(row) & ~3;  // the group's four-row block
-    const int e = a.ids[pair_of(a, r0)];
+    const int e = pp.ids[pair_of(a, r0)];
     return a.down + ((size_t)e * a.H + out_of(a, r0) + (row & 3)) * a.rb;
   }
-  static DEV auto load(const Args &a, int row, int u) { return F::load_row(row_ptr(a, row), u); }
+  static DEV auto load(const Args &a, const Prep &pp, int row, int u) { return F::load_row(row_ptr(a, pp, row), u); }
   static DEV XPre stage_load(const Args &, const uint16_t *, int) { return {}; }
-  // x = the pairs' h [P][I] (the gate/up launch's output)
-  static DEV void stage(const Args &a, const uint16_t *h, u4 *xs, float *xsum, u4 *extra, int units, const XPre &,
-                        int im0, int im1) {
-    F::stage_images(h + (size_t)im0 * a.K, a.K, im1 - im0 + 1, xs, xsum, units);
-    F::gemv_tables(extra);
+  static DEV void stage(const Args &, const uint16_t *, u4 *, float *, u4 *extra, int, const XPre &, int, int) {
+    F::gemv_tables(extra);  // h was staged by prepare
     __syncthreads();
   }
   // rows row0 .. row0 + nrows (whole runs of k four-row blocks): one output per four-row block
   // position, its k slots' fp16 rows weighted in fp32 in slot order, then the shared term.
-  static DEV void store(const Args &a, uint16_t *y, int row0, int nrows, const float *vals) {
+  static DEV void store(const Args &a, uint16_t *y, int row0, int nrows, const float *vals, const Prep &pp) {
     const int run = 4 * a.k;
     for (int q = threadIdx.x; q < nrows / a.k; q += blockDim.x) {
       const int blk = q >> 2, rr = q & 3, j0 = row0 + blk * run;
       const int t = j0 / (a.H * a.k), r = out_of(a, j0) + rr;
       float acc = 0.0f;
-      for (int s = 0; s < a.k; s++) acc += h2f(f2h(vals[blk * run + 4 * s + rr])) * a.w[t * a.k + s];
+      for (int s = 0; s < a.k; s++) acc += h2f(f2h(vals[blk * run + 4 * s + rr])) * pp.w[t * a.k + s];
       if (a.shared) {
         const float sg = r16(1.0f / (1.0f + __expf(-h2f(a.shared_gate[t]))));
         acc += r16(sg * h2f(a.shared[(size_t)t * a.H + r]));
@@ -658,7 +701,7 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
     int rc = launch_gemv<FMoeGateUp<F>>(ga, x, gu, st);
     if (rc) return rc;
     const typename FMoeDown<F>::Args da{(const uint8_t *)down, (size_t)(I / F::BS) * F::TS, I, P * H, H, k,
-                                        R.ids, R.w, shared, shared_gate};
+                                        R.ids, R.w, shared, shared_gate, gu};
     return launch_gemv<FMoeDown<F>>(da, gu, y, st);
   }
   // streaming MFMA kernels from 3 tokens up; one or two tokens (a GEMV per expert) run faster on
@@ -746,9 +789,13 @@ struct FMoeGateUpA : FMoeGateUp<F> {
   using Prep = typename FMoeGateUp<F>::Prep;
   static DEV auto load(const Args &a, const Prep &pp, int row, int u) {
     using B = FMoeGateUp<F>;
-    const int p = __builtin_amdgcn_readfirstlane(row) / (2 * a.I);
+    const int r0 = __builtin_amdgcn_readfirstlane(row);
+    const int p = r0 / (2 * a.I);
     const int e = pp.ids[p], j = row - p * 2 * a.I;
-    return F::load_unit((B::is_up(j) ? a.u : a.g).row((size_t)e * a.I + B::wrow(j)), u);
+    const bool up = B::is_up(r0 - p * 2 * a.I);
+    const AffPack pk{pick_ptr(up, a.g.codes, a.u.codes), pick_ptr(up, a.g.scales, a.u.scales),
+                     pick_ptr(up, a.g.biases, a.u.biases), a.g.wpr, a.g.gpr};
+    return F::load_unit(pk.row((size_t)e * a.I + B::wrow(j)), u);
   }
 };
 template <class F>
@@ -756,9 +803,10 @@ struct FMoeDownA : FMoeDown<F> {
   struct Args : FMoeDown<F>::Args {
     AffPack d;
   };
-  static DEV auto load(const Args &a, int row, int u) {
+  using Prep = typename FMoeDown<F>::Prep;
+  static DEV auto load(const Args &a, const Prep &pp, int row, int u) {
     const int r0 = __builtin_amdgcn_readfirstlane(row) & ~3;
-    const int e = a.ids[FMoeDown<F>::pair_of(a, r0)];
+    const int e = pp.ids[FMoeDown<F>::pair_of(a, r0)];
     return F::load_unit(a.d.row((size_t)e * a.H + FMoeDown<F>::out_of(a, r0) + (row & 3)), u);
   }
 };
@@ -781,7 +829,7 @@ static int moe_ffn_affine(const void *x, int T, int H, int E, int I, int k, cons
     if (rc) return rc;
     typename FMoeDownA<F>::Args da{};
     static_cast<typename FMoeDown<F>::Args &>(da) =
-        typename FMoeDown<F>::Args{nullptr, 0, I, P * H, H, k, R.ids, R.w, shared, shared_gate};
+        typename FMoeDown<F>::Args{nullptr, 0, I, P * H, H, k, R.ids, R.w, shared, shared_gate, gu};
     da.d = down;
     return launch_gemv<FMoeDownA<F>>(da, gu, y, st);
   }

@@ -1,5 +1,6 @@
 """The i-quant GEMV and verify decoders build fp16 sign-bit masks in registers by one multiply per
-word (sign_words in csrc/ggml_iq.h, iq2xs_sign_words in csrc/ggml_formats.h). For every sign
+word (sign_words in csrc/ggml_iq.h, iq2xs_sign_words in csrc/ggml_formats.h): the pattern shifted
+left by 7 times a constant, both within 24 bits (v_mul_u32_u24). For every sign
 pattern, the multiplied words must put sign bit j of the pattern on exactly the fp16 weight the
 decoder pairs it with: natural order (w0,w1 | w2,w3 | ...) for sign_words, the GEMV's permuted
 order (x0,x2 | x1,x3 | x4,x6 | x5,x7) for IQ2_XS. ksigns patterns carry their parity as bit 7
@@ -14,11 +15,18 @@ def _multipliers(fname, func):
     src = open(os.path.join(CSRC, fname)).read()
     body = src[src.index(func):]
     body = body[:body.index("}")]
-    return [int(m, 16) for m in re.findall(r"s \* (0x[0-9A-Fa-f]+)u", body)]
+    assert "<< 7" in body
+    return [int(m, 16) for m in re.findall(r"mul24\(t, (0x[0-9A-Fa-f]+)u\)", body)]
 
 
 def _masks(mults, s):
-    return [(s * m) & 0x80008000 & 0xFFFFFFFF for m in mults]
+    t = s << 7
+    assert t < 1 << 24
+    out = []
+    for m in mults:
+        assert m < 1 << 24  # a 24-bit operand: the product is exact in 48 bits, low 32 kept
+        out.append((t * m) & 0x80008000 & 0xFFFFFFFF)
+    return out
 
 
 def _expect(s, order):
