@@ -595,9 +595,11 @@ extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, cons
     return affine_dispatch(x, M, K, signs, block, codes, scales, biases, bf16s, N, group, o, st);
   if (block <= 128 && K % 256 == 0) {
     // x rotated and staged once into the workspace (every token's image), else the rotation is
-    // fused into each workgroup's staging
+    // fused into each workgroup's staging; two tokens rotate faster in the workgroups than the
+    // extra launch costs (measured on MI355X at 17408x5120: 14.3 vs 15.3 us; from four tokens up
+    // the prestaged image wins)
     const u4 *img = nullptr;
-    if (workspace && workspace_bytes >= ishz_affine_workspace_size(M, K)) {
+    if (M > 2 && workspace && workspace_bytes >= ishz_affine_workspace_size(M, K)) {
       const FAffine<64, false>::Args a{codes, nullptr, nullptr, signs, block, K, N};
       hipLaunchKernelGGL(affine_prestage_kernel, dim3((K + 511) / 512, M), dim3(64), 0, st, a, (const uint16_t *)x,
                          (u4 *)workspace);
