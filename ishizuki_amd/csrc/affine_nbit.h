@@ -67,7 +67,7 @@ struct FAffineN : GgmlGemv<FAffineN<BITS, GS, BF16S>> {
   };
   static constexpr int WPU = 64 * BITS / 32;  // code words per 64-weight unit
   static constexpr int BS = 64, UPB = 1, UNIT_BLOCKS = 1;
-  static constexpr int RING = 5;
+  static constexpr int RING = 3;  // as FAffine::RING
   static constexpr int R = 8, Q = 2, SUM_LEN = 32;
   static constexpr bool XSUM = true, GRID = false, VGRID = false, XPERM = BITS == 8;
   static constexpr bool MASKED = BITS == 4 || BITS == 8;  // whole codes per word: masked in place

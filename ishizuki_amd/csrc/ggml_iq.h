@@ -63,7 +63,6 @@ DEV uint32_t ksigns_pattern(uint32_t idx) { return idx | (__builtin_popcount(idx
 template <class D>
 struct GgmlQuarter : GgmlGemv<D> {
   static constexpr int BS = 256, UPB = 4, UNIT_BLOCKS = 1, GEMV_K_MULT = 256;
-  static constexpr int RING = 5;
   static constexpr bool GRID = false, VGRID = false;
   static constexpr int R = 8;
   static DEV int slot_k(int u, int r) { return (u >> 2) * 256 + D::xk(u & 3, r); }
