@@ -155,7 +155,7 @@ struct FAffineN : GgmlGemv<FAffineN<BITS, GS, BF16S>> {
 
   // Streaming MFMA verify: quarter g of step j is unit 4j + g of the chunk; one scale group per
   // quarter (VNS = 1, eight MFMAs).
-  static constexpr int VNS = 1, VSTEP_BYTES = 0, VDEPTH = BITS <= 4 ? 3 : 2;
+  static constexpr int VNS = 1, VSTEP_BYTES = 0, VDEPTH = 2;
   typedef Raw VRaw;
   // Any problem whose rows are affine rows: P::arow(group, row) or, with one group, P::arow(row).
   template <class P>

@@ -60,6 +60,9 @@ struct GgmlGemv {
   // beats three to five for every GGUF format by 6-11 % (a deeper ring unrolls more copies of the
   // decode loop body and issues more of a short wave's work before its first consume)
   static constexpr int RING = 2;
+  // Streaming-verify ring depth: two, measured best for every GGUF format at 17408x5120, M = 8
+  // (4-10 % faster than three to six)
+  static constexpr int VDEPTH = 2;
   // Resident waves per SIMD the grid is sized for: two measured best on MI355X at 17408x5120
   // (fewer, longer waves amortise the x staging every workgroup repeats).
   static int occ(const Args &) { return 2; }
@@ -281,7 +284,7 @@ struct FQ4_0 : GgmlGemv<FQ4_0> {
   // Streaming verify: a lane's quarter of a 256-weight step is its GEMV unit (blocks 8j + 2g,
   // 8j + 2g + 1); sub-units (block, low / high nibbles), two MFMAs each. High nibbles decode to
   // 1024 + 16q, so their scale carries the 1/16.
-  static constexpr int VNS = 4, VSTEP_BYTES = 8 * TS, VDEPTH = 4;
+  static constexpr int VNS = 4, VSTEP_BYTES = 8 * TS;
   static constexpr bool VGRID = false;
   typedef Raw VRaw;
   static DEV VRaw vload(const uint8_t *row, int j, int g) { return load_row(row + (size_t)j * VSTEP_BYTES, g); }
@@ -413,7 +416,7 @@ struct FQ4_K : GgmlGemv<FQ4_K> {
 
   // Streaming verify: step = one super-block; a lane's quarter is chunk g (32 bytes of qs):
   // sub-unit 0 = sub-block 2g (low nibbles), 1 = sub-block 2g + 1 (high, 1024 + 16q).
-  static constexpr int VNS = 2, VSTEP_BYTES = TS, VDEPTH = 4;
+  static constexpr int VNS = 2, VSTEP_BYTES = TS;
   static constexpr bool VGRID = false;
   struct VRaw {
     u4 h, q0, q1;
@@ -568,7 +571,7 @@ struct FQ6_K : GgmlGemv<FQ6_K> {
   // Streaming verify: step = one super-block; lane group g takes half n = g / 2, l in
   // 16 (g % 2) .. + 15: sub-unit qq (scale sc[8n + g % 2 + 2qq]) = weights 128n + 32qq + l, two
   // MFMAs (l halves). Codes decode to 1024 + q (q = 0..63) from a nibble of ql and two bits of qh.
-  static constexpr int VNS = 4, VSTEP_BYTES = TS, VDEPTH = 2;
+  static constexpr int VNS = 4, VSTEP_BYTES = TS;
   static constexpr bool VGRID = false;
   struct VRaw {
     u4 ql0, ql1, qh, sc;
@@ -765,7 +768,7 @@ struct FIQ2_XS : GgmlGemv<FIQ2_XS> {
   // Streaming verify: step = one super-block; lane group g takes groups 2g, 2g + 1 (entries
   // e = 0..7, 8 weights each, one MFMA each); sub-unit e / 2 shares one 4-bit scale. B is the
   // grid entry with its signs (exact small integers in fp16); A is x in natural order.
-  static constexpr int VNS = 4, VSTEP_BYTES = TS, VDEPTH = 4;
+  static constexpr int VNS = 4, VSTEP_BYTES = TS;
   static constexpr bool VGRID = true;
   struct VRaw {
     u4 q;

@@ -148,7 +148,7 @@ struct FQ2_K : GgmlQuarter<FQ2_K> {
     uint32_t dd;
   };
   ISHZ_QUARTER_COMMON(FQ2_K, ISHZ_GGML_Q2_K, 84)
-  static constexpr int VNS = 4, VDEPTH = 4, Q = 4, SUM_LEN = 16;
+  static constexpr int VNS = 4, Q = 4, SUM_LEN = 16;
   static constexpr bool XSUM = true, XPERM = true;
   static constexpr float OFF = 1024.0f;
   static constexpr size_t TAB_BYTES = 0;
@@ -189,7 +189,7 @@ struct FIQ4_XS : GgmlQuarter<FIQ4_XS> {
     uint32_t hd, sl;
   };
   ISHZ_QUARTER_COMMON(FIQ4_XS, ISHZ_GGML_IQ4_XS, 136)
-  static constexpr int VNS = 2, VDEPTH = 3, Q = 1, SUM_LEN = 32;
+  static constexpr int VNS = 2, Q = 1, SUM_LEN = 32;
   static constexpr bool XSUM = false, XPERM = false;
   static constexpr float OFF = 0.0f;
   static constexpr size_t TAB_BYTES = 256 * 4;
@@ -242,7 +242,7 @@ struct FIQ2_XXS : GgmlQuarter<FIQ2_XXS> {
     uint32_t d;
   };
   ISHZ_QUARTER_COMMON(FIQ2_XXS, ISHZ_GGML_IQ2_XXS, 66)
-  static constexpr int VNS = 2, VDEPTH = 4, Q = 1, SUM_LEN = 32;
+  static constexpr int VNS = 2, Q = 1, SUM_LEN = 32;
   static constexpr bool XSUM = false, XPERM = false;
   static constexpr float OFF = 0.0f;
   static constexpr size_t TAB_BYTES = 256 * 16;
@@ -275,7 +275,7 @@ struct FIQ2_S : GgmlQuarter<FIQ2_S> {
     uint32_t qh, sc, d;
   };
   ISHZ_QUARTER_COMMON(FIQ2_S, ISHZ_GGML_IQ2_S, 82)
-  static constexpr int VNS = 4, VDEPTH = 3, Q = 1, SUM_LEN = 16;
+  static constexpr int VNS = 4, Q = 1, SUM_LEN = 16;
   static constexpr bool XSUM = false, XPERM = false;
   static constexpr float OFF = 0.0f;
   static constexpr size_t TAB_BYTES = 1024 * 16;
@@ -316,7 +316,7 @@ struct FIQ3_XXS : GgmlQuarter<FIQ3_XXS> {
     uint32_t d;
   };
   ISHZ_QUARTER_COMMON(FIQ3_XXS, ISHZ_GGML_IQ3_XXS, 98)
-  static constexpr int VNS = 2, VDEPTH = 3, Q = 1, SUM_LEN = 32;
+  static constexpr int VNS = 2, Q = 1, SUM_LEN = 32;
   static constexpr bool XSUM = false, XPERM = false;
   static constexpr float OFF = 0.0f;
   static constexpr size_t TAB_BYTES = 256 * 8;
@@ -354,7 +354,7 @@ struct FIQ3_S : GgmlQuarter<FIQ3_S> {
     uint32_t qh, sc, d;
   };
   ISHZ_QUARTER_COMMON(FIQ3_S, ISHZ_GGML_IQ3_S, 110)
-  static constexpr int VNS = 2, VDEPTH = 3, Q = 1, SUM_LEN = 32;
+  static constexpr int VNS = 2, Q = 1, SUM_LEN = 32;
   static constexpr bool XSUM = false, XPERM = false;
   static constexpr float OFF = 0.0f;
   static constexpr size_t TAB_BYTES = 512 * 8;
@@ -399,7 +399,7 @@ struct FIQ1_S : GgmlQuarter<FIQ1_S> {
     uint32_t qh, d;
   };
   ISHZ_QUARTER_COMMON(FIQ1_S, ISHZ_GGML_IQ1_S, 50)
-  static constexpr int VNS = 2, VDEPTH = 4, Q = 2, SUM_LEN = 32;
+  static constexpr int VNS = 2, Q = 2, SUM_LEN = 32;
   static constexpr bool XSUM = true, XPERM = false;
   static constexpr float OFF = 0.0f;
   static constexpr size_t TAB_BYTES = 2048 * 16;
@@ -434,7 +434,7 @@ struct FIQ1_M : GgmlQuarter<FIQ1_M> {
     u2 sc;
   };
   ISHZ_QUARTER_COMMON(FIQ1_M, ISHZ_GGML_IQ1_M, 56)
-  static constexpr int VNS = 8, VDEPTH = 4, Q = 8, SUM_LEN = 8;
+  static constexpr int VNS = 8, Q = 8, SUM_LEN = 8;
   static constexpr bool XSUM = true, XPERM = false;
   static constexpr float OFF = 0.0f;
   static constexpr size_t TAB_BYTES = 2048 * 16;
