@@ -97,15 +97,19 @@ __host__ __device__ int gemv_align(const typename F::Args &a, int rpw) {
 }
 
 // Threads per workgroup: F::WG where the format sets it (the workgroup shares one staged copy of
-// x, so a larger one stages fewer copies, each with more waves), else 256.
-template <class F>
+// x, so a larger one stages fewer copies, each with more waves), else 256; rows of more than 384
+// units (64 lanes per row, K above 24576 for 64-weight units) take 1024, one workgroup per CU: x
+// is then 50 KB and more, and staging it once per CU instead of two to four times measured 10-14 %
+// faster at K = 25600 (Q4_K, Q6_K, IQ2_XS, N = 5120) on MI355X.
+template <class F, int LPR = 16>
 __host__ __device__ constexpr int gemv_threads() {
-  if constexpr (requires { F::WG; }) return F::WG;
+  if constexpr (LPR >= 64) return 1024;
+  else if constexpr (requires { F::WG; }) return F::WG;
   else return 256;
 }
 
 template <class F, int LPR, int D, bool RAGGED>
-__global__ __launch_bounds__(gemv_threads<F>()) void gemv_kernel(typename F::Args args, const uint16_t *__restrict__ x,
+__global__ __launch_bounds__((gemv_threads<F, LPR>())) void gemv_kernel(typename F::Args args, const uint16_t *__restrict__ x,
                                                    Out out, int nwg, int part_off) {
   static_assert(LPR % 16 == 0, "lanes per row must be a multiple of 16");
   extern __shared__ __align__(16) uint32_t smem[];
@@ -118,7 +122,7 @@ __global__ __launch_bounds__(gemv_threads<F>()) void gemv_kernel(typename F::Arg
   u4 *extra = (u4 *)(xsum + nx * ugroups * 16 * F::Q);  // format tables / scratch
   float *part = (float *)((char *)smem + part_off);      // [wave][row of the workgroup] partial dots
 
-  constexpr int RPW = 64 / LPR, WPG = gemv_threads<F>() / 64;
+  constexpr int RPW = 64 / LPR, WPG = gemv_threads<F, LPR>() / 64;
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int sub = lane % LPR, rg = lane / LPR;
   const int upl = (units + LPR - 1) / LPR;  // units per lane per row
@@ -253,7 +257,7 @@ int gemv_num_cu();
 template <class F, int LPR, bool RAGGED>
 static int launch_gemv_k(const typename F::Args &a, const void *x, const Out &o, hipStream_t st) {
   constexpr int RPW = 64 / LPR;
-  constexpr int NT = gemv_threads<F>(), WPG = NT / 64;
+  constexpr int NT = gemv_threads<F, LPR>(), WPG = NT / 64;
   const int units = F::units(a.K);
   const size_t ug = (size_t)(units + 15) / 16;
   const size_t xlds = gemv_nx<F>(a) * (ug * 16 * F::R * 16 + ug * 16 * F::Q * 4) + F::extra_lds_bytes(a);
