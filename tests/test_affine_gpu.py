@@ -69,6 +69,35 @@ def test_affine_matmul(M, group):
     assert_close(y.float().cpu().numpy(), ref, bound=bd, what=f"affine M={M} g={group}")
 
 
+@pytest.mark.parametrize("group", [64, 128])
+@pytest.mark.parametrize("block", [0, 128])
+def test_affine_long_k_gemv(group, block):
+    """K = 25600, M = 1: 400 units per row take 64 lanes per row and 1024-thread workgroups,
+    whose sixteen waves stage (and rotate) x."""
+    N, K = 200, 25600
+    (x, w, s, b), signs, (ref, bd) = affine_case(N, K, 1, group, seed=41 + block, block=block, signs_seed=3)
+    if block:
+        y = affine.linear(x, w, s, b, signs=torch.from_numpy(signs), block=block, group_size=group)
+    else:
+        y = affine.quantized_matmul(x, w, s, b, group_size=group)
+    assert y is not None
+    assert_close(y.float().cpu().numpy(), ref, bound=bd, what=f"affine long K g={group} block={block}")
+
+
+@pytest.mark.parametrize("bits", [4, 3])
+def test_affine_wide_bits_long_k_gemv(bits):
+    N, K = 96, 25600
+    codes, s, b = synth.affine_pack_bits(N, K, bits, group=64, seed=bits + 50)
+    x = synth.fp16_normal((1, K), seed=bits + 51)
+    xf = x.astype(np.float32)
+    ref = oracle.affine_matmul(xf, codes, s.view(np.uint16), b.view(np.uint16), N, bits, 64)
+    bd = affine_bound(xf, codes, s, b, N, K, bits, 64)
+    dev = lambda a: torch.from_numpy(a).to(DEV)
+    y = affine.quantized_matmul(dev(x), dev(codes.view(np.int32)), dev(s), dev(b), group_size=64, bits=bits)
+    assert y is not None
+    assert_close(y.float().cpu().numpy(), ref, bound=bd, what=f"affine {bits}-bit long K")
+
+
 @pytest.mark.parametrize("bits", [3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("M", [1, 2, 5, 8, 16])
 @pytest.mark.parametrize("group,bf16", [(64, False), (128, True)])

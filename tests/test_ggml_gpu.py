@@ -89,6 +89,16 @@ def test_gemv_wide_lanes():
 
 
 @pytest.mark.parametrize("t", TYPES)
+def test_gemv_long_k(t):
+    """K = 25600, M = 1: 400 units per row, so 64 lanes per row (ragged) and 1024-thread
+    workgroups; N not a multiple of the workgroup's rows."""
+    N, K = 130, 25600
+    print(f"gemv long K type={t}", flush=True)
+    y, ref, bd = run_matvec(t, 1, N, K, seed=31 + t)
+    assert_close(y, ref, bound=bd, what=f"gemv long K t={t}")
+
+
+@pytest.mark.parametrize("t", TYPES)
 @pytest.mark.parametrize("M", [2, 3, 5, 8, 16])
 def test_verify_rows(t, M):
     N, K = 4100, 1024   # N >= 4096: two tiles per workgroup, ragged last tile
