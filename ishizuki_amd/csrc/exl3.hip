@@ -647,7 +647,6 @@ static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis
     if constexpr (!HALF && (KA == 1 || KA == 2 || KA == 4)) {
       constexpr int TN = 32 / KA, KS3 = 4, D = 4;  // a step covers TN column tiles: N must tile by them
       if ((N / 16) % TN == 0) {
-        if (suh && M != 1) return einval("the fused input rotation is for one row");
         const int tn_blocks = N / 16 / TN;
         const int per = (tiles_k + exl3_splits(M, K, tn_blocks) - 1) / exl3_splits(M, K, tn_blocks);
         const int nsplit = (tiles_k + per - 1) / per;
@@ -666,6 +665,9 @@ static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis
           else if (M == 1)
             hipLaunchKernelGGL((exl3_mm3<KA, CB, false, D>), dim3(tn_blocks, nsplit), dim3(64 * KS3), lds, st,
                                (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per, part ? 1 : 0);
+          else if (suh)
+            hipLaunchKernelGGL((exl3_mm3<KA, CB, true, D, true>), dim3(tn_blocks, nsplit), dim3(64 * KS3), lds, st,
+                               (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per, part ? 1 : 0, suh);
           else
             hipLaunchKernelGGL((exl3_mm3<KA, CB, true, D>), dim3(tn_blocks, nsplit), dim3(64 * KS3), lds, st,
                                (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per, part ? 1 : 0);
@@ -741,7 +743,10 @@ extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const
 // 2 bpw: 37.8 us against 34.7 us for the separate rotation launch).
 static bool exl3_fused_rotation(int M, int K, int N, int bits2) {
   const int KA = bits2 / 2;
-  if (M != 1 || !(bits2 == 2 || bits2 == 4 || bits2 == 8) || (N / 16) % (32 / KA)) return false;
+  // up to two rows: every workgroup rotates its K range of every row, which measured faster than
+  // the separate rotation launch at M = 1 and 2 (17408x5120: 32.7 vs 33.7 us at M = 2), even at 4
+  // and slower at 8 (38.0 vs 35.3)
+  if (M > 2 || !(bits2 == 2 || bits2 == 4 || bits2 == 8) || (N / 16) % (32 / KA)) return false;
   const int TN = 32 / KA, tiles_k = K / 16, splits = exl3_splits(M, K, N / 16 / TN);
   const size_t per = (tiles_k + splits - 1) / splits;
   const size_t own = 4 * 256 * 4 + (M == 1 ? (size_t)4 * TN * 16 * 4 : (size_t)TN * 256 * 4);
