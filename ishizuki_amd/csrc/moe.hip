@@ -707,12 +707,15 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
   // streaming MFMA kernels from 3 tokens up; one or two tokens (a GEMV per expert) run faster on
   // the per-block kernels below, which start streaming without staging x
   if (H % 256 == 0 && I % 256 == 0 && T > 2) {
-    // tiles per workgroup: about two workgroups per CU over the routed experts (gate/up: an even
-    // count, whole SwiGLU pairs); with 8 or more a wave takes whole tiles
+    // tiles per workgroup: about two workgroups per CU over the routed experts, one when they hold
+    // two tokens or fewer each (measured at the Qwen shape: T = 8, 1.2 tokens per expert, 65.6 ->
+    // 60.7 us with one; T = 64, 4 per expert, 134 -> 153 us); gate/up: an even count, whole SwiGLU
+    // pairs; with 8 or more a wave takes whole tiles
     const int tiles_gu = 2 * ((I + 15) / 16), tiles_dn = (H + 15) / 16;
     const int act = std::min(amax, 128);
+    const int per_cu = T * k <= 2 * act ? 1 : 2;
     auto pick = [&](int tiles, int even) {
-      int t = std::max(1, std::min(32, tiles * act / (gemv_num_cu() * 2)));
+      int t = std::max(1, std::min(32, tiles * act / (gemv_num_cu() * per_cu)));
       if (even) t = std::max(2, t & ~1);
       return t;
     };
@@ -835,7 +838,7 @@ static int moe_ffn_affine(const void *x, int T, int H, int E, int I, int k, cons
   }
   const int tiles_gu = 2 * ((I + 15) / 16), tiles_dn = (H + 15) / 16;
   const int act = std::min(amax, 128);
-  auto pick = [&](int tiles, int even) {
+  auto pick = [&](int tiles, int even) {  // two workgroups per CU (one measured slower here)
     int t = std::max(1, std::min(32, tiles * act / (gemv_num_cu() * 2)));
     if (even) t = std::max(2, t & ~1);
     return t;
