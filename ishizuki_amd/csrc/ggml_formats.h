@@ -663,6 +663,19 @@ struct FQ6_K : GgmlGemv<FQ6_K> {
   }
 };
 
+// Sign masks, computed in registers: bit j of the 8-bit pattern s flips the fp16 sign of weight j
+// (natural pair order). With t = s << 7 (bits 7..14), word w is t * (2^(8-2w) + 2^(23-2w)): both
+// multiplier and t fit 24 bits, so this is one full-rate v_mul_u32_u24 (a 32-bit v_mul_lo_u32 is
+// quarter rate), and the two shifted copies of the pattern occupy disjoint bits, so bits 15 and 31
+// hold signs 2w and 2w + 1; everything else is masked off.
+DEV u4 sign_words(uint32_t s) {
+  constexpr uint32_t SB = 0x80008000u;
+  const uint32_t t = s << 7;
+  return u4{mul24(t, 0x800100u) & SB, mul24(t, 0x200040u) & SB, mul24(t, 0x080010u) & SB,
+            mul24(t, 0x020004u) & SB};
+}
+DEV uint32_t ksigns_pattern(uint32_t idx) { return idx | (__builtin_popcount(idx) & 1u) << 7; }
+
 // ----------------------------------------------------------------------------------- IQ2_XS
 // GGMLDequant.iq2XS (Core/GGMLDequant.swift:264-285): fp16 d at 0, qs u16[32] at 2 (9-bit grid
 // index, 7-bit sign index), scales u8[8] at 66. Entry l of group ib (weights 32ib + 8l + j) is
@@ -778,11 +791,13 @@ struct FIQ2_XS : GgmlGemv<FIQ2_XS> {
     const uint8_t *p = row + (size_t)j * TS;
     return {ld16<2>(p + 2 + 16 * g), ld2(p + 66 + 2 * g), ld2(p)};
   }
-  static DEV void vdecode(const VRaw &r, u4 *B, uint32_t, const u4 *grid, const u4 *sgn) {
+  // signs from registers (sign_words) rather than the LDS table: one random LDS read fewer per
+  // eight weights, 2-3 % faster at 17408x5120, M = 8
+  static DEV void vdecode(const VRaw &r, u4 *B, uint32_t, const u4 *grid, const u4 *) {
 #pragma unroll
     for (int e = 0; e < 8; e++) {
       const uint32_t q = (r.q[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-      B[e] = grid[q & 511] ^ sgn[q >> 9];
+      B[e] = grid[q & 511] ^ sign_words(ksigns_pattern(q >> 9));
     }
   }
   static DEV void vstage(const uint16_t *x, int j, int g, int s, u4 *A, float &off1, float &X) {

@@ -46,18 +46,6 @@ DEV void tab_grid4(const uint32_t *g, int n, u2 *dst) {
     dst[e] = u2{h[0] | h[1] << 16, h[2] | h[3] << 16};
   }
 }
-// Sign masks, computed in registers: bit j of the 8-bit pattern s flips the fp16 sign of weight j
-// (natural pair order). With t = s << 7 (bits 7..14), word w is t * (2^(8-2w) + 2^(23-2w)): both
-// multiplier and t fit 24 bits, so this is one full-rate v_mul_u32_u24 (a 32-bit v_mul_lo_u32 is
-// quarter rate), and the two shifted copies of the pattern occupy disjoint bits, so bits 15 and 31
-// hold signs 2w and 2w + 1; everything else is masked off.
-DEV u4 sign_words(uint32_t s) {
-  constexpr uint32_t SB = 0x80008000u;
-  const uint32_t t = s << 7;
-  return u4{mul24(t, 0x800100u) & SB, mul24(t, 0x200040u) & SB, mul24(t, 0x080010u) & SB,
-            mul24(t, 0x020004u) & SB};
-}
-DEV uint32_t ksigns_pattern(uint32_t idx) { return idx | (__builtin_popcount(idx) & 1u) << 7; }
 
 // ------------------------------------------------------------------------- shared base
 template <class D>

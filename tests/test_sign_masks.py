@@ -1,5 +1,5 @@
 """The i-quant GEMV and verify decoders build fp16 sign-bit masks in registers by one multiply per
-word (sign_words in csrc/ggml_iq.h, iq2xs_sign_words in csrc/ggml_formats.h): the pattern shifted
+word (sign_words and iq2xs_sign_words in csrc/ggml_formats.h): the pattern shifted
 left by 7 times a constant, both within 24 bits (v_mul_u32_u24). For every sign
 pattern, the multiplied words must put sign bit j of the pattern on exactly the fp16 weight the
 decoder pairs it with: natural order (w0,w1 | w2,w3 | ...) for sign_words, the GEMV's permuted
@@ -37,7 +37,7 @@ def _expect(s, order):
 
 
 def test_sign_words_natural_order_all_patterns():
-    mults = _multipliers("ggml_iq.h", "DEV u4 sign_words(uint32_t s)")
+    mults = _multipliers("ggml_formats.h", "DEV u4 sign_words(uint32_t s)")
     assert len(mults) == 4
     for s in range(256):
         assert _masks(mults, s) == _expect(s, [(0, 1), (2, 3), (4, 5), (6, 7)]), s
