@@ -66,9 +66,10 @@ def verify_apply(x, weight, scales, biases, group_size=64, bits=2):
 def linear(x, weight, scales, biases, signs=None, block=0, group_size=64, bits=2, _prestage=True):
     """Rotated PackedLinear forward: rotate (fused for one row) then the quantized matmul.
 
-    With block <= 128 the workspace holds every row's x rotated and staged once for all
-    workgroups; `_prestage=False` passes none, so each workgroup rotates x itself (test hook; the
-    general path for other blocks needs the workspace)."""
+    With block <= 128 and more than two rows the workspace holds every row's x rotated and staged
+    once for all workgroups (with one or two rows each workgroup rotates x itself, which measured
+    faster); `_prestage=False` passes none, so each workgroup rotates x itself at any row count
+    (test hook; the general path for other blocks needs the workspace)."""
     require_cuda(x, weight, scales, biases)
     x = x.contiguous()
     M, K = x.shape
