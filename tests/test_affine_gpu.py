@@ -169,6 +169,26 @@ def test_affine_rotated_linear(M, signs_seed):
     assert_close(y.float().cpu().numpy(), ref, bound=bd, what=f"rotated M={M}")
 
 
+def _random_affine_cases(n, seed):
+    """Seeded 2-bit shapes: N from 1 to 2499, K any multiple of 128 up to 8192, M from 1 to 8,
+    groups of 64 and 128, unrotated or rotated in blocks of 64 or 128."""
+    r = np.random.default_rng(seed)
+    return [(int(r.integers(1, 2500)), 128 * int(r.integers(1, 65)), int(r.integers(1, 9)), (64, 128)[i % 2],
+             (0, 64, 128)[i % 3]) for i in range(n)]
+
+
+@pytest.mark.parametrize("N,K,M,group,block", _random_affine_cases(24, 2025))
+def test_affine_random_shapes(N, K, M, group, block):
+    print(f"affine random N={N} K={K} M={M} g={group} block={block}", flush=True)
+    (x, w, s, b), signs, (ref, bd) = affine_case(N, K, M, group, seed=N + K, block=block, signs_seed=K)
+    if block:
+        y = affine.linear(x, w, s, b, signs=torch.from_numpy(signs), block=block, group_size=group)
+    else:
+        y = affine.quantized_matmul(x, w, s, b, group_size=group)
+    assert y is not None
+    assert_close(y.float().cpu().numpy(), ref, bound=bd, what=f"affine random N={N} K={K} M={M} g={group} b={block}")
+
+
 @pytest.mark.parametrize("block", [2, 32, 64, 128, 512])
 @pytest.mark.parametrize("prestage", [True, False])
 @pytest.mark.parametrize("K", [1152, 5120])

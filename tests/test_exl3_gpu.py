@@ -121,6 +121,31 @@ def test_apply_matches_oracle(M):
     assert_close(y.float().cpu().numpy(), ref, bound=bd, elem=APPLY_ELEM, what=f"exl3 apply M={M}")
 
 
+def _random_apply_cases(n, seed):
+    """Seeded shapes for the full apply: K and N any multiple of 128 up to 3072 (both sides are
+    rotated in 128-blocks), M from 1 to 8, bits2 (twice the rate) 2 to 8 over the three codebooks
+    (half-integer rates take the MUL1 codebook, the only one defined for them)."""
+    r = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        K, N, M = 128 * int(r.integers(1, 25)), 128 * int(r.integers(1, 25)), int(r.integers(1, 9))
+        bits2 = (2, 3, 4, 5, 6, 8)[int(r.integers(0, 6))]
+        cases.append((K, N, M, bits2, 2 if bits2 % 2 else i % 3))
+    return cases
+
+
+@pytest.mark.parametrize("K,N,M,bits2,cb", _random_apply_cases(24, 2026))
+def test_apply_random_shapes(K, N, M, bits2, cb):
+    print(f"exl3 random apply K={K} N={N} M={M} bits2={bits2} cb={cb}", flush=True)
+    t, suh, svh, ten = make(K, N, bits2, cb, seed=K + N + M)
+    x = synth.fp16_normal((M, K), seed=K + M)
+    ref, bd = apply_reference(x, t, suh, svh, bits2, cb)
+    y = exl3.apply(torch.from_numpy(x).to(DEV), ten)
+    assert y is not None
+    assert_close(y.float().cpu().numpy(), ref, bound=bd, elem=APPLY_ELEM,
+                 what=f"exl3 random apply K={K} N={N} M={M} bits2={bits2} cb={cb}")
+
+
 @pytest.mark.parametrize("M", [1, 3, 16])
 @pytest.mark.parametrize("K", [128, 1152, 5120])
 @pytest.mark.parametrize("bits2,cb", [(2, 0), (4, 1), (8, 2), (4, 0)])

@@ -82,6 +82,25 @@ def test_gemv_m1(t, N, K):
     assert_close(y, ref, bound=bd, what=f"gemv t={t} N={N} K={K}")
 
 
+def _random_cases(n, seed):
+    """Seeded shapes across every format: N from 1 to 2499 (ragged tiles, single rows), K any
+    whole number of blocks up to about 12K, M from 1 to 8 (GEMV, verify, per-block paths)."""
+    r = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        t = TYPES[i % len(TYPES)]
+        bk = synth.BLOCK[t][0]
+        cases.append((t, int(r.integers(1, 2500)), bk * int(r.integers(1, 12288 // bk + 1)), int(r.integers(1, 9))))
+    return cases
+
+
+@pytest.mark.parametrize("t,N,K,M", _random_cases(48, 2024))
+def test_random_shapes(t, N, K, M):
+    print(f"random shape type={t} N={N} K={K} M={M}", flush=True)
+    y, ref, bd = run_matvec(t, M, N, K, seed=N + K + M)
+    assert_close(y, ref, bound=bd, what=f"random t={t} N={N} K={K} M={M}")
+
+
 def test_gemv_wide_lanes():
     # units >= 1024 per row: the 32-lanes-per-row variant
     y, ref, bd = run_matvec(ggml.Q4_0, 1, 48, 32768, seed=5)

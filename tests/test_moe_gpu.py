@@ -96,6 +96,33 @@ def test_swiglu_qwen_shape(T):
     assert_close(y.float().cpu().numpy(), ref, bound=bd, elem=MOE_ELEM, what=f"moe qwen shape T={T}")
 
 
+def _random_moe_cases(n, seed):
+    """Seeded problems: T from 1 to 12 tokens (the gathered GEMVs and the streaming kernels),
+    E from 4 to 64 experts, top-k from 1 to min(8, E), H and I multiples of 256 up to 1536, the
+    three expert formats in turn."""
+    r = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        E = int(r.integers(4, 65))
+        cases.append((int(r.integers(1, 13)), E, int(r.integers(1, min(8, E) + 1)), 256 * int(r.integers(1, 7)),
+                      256 * int(r.integers(1, 7)), (ggml.Q4_0, ggml.Q4_K, ggml.Q6_K)[i % 3]))
+    return cases
+
+
+@pytest.mark.parametrize("T,E,k,H,I,type_", _random_moe_cases(12, 2027))
+def test_swiglu_random_shapes(T, E, k, H, I, type_):
+    print(f"moe random T={T} E={E} k={k} H={H} I={I} type={type_}", flush=True)
+    (g, u, d), ex = experts(E, H, I, type_, seed=T + E)
+    x = synth.fp16_normal((T, H), seed=H + T)
+    logits = np.random.default_rng(E + k).standard_normal((T, E)).astype(np.float32)
+    y = moe.swiglu(torch.from_numpy(x).to(DEV), torch.from_numpy(logits).to(DEV), ex, top_k=k)
+    assert y is not None
+    rid, rw = oracle.moe_route(logits, k)
+    ref, bd = moe_reference(type_, x.astype(np.float32), rid, rw, g, u, d, E, I)
+    assert_close(y.float().cpu().numpy(), ref, bound=bd, elem=MOE_ELEM,
+                 what=f"moe random T={T} E={E} k={k} H={H} I={I} type={type_}")
+
+
 @pytest.mark.parametrize("T,k", [(2, 32), (1, 64)])
 def test_swiglu_large_topk_few_tokens(T, k):
     """Many slots for one or two tokens: past the gathered GEMVs' LDS the per-block kernels run."""
