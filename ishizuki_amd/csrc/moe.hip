@@ -476,7 +476,10 @@ struct FMoeGateUp : F {
   struct Prep {
     lds_i32 *ids;  // [T k] expert of (t, s), in LDS
   };
-  static int occ(const Args &) { return 2; }
+  // one workgroup per CU for both gathered GEMVs: measured at the Qwen shape, T = 1, Q4_K experts
+  // 20.95 -> 20.4 us against two (down alone 21.0 -> 20.7; gate/up alone neutral; three and four
+  // slower: 21.6, 22.8)
+  static int occ(const Args &) { return 1; }
   // LDS after the format's tables: a routing row per token, the ids, scratch for the weights
   static size_t route_words(const Args &a) { return (size_t)a.rt.T * route_row_words(a.rt.E, a.k) + 2 * a.rt.T * a.k; }
   static size_t extra_lds_bytes(const Args &a) { return F::tab_bytes() + route_words(a) * 4; }
@@ -554,7 +557,7 @@ struct FMoeDown : F {
     lds_i32 *ids;  // [P] expert of each pair, in LDS before the first weight load
     lds_f32 *w;    // [P] routing weight of each pair
   };
-  static int occ(const Args &) { return 2; }
+  static int occ(const Args &) { return 1; }  // as FMoeGateUp
   static size_t extra_lds_bytes(const Args &a) { return F::tab_bytes() + ((size_t)nx(a) * 8 + 15) / 16 * 16; }
   static __host__ __device__ int nx(const Args &a) { return a.N / a.H; }  // pairs
   static constexpr bool X_ALL = true;  // every pair's h is staged (by prepare), image p at p
