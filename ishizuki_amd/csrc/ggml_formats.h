@@ -783,6 +783,7 @@ struct FIQ2_XS : GgmlGemv<FIQ2_XS> {
   // grid entry with its signs (exact small integers in fp16); A is x in natural order.
   static constexpr int VNS = 4, VSTEP_BYTES = TS;
   static constexpr bool VGRID = true;
+  static constexpr bool VPLAIN = true;  // signed grid entries times the scale: value = sc * C
   struct VRaw {
     u4 q;
     uint32_t sc, d;

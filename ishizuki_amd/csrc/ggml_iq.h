@@ -180,6 +180,7 @@ struct FIQ4_XS : GgmlQuarter<FIQ4_XS> {
   static constexpr int VNS = 2, Q = 1, SUM_LEN = 32;
   static constexpr bool XSUM = false, XPERM = false;
   static constexpr float OFF = 0.0f;
+  static constexpr bool VPLAIN = true;  // no offset, no min: value = sc * C
   static constexpr size_t TAB_BYTES = 256 * 4;
   static DEV void build_tab(u4 *t) {
     uint32_t *p = (uint32_t *)t;
@@ -233,6 +234,7 @@ struct FIQ2_XXS : GgmlQuarter<FIQ2_XXS> {
   static constexpr int VNS = 2, Q = 1, SUM_LEN = 32;
   static constexpr bool XSUM = false, XPERM = false;
   static constexpr float OFF = 0.0f;
+  static constexpr bool VPLAIN = true;  // no offset, no min: value = sc * C
   static constexpr size_t TAB_BYTES = 256 * 16;
   static DEV void build_tab(u4 *t) { tab_grid8<false>(ishz_iq2xxs_grid, 256, t); }
   static DEV int xk(int g, int r) { return 64 * g + 8 * r; }
@@ -266,6 +268,7 @@ struct FIQ2_S : GgmlQuarter<FIQ2_S> {
   static constexpr int VNS = 4, Q = 1, SUM_LEN = 16;
   static constexpr bool XSUM = false, XPERM = false;
   static constexpr float OFF = 0.0f;
+  static constexpr bool VPLAIN = true;  // no offset, no min: value = sc * C
   static constexpr size_t TAB_BYTES = 1024 * 16;
   static DEV void build_tab(u4 *t) { tab_grid8<false>(ishz_iq2s_grid, 1024, t); }
   static DEV int xk(int g, int r) { return 64 * g + 8 * r; }
@@ -307,6 +310,7 @@ struct FIQ3_XXS : GgmlQuarter<FIQ3_XXS> {
   static constexpr int VNS = 2, Q = 1, SUM_LEN = 32;
   static constexpr bool XSUM = false, XPERM = false;
   static constexpr float OFF = 0.0f;
+  static constexpr bool VPLAIN = true;  // no offset, no min: value = sc * C
   static constexpr size_t TAB_BYTES = 256 * 8;
   static DEV void build_tab(u4 *t) { tab_grid4(ishz_iq3xxs_grid, 256, (u2 *)t); }
   static DEV int xk(int g, int r) { return 64 * g + 8 * r; }
@@ -345,6 +349,7 @@ struct FIQ3_S : GgmlQuarter<FIQ3_S> {
   static constexpr int VNS = 2, Q = 1, SUM_LEN = 32;
   static constexpr bool XSUM = false, XPERM = false;
   static constexpr float OFF = 0.0f;
+  static constexpr bool VPLAIN = true;  // no offset, no min: value = sc * C
   static constexpr size_t TAB_BYTES = 512 * 8;
   static DEV void build_tab(u4 *t) { tab_grid4(ishz_iq3s_grid, 512, (u2 *)t); }
   static DEV int xk(int g, int r) { return 64 * g + 8 * r; }

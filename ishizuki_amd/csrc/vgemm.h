@@ -26,6 +26,8 @@
 //   void vscale(r, g, s, sc, mn)     value of sub-unit s = sc * (C - off1) + mn * X
 //   vtables(tabs), tab_bytes()       LDS tables the decoder reads (codebooks, sign masks)
 //   VDEPTH                           steps kept in flight (register ring)
+//   VPLAIN (optional, true)          off1 and mn are always zero: value = sc * C, so the epilogue
+//                                    reads no sums
 #pragma once
 #include <algorithm>
 #include <cstdlib>
@@ -33,6 +35,12 @@
 #include "common.h"
 
 namespace ishz {
+
+template <class F>
+__host__ __device__ constexpr bool vgemm_plain() {
+  if constexpr (requires { F::VPLAIN; }) return F::VPLAIN;
+  else return false;
+}
 
 // What is multiplied: a "problem" P supplies, per workgroup row blockIdx.y (a group: the whole
 // matrix, or one routed expert), the token rows of x, the weight rows, and the output writer.
@@ -162,10 +170,15 @@ __global__ __launch_bounds__(64 * NW) void vgemm_kernel(P p, int K, int Kc, int 
               f4 C = f4{0, 0, 0, 0};
 #pragma unroll
               for (int b = 0; b < MPS; b++) C = mfma32(as_h8(ab[s * MPS + b]), as_h8(B[s * MPS + b]), C);
-              const float *sp = sums + (((j * 4 + G) * NS + s) * 2) * MT + 4 * q;
-              const f4 off = *(const f4 *)sp, X = *(const f4 *)(sp + MT);
+              if constexpr (vgemm_plain<F>()) {
 #pragma unroll
-              for (int e = 0; e < 4; e++) acc[q][e] += sc[s] * (C[e] - off[e]) + mn[s] * X[e];
+                for (int e = 0; e < 4; e++) acc[q][e] = fmaf(sc[s], C[e], acc[q][e]);
+              } else {
+                const float *sp = sums + (((j * 4 + G) * NS + s) * 2) * MT + 4 * q;
+                const f4 off = *(const f4 *)sp, X = *(const f4 *)(sp + MT);
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[q][e] += sc[s] * (C[e] - off[e]) + mn[s] * X[e];
+              }
             }
           }
           // park at the wave's last item of a tile: sum the row's four lane-group quarters
