@@ -178,6 +178,7 @@ struct FAffineN : GgmlGemv<FAffineN<BITS, GS, BF16S>> {
     }
     off1 = 1024.0f * X;
   }
+  static constexpr float voff() { return 1024.0f; }  // off1 of vstage, per unit of X
   static DEV void vscale(const VRaw &r, int, int, float &sc, float &mn) {
     sc = ld_s(r.s);
     mn = ld_s(r.b);

@@ -310,6 +310,7 @@ struct FQ4_0 : GgmlGemv<FQ4_0> {
     A[1] = vx8p(p + 8, X);
     off1 = 1024.0f * X;
   }
+  static constexpr float voff() { return 1024.0f; }  // off1 of vstage, per unit of X
   static DEV void vscale(const VRaw &r, int, int s, float &sc, float &mn) {
     const float d = h2f(s >> 1 ? r.b.x >> 16 : r.a.x & 0xffff);
     sc = (s & 1) ? 0.0625f * d : d;
@@ -443,6 +444,7 @@ struct FQ4_K : GgmlGemv<FQ4_K> {
     for (int b = 0; b < 4; b++) A[b] = vx8p(p + 8 * b, X);
     off1 = 1024.0f * X;
   }
+  static constexpr float voff() { return 1024.0f; }  // off1 of vstage, per unit of X
   static DEV void vscale(const VRaw &r, int g, int s, float &sc, float &mn) {
     int scv, m;
     q4k_scale_min(r.h.y, r.h.z, r.h.w, 2 * g + s, scv, m);
@@ -608,6 +610,7 @@ struct FQ6_K : GgmlGemv<FQ6_K> {
     A[1] = vx8p(p + 8, X);
     off1 = 1024.0f * X;
   }
+  static constexpr float voff() { return 1024.0f; }  // off1 of vstage, per unit of X
   static DEV void vscale(const VRaw &r, int g, int s, float &sc, float &mn) {
     const int bi = 8 * (g >> 1) + (g & 1) + 2 * s;  // scale byte
     const float d = h2f(r.d) * (float)(int8_t)(r.sc[bi >> 2] >> (8 * (bi & 3)));

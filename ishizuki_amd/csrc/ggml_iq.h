@@ -107,6 +107,7 @@ struct GgmlQuarter : GgmlGemv<D> {
     }
     off1 = D::OFF * X;
   }
+  static constexpr float voff() { return D::OFF; }  // off1 of vstage, per unit of X
   // Natural order, with the sum of the 8 values.
   static DEV u4 vx8s(const uint16_t *p, float &X) {
     const u4 v = *(const u4 *)p;

@@ -28,6 +28,7 @@
 //   VDEPTH                           steps kept in flight (register ring)
 //   VPLAIN (optional, true)          off1 and mn are always zero: value = sc * C, so the epilogue
 //                                    reads no sums
+//   voff() (optional)                off1 is always voff() * X: the epilogue reads X only
 #pragma once
 #include <algorithm>
 #include <cstdlib>
@@ -173,6 +174,12 @@ __global__ __launch_bounds__(64 * NW) void vgemm_kernel(P p, int K, int Kc, int 
               if constexpr (vgemm_plain<F>()) {
 #pragma unroll
                 for (int e = 0; e < 4; e++) acc[q][e] = fmaf(sc[s], C[e], acc[q][e]);
+              } else if constexpr (requires { F::voff(); }) {
+                // off1 = voff X: sc (C - voff X) + mn X = sc C + (mn - voff sc) X, one sum read
+                const f4 X = *(const f4 *)(sums + (((j * 4 + G) * NS + s) * 2 + 1) * MT + 4 * q);
+                const float cx = mn[s] - F::voff() * sc[s];
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[q][e] = fmaf(sc[s], C[e], fmaf(cx, X[e], acc[q][e]));
               } else {
                 const float *sp = sums + (((j * 4 + G) * NS + s) * 2) * MT + 4 * q;
                 const f4 off = *(const f4 *)sp, X = *(const f4 *)(sp + MT);
