@@ -183,7 +183,10 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict_
 
 // Pair lists (one workgroup): per-expert counts in LDS, an exclusive prefix over experts by wave
 // 0, then each pair takes the next free position of its expert (the order inside an expert does
-// not affect any result: every pair's rows are computed independently).
+// not affect any result: every pair's rows are computed independently). ORDERED: positions in
+// (token, slot) order inside each expert instead, the same in every workgroup that places the
+// same ids (a pair's rank among the earlier pairs of its expert: P^2 / 2 compares, for few pairs).
+template <bool ORDERED = false>
 DEV void place_pairs(int T, int E, int k, const MoeRoute &R, const int32_t *ids, int32_t *cnt) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int P = T * k;
@@ -219,7 +222,15 @@ DEV void place_pairs(int T, int E, int k, const MoeRoute &R, const int32_t *ids,
   }
   __syncthreads();
   for (int q = threadIdx.x; q < P; q += blockDim.x) {
-    const int pos = atomicAdd(&cnt[ids[q]], 1);
+    int pos;
+    if constexpr (ORDERED) {
+      const int e = ids[q];
+      int r = 0;
+      for (int q2 = 0; q2 < q; q2++) r += ids[q2] == e;
+      pos = R.offs[e] + r;
+    } else {
+      pos = atomicAdd(&cnt[ids[q]], 1);
+    }
     R.pair_tok[pos] = q / k;
     R.inv[q] = pos;
   }
@@ -393,6 +404,73 @@ struct VMoeGateUp {
       }
     }
   }
+};
+
+// gate + up with the routing done by every workgroup (a few tokens): the separate route + place
+// launch is skipped. Each workgroup routes every token and places the pairs (ORDERED, so all of
+// them agree) into its own LDS; workgroup (0, 0) publishes ids, weights and the pair lists for
+// the down projection and the combine, which run after this launch.
+struct VMoeGateUpR : VMoeGateUp {
+  const float *logits;
+  int T, E, k, normalize;
+  uint32_t lds_off;  // byte offset of the routing scratch in the dynamic LDS (set at launch)
+  // scratch (int32 words): routing rows, ids [P], w [P], counts [E], count, active [E],
+  // offs [E + 1], pair_tok [P], inv [P]
+  static int rows_used(int T) { return T < 32 ? T : 32; }  // 16-lane rows of a 512-thread workgroup
+  static size_t extra_lds(const VMoeGateUpR &p) {
+    const size_t P = (size_t)p.T * p.k;
+    return ((size_t)rows_used(p.T) * route_row_words(p.E, p.k) + 4 * P + 3 * (size_t)p.E + 2) * 4;
+  }
+  DEV int32_t *scratch() const {
+    extern __shared__ __align__(16) u4 vgsm[];
+    return (int32_t *)((char *)vgsm + lds_off);
+  }
+  DEV MoeRoute lds_route() const {
+    const int P = T * k, nr = min(T, (int)(blockDim.x >> 4));
+    int32_t *b = scratch() + nr * route_row_words(E, k);
+    int32_t *ids = b, *w = b + P, *cnt = w + P, *count = cnt + E, *active = count + 1, *offs = active + E;
+    int32_t *pair_tok = offs + E + 1, *inv = pair_tok + P;
+    return MoeRoute{ids, (float *)w, count, active, offs, pair_tok, inv, nullptr, nullptr};
+  }
+  DEV void prologue() const {
+    const MoeRoute L = lds_route();
+    const int nr = min(T, (int)(blockDim.x >> 4)), rw = route_row_words(E, k), row = threadIdx.x >> 4;
+    if (row < nr)
+      for (int t = row; t < T; t += nr) {
+#define ISHZ_CALL(NPL) route_token<NPL>(logits + (size_t)t * E, E, k, normalize, t, (uint32_t *)scratch() + row * rw, L, nullptr)
+        ISHZ_ROUTE_NPL(E, 256, ISHZ_CALL);
+#undef ISHZ_CALL
+        __builtin_amdgcn_wave_barrier();  // the row's LDS is reused by its next token
+      }
+    __syncthreads();
+    place_pairs<true>(T, E, k, L, L.ids, L.ids + 2 * T * k);
+    __syncthreads();
+    if (blockIdx.x == 0 && blockIdx.y == 0) {  // publish
+      const int P = T * k;
+      for (int q = threadIdx.x; q < P; q += blockDim.x) {
+        R.ids[q] = L.ids[q];
+        R.w[q] = L.w[q];
+        R.pair_tok[q] = L.pair_tok[q];
+        R.inv[q] = L.inv[q];
+        if (R.ids_out) R.ids_out[q] = L.ids[q];
+        if (R.w_out) R.w_out[q] = L.w[q];
+      }
+      for (int e = threadIdx.x; e <= E; e += blockDim.x) {
+        R.offs[e] = L.offs[e];
+        if (e < E) R.active[e] = L.active[e];
+      }
+      if (threadIdx.x == 0) R.count[0] = L.count[0];
+    }
+  }
+  DEV bool group(int a, Group &g) const {
+    const MoeRoute L = lds_route();
+    if (a >= L.count[0]) return false;
+    g.e = L.active[a];
+    g.p0 = L.offs[g.e];
+    g.p1 = L.offs[g.e + 1];
+    return true;
+  }
+  DEV const uint16_t *xrow(const Group &g, int tk) const { return x + (size_t)lds_route().pair_tok[g.p0 + tk] * H; }
 };
 
 // down: o[pair][H] = h[pair] . down_e^T (fp16).
@@ -688,6 +766,13 @@ static bool gathered_gemv(int T, int H, int I, int k) {
   return H % 256 == 0 && I % 256 == 0 && T <= 2 && (size_t)T * k * per_pair <= 144 * 1024;
 }
 
+// Three to sixteen tokens on the streaming kernels: gate/up routes inside every workgroup
+// (VMoeGateUpR) in place of the route + place launch.
+static bool route_in_gate_up(int T, int H, int E, int I, int k) {
+  return !gathered_gemv(T, H, I, k) && H % 256 == 0 && I % 256 == 0 && T > 2 && T <= 16 && E <= 256 &&
+         T * k <= 256;
+}
+
 template <class F>
 static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void *gate,
                    const void *up, const void *down, const MoeTokens &rt, uint16_t *h, uint16_t *gu, uint16_t *o,
@@ -724,7 +809,19 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
     };
     const VMoeGateUp gu{(const uint16_t *)x, (const uint8_t *)gate, (const uint8_t *)up,
                         (size_t)(H / F::BS) * F::TS, H, I, R, h};
-    int rc = moe_vgemm<F>(gu, T, E, k, H, tiles_gu * 16, amax, pick(tiles_gu, 1), st);
+    int rc;
+    if (route_in_gate_up(T, H, E, I, k)) {
+      VMoeGateUpR gr{};
+      static_cast<VMoeGateUp &>(gr) = gu;
+      gr.logits = rt.logits;
+      gr.T = T;
+      gr.E = E;
+      gr.k = k;
+      gr.normalize = rt.normalize;
+      rc = moe_vgemm<F>(gr, T, E, k, H, tiles_gu * 16, amax, pick(tiles_gu, 1), st);
+    } else {
+      rc = moe_vgemm<F>(gu, T, E, k, H, tiles_gu * 16, amax, pick(tiles_gu, 1), st);
+    }
     if (rc) return rc;
     const VMoeDown dn{h, (const uint8_t *)down, (size_t)(I / F::BS) * F::TS, I, H, R, o};
     rc = moe_vgemm<F>(dn, T, E, k, I, H, amax, pick(tiles_dn, 0), st);
@@ -906,7 +1003,8 @@ extern "C" int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T,
   R.w_out = weights_out;
   hipStream_t st = S(stream);
   const MoeTokens rt{logits, T, E, normalize, R};
-  if (!gathered_gemv(T, H, I, topk)) {  // (the gathered GEMVs route inside their first launch)
+  // (the gathered GEMVs, and gate/up for a few tokens, route inside their first launch)
+  if (!gathered_gemv(T, H, I, topk) && !route_in_gate_up(T, H, E, I, topk)) {
     const int rc = moe_route_all(logits, T, E, topk, normalize, R, true, st);
     if (rc) return rc;
   }

@@ -52,6 +52,8 @@ __host__ __device__ constexpr bool vgemm_plain() {
 //   void finish(g, c0, M, tb, te, out)   write tokens c0 .. c0 + M - 1 of tiles tb .. te - 1;
 //                                 out[(tile - tb) * 256 + tk * 16 + n] is row 16 tile + n
 //   PAIRS                         tiles_per_wg must be even and start even (SwiGLU pairs)
+//   optional: void prologue() run by every thread of every workgroup before group() (ends with a
+//   barrier), with static size_t extra_lds(p) bytes of its own LDS at byte offset p.lds_off
 // Work split: a workgroup owns tiles tb .. te - 1 of its group and, with S > 1 (K split: the
 // problem's finish then writes fp32 partials), the S-th part blockIdx.x % S of the K steps; the
 // (tile, step) items go to its waves round-robin (item i to wave i % NW), so short K still uses
@@ -62,8 +64,9 @@ __global__ __launch_bounds__(64 * NW) void vgemm_kernel(P p, int K, int Kc, int 
   constexpr int MT = 4 * NQ;                // tokens per pass, padded to whole quads
   typedef typename P::Group Group;
   Group gp;
-  if (!p.group(blockIdx.y, gp)) return;
   extern __shared__ __align__(16) u4 vgsm[];
+  if constexpr (requires { p.prologue(); }) p.prologue();  // every thread; ends with a barrier
+  if (!p.group(blockIdx.y, gp)) return;
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int n = lane & 15, G = lane >> 4;
   const int N = p.rows(gp), ntiles = (N + 15) / 16;
@@ -243,13 +246,21 @@ static int launch_vgemm_p(const P &p, int K, int rows, int groups, int T, hipStr
   constexpr int NW = 8;
   constexpr int D = F::VDEPTH;  // ring depth: what fits the registers with the format's raw
   const int ntiles = (rows + 15) / 16;
-  const size_t budget = 150 * 1024;
+  size_t extra = 0;  // the problem's own LDS (P::extra_lds), after the kernel's
+  if constexpr (requires { P::extra_lds(p); }) extra = (P::extra_lds(p) + 15) / 16 * 16;
+  const size_t budget = 150 * 1024 - extra;
   int Kc = (K / 256 + S - 1) / S * 256;  // one part of K
   while (Kc > 256 && vgemm_lds<F, NQ, NW>(Kc, T) > budget) Kc -= 256;
   if (vgemm_lds<F, NQ, NW>(Kc, T) > budget) return decline("verify x does not fit in LDS");
-  const size_t lds = vgemm_lds<F, NQ, NW>(Kc, T);
+  size_t lds = vgemm_lds<F, NQ, NW>(Kc, T);
+  P p2 = p;
+  if constexpr (requires { P::extra_lds(p); }) {
+    lds = (lds + 15) / 16 * 16;
+    p2.lds_off = (uint32_t)lds;
+    lds += extra;
+  }
   hipLaunchKernelGGL((vgemm_kernel<F, P, NQ, D, NW>), dim3((ntiles + T - 1) / T * S, groups), dim3(64 * NW), lds, st,
-                     p, K, Kc, T, S);
+                     p2, K, Kc, T, S);
   ISHZ_LAUNCH_CHECK("vgemm launch");
   return ISHZ_OK;
 }
