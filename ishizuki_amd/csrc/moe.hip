@@ -28,8 +28,7 @@ struct MoeRoute {
   int32_t *count;     // [1] number of active experts
   int32_t *active;    // [E] active experts, ascending
   int32_t *offs;      // [E+1] pair range of expert e in the sorted list
-  int32_t *pair_tok;  // [T*k] token of sorted pair
-  int32_t *inv;       // [T*k] sorted position of (t, s)
+  int32_t *pair_q;    // [T*k] slot index q = t k + s of sorted pair (its token is q / k)
   int32_t *ids_out;   // optional caller copies of ids / w (null: none)
   float *w_out;
 };
@@ -231,8 +230,7 @@ DEV void place_pairs(int T, int E, int k, const MoeRoute &R, const int32_t *ids,
     } else {
       pos = atomicAdd(&cnt[ids[q]], 1);
     }
-    R.pair_tok[pos] = q / k;
-    R.inv[q] = pos;
+    R.pair_q[pos] = q;
   }
 }
 
@@ -263,7 +261,7 @@ DEV float r16(float v) { return (float)(_Float16)v; }
 template <class F>
 __global__ __launch_bounds__(1024) void moe_gate_up_kernel(const uint16_t *__restrict__ x, int H,
                                                            const uint8_t *__restrict__ gate,
-                                                           const uint8_t *__restrict__ up, int I,
+                                                           const uint8_t *__restrict__ up, int I, int k,
                                                            MoeRoute R, uint16_t *__restrict__ h) {
   extern __shared__ __align__(16) float red[];
   const int a = blockIdx.y;
@@ -278,7 +276,7 @@ __global__ __launch_bounds__(1024) void moe_gate_up_kernel(const uint16_t *__res
   const uint8_t *rows[2] = {gate + erow * rb, up + erow * rb};
   for (int c0 = p0; c0 < p1; c0 += 16) {
     const bool tok = c0 + j < p1;
-    const uint16_t *xr = x + (size_t)(tok ? R.pair_tok[c0 + j] : 0) * H;
+    const uint16_t *xr = x + (size_t)(tok ? R.pair_q[c0 + j] / k : 0) * H;
     f4 acc[2] = {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}};
     for (int b = wave; b < nblk; b += KS) F::template vblock<2>(rows, b, g, xr, tok, acc);
 #pragma unroll
@@ -335,14 +333,14 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(const uint16_t *__restri
       float s = 0.0f;
       for (int v = 0; v < KS; v++) s += red[((v * 2 + t2) * 4 + r) * 64 + l];
       const int t = 4 * (l >> 4) + r, n = n0 + 16 * t2 + (l & 15);
-      if (c0 + t < p1 && n < H) o[(size_t)(c0 + t) * H + n] = f2h(s);
+      if (c0 + t < p1 && n < H) o[(size_t)R.pair_q[c0 + t] * H + n] = f2h(s);  // slot order
     }
     __syncthreads();
   }
 }
 
 __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__restrict__ o, int H,
-                                                          int T, int k, MoeRoute R, bool sorted,
+                                                          int T, int k, MoeRoute R,
                                                           const uint16_t *__restrict__ shared,
                                                           const uint16_t *__restrict__ shared_gate,
                                                           uint16_t *__restrict__ y) {
@@ -352,8 +350,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__rest
     const int t = (int)(q / H), n = (int)(q % H);
     float acc = 0.0f;
     for (int s = 0; s < k; s++) {
-      const int q2 = sorted ? R.inv[t * k + s] : t * k + s;  // row of o holding pair (t, s)
-      acc += h2f(o[(size_t)q2 * H + n]) * R.w[t * k + s];
+      acc += h2f(o[((size_t)t * k + s) * H + n]) * R.w[t * k + s];  // o rows in slot order
     }
     if (shared) {  // the shared expert, widened and added before the one narrowing
       const float sg = (float)(_Float16)(1.0f / (1.0f + __expf(-h2f(shared_gate[t]))));
@@ -376,6 +373,7 @@ struct VMoeGateUp {
   int H, I;
   MoeRoute R;
   uint16_t *h;
+  int k;
   struct Group {
     int e, p0, p1;
   };
@@ -388,7 +386,7 @@ struct VMoeGateUp {
   }
   DEV int count(const Group &g) const { return g.p1 - g.p0; }
   DEV int rows(const Group &) const { return 2 * ((I + 15) / 16) * 16; }
-  DEV const uint16_t *xrow(const Group &g, int tk) const { return x + (size_t)R.pair_tok[g.p0 + tk] * H; }
+  DEV const uint16_t *xrow(const Group &g, int tk) const { return x + (size_t)(R.pair_q[g.p0 + tk] / k) * H; }
   DEV const uint8_t *wrow(const Group &g, int row) const {
     const int tile = row >> 4, i = min((tile >> 1) * 16 + (row & 15), I - 1);
     return ((tile & 1) ? up : gate) + ((size_t)g.e * I + i) * rb;
@@ -412,14 +410,14 @@ struct VMoeGateUp {
 // the down projection and the combine, which run after this launch.
 struct VMoeGateUpR : VMoeGateUp {
   const float *logits;
-  int T, E, k, normalize;
+  int T, E, normalize;
   uint32_t lds_off;  // byte offset of the routing scratch in the dynamic LDS (set at launch)
   // scratch (int32 words): routing rows, ids [P], w [P], counts [E], count, active [E],
-  // offs [E + 1], pair_tok [P], inv [P]
+  // offs [E + 1], pair_q [P]
   static int rows_used(int T) { return T < 32 ? T : 32; }  // 16-lane rows of a 512-thread workgroup
   static size_t extra_lds(const VMoeGateUpR &p) {
     const size_t P = (size_t)p.T * p.k;
-    return ((size_t)rows_used(p.T) * route_row_words(p.E, p.k) + 4 * P + 3 * (size_t)p.E + 2) * 4;
+    return ((size_t)rows_used(p.T) * route_row_words(p.E, p.k) + 3 * P + 3 * (size_t)p.E + 2) * 4;
   }
   DEV int32_t *scratch() const {
     extern __shared__ __align__(16) u4 vgsm[];
@@ -429,8 +427,8 @@ struct VMoeGateUpR : VMoeGateUp {
     const int P = T * k, nr = min(T, (int)(blockDim.x >> 4));
     int32_t *b = scratch() + nr * route_row_words(E, k);
     int32_t *ids = b, *w = b + P, *cnt = w + P, *count = cnt + E, *active = count + 1, *offs = active + E;
-    int32_t *pair_tok = offs + E + 1, *inv = pair_tok + P;
-    return MoeRoute{ids, (float *)w, count, active, offs, pair_tok, inv, nullptr, nullptr};
+    int32_t *pair_q = offs + E + 1;
+    return MoeRoute{ids, (float *)w, count, active, offs, pair_q, nullptr, nullptr};
   }
   DEV void prologue() const {
     const MoeRoute L = lds_route();
@@ -450,8 +448,7 @@ struct VMoeGateUpR : VMoeGateUp {
       for (int q = threadIdx.x; q < P; q += blockDim.x) {
         R.ids[q] = L.ids[q];
         R.w[q] = L.w[q];
-        R.pair_tok[q] = L.pair_tok[q];
-        R.inv[q] = L.inv[q];
+        R.pair_q[q] = L.pair_q[q];
         if (R.ids_out) R.ids_out[q] = L.ids[q];
         if (R.w_out) R.w_out[q] = L.w[q];
       }
@@ -470,7 +467,7 @@ struct VMoeGateUpR : VMoeGateUp {
     g.p1 = L.offs[g.e + 1];
     return true;
   }
-  DEV const uint16_t *xrow(const Group &g, int tk) const { return x + (size_t)lds_route().pair_tok[g.p0 + tk] * H; }
+  DEV const uint16_t *xrow(const Group &g, int tk) const { return x + (size_t)(lds_route().pair_q[g.p0 + tk] / k) * H; }
 };
 
 // down: o[pair][H] = h[pair] . down_e^T (fp16).
@@ -498,7 +495,7 @@ struct VMoeDown {
   DEV void finish(const Group &g, int c0, int m, int tb, int te, const float *out) const {
     for (int q = threadIdx.x; q < (te - tb) * 256; q += blockDim.x) {
       const int tk = (q >> 4) & 15, row = (tb + (q >> 8)) * 16 + (q & 15);
-      if (tk < m && row < H) o[(size_t)(g.p0 + c0 + tk) * H + row] = f2h(out[q]);
+      if (tk < m && row < H) o[(size_t)R.pair_q[g.p0 + c0 + tk] * H + row] = f2h(out[q]);  // slot order
     }
   }
 };
@@ -725,7 +722,7 @@ static int route_launch(const float *logits, int T, int E, int k, int normalize,
 }
 
 struct MoeLayout {
-  size_t ids, w, count, active, offs, pair_tok, inv, h, gu, o, total;
+  size_t ids, w, count, active, offs, pair_q, h, gu, o, total;
 };
 static MoeLayout moe_layout(int T, int H, int E, int I, int k) {
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
@@ -737,8 +734,7 @@ static MoeLayout moe_layout(int T, int H, int E, int I, int k) {
   L.count = off; off += al(4);
   L.active = off; off += al((size_t)E * 4);
   L.offs = off; off += al((size_t)(E + 1) * 4);
-  L.pair_tok = off; off += al(P * 4);
-  L.inv = off; off += al(P * 4);
+  L.pair_q = off; off += al(P * 4);
   L.h = off; off += al(P * I * 2);
   L.gu = off; off += al(P * 2 * I * 2);
   L.o = off; off += al(P * H * 2);
@@ -749,8 +745,8 @@ static MoeLayout moe_layout(int T, int H, int E, int I, int k) {
 static MoeRoute moe_route_ptrs(void *ws, const MoeLayout &L) {
   uint8_t *b = (uint8_t *)ws;
   return MoeRoute{(int32_t *)(b + L.ids), (float *)(b + L.w), (int32_t *)(b + L.count),
-                  (int32_t *)(b + L.active), (int32_t *)(b + L.offs), (int32_t *)(b + L.pair_tok),
-                  (int32_t *)(b + L.inv), nullptr, nullptr};
+                  (int32_t *)(b + L.active), (int32_t *)(b + L.offs), (int32_t *)(b + L.pair_q), nullptr,
+                  nullptr};
 }
 
 static int ks_for(int tiles, int nblk) {
@@ -808,7 +804,7 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
       return t;
     };
     const VMoeGateUp gu{(const uint16_t *)x, (const uint8_t *)gate, (const uint8_t *)up,
-                        (size_t)(H / F::BS) * F::TS, H, I, R, h};
+                        (size_t)(H / F::BS) * F::TS, H, I, R, h, k};
     int rc;
     if (route_in_gate_up(T, H, E, I, k)) {
       VMoeGateUpR gr{};
@@ -816,7 +812,6 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
       gr.logits = rt.logits;
       gr.T = T;
       gr.E = E;
-      gr.k = k;
       gr.normalize = rt.normalize;
       rc = moe_vgemm<F>(gr, T, E, k, H, tiles_gu * 16, amax, pick(tiles_gu, 1), st);
     } else {
@@ -829,7 +824,7 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
   } else {
     int ks = ks_for((I / 16) * amax, H / F::BS);
     hipLaunchKernelGGL((moe_gate_up_kernel<F>), dim3(I / 16, amax), dim3(64 * ks), (size_t)ks * 2 * 256 * 4, st,
-                       (const uint16_t *)x, H, (const uint8_t *)gate, (const uint8_t *)up, I, R, h);
+                       (const uint16_t *)x, H, (const uint8_t *)gate, (const uint8_t *)up, I, k, R, h);
     ISHZ_LAUNCH_CHECK("moe gate/up launch");
     ks = ks_for((H / 32) * amax, I / F::BS);
     hipLaunchKernelGGL((moe_down_kernel<F>), dim3((H + 31) / 32, amax), dim3(64 * ks), (size_t)ks * 2 * 256 * 4,
@@ -837,7 +832,7 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
     ISHZ_LAUNCH_CHECK("moe down launch");
   }
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)std::min<size_t>((total + 255) / 256, 4096)), dim3(256), 0,
-                     st, o, H, T, k, R, true, shared, shared_gate, (uint16_t *)y);
+                     st, o, H, T, k, R, shared, shared_gate, (uint16_t *)y);
   ISHZ_LAUNCH_CHECK("moe combine launch");
   return ISHZ_OK;
 }
@@ -944,7 +939,7 @@ static int moe_ffn_affine(const void *x, int T, int H, int E, int I, int k, cons
     return t;
   };
   VMoeGateUpA pgu{};
-  static_cast<VMoeGateUp &>(pgu) = VMoeGateUp{(const uint16_t *)x, nullptr, nullptr, 0, H, I, R, h};
+  static_cast<VMoeGateUp &>(pgu) = VMoeGateUp{(const uint16_t *)x, nullptr, nullptr, 0, H, I, R, h, k};
   pgu.g = gate;
   pgu.u = up;
   int rc = moe_vgemm<F>(pgu, T, E, k, H, tiles_gu * 16, amax, pick(tiles_gu, 1), st);
@@ -955,7 +950,7 @@ static int moe_ffn_affine(const void *x, int T, int H, int E, int I, int k, cons
   rc = moe_vgemm<F>(dn, T, E, k, I, H, amax, pick(tiles_dn, 0), st);
   if (rc) return rc;
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)std::min<size_t>((total + 255) / 256, 4096)), dim3(256), 0,
-                     st, o, H, T, k, R, true, shared, shared_gate, (uint16_t *)y);
+                     st, o, H, T, k, R, shared, shared_gate, (uint16_t *)y);
   ISHZ_LAUNCH_CHECK("moe combine launch");
   return ISHZ_OK;
 }
@@ -973,7 +968,7 @@ extern "C" int ishz_moe_route(const float *logits, int T, int E, int topk, int n
   if (T <= 0 || E <= 0 || topk <= 0 || topk > E || topk > 64) return decline("bad routing shape");
   if ((size_t)4 * route_row_words(E, topk) * 4 > 160 * 1024) return decline("too many experts for one routing workgroup");
   if (!logits || !ids || !weights) return einval("null pointer");
-  MoeRoute R{ids, weights, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+  MoeRoute R{ids, weights, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
   return route_launch(logits, T, E, topk, normalize, R, S(stream));
 }
 
