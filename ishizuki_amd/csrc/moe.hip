@@ -6,13 +6,19 @@
 // down(silu(gate(x)) * up(x)), the k outputs weighted and summed in fp32, narrowed once.
 // Activations between stages are fp16 as the reference's gatherQuantizedMM outputs x.dtype.
 //
-// Kernels: route + place (one workgroup, a wave per token: top-k by rounds of wave argmax, then
-// per-expert pair lists and the active-expert list). One or two tokens: gate+up and down as
-// gathered GEMVs over every (token, slot) pair (the streaming GEMV skeleton; SwiGLU while
-// staging down's x). More tokens: the streaming MFMA kernel over active experts x tiles (the
-// expert's gate and up rows are two tiles of the same workgroup, tokens gathered through the pair
-// list, SwiGLU in the epilogue), then down likewise. Combine: weighted fp32 sum per token. Only
-// routed experts' blocks are ever read.
+// Kernels:
+//  * Route + place: one workgroup, a 16-lane row per token. Top-k by rounds of a row-wide argmax,
+//    then the per-expert pair lists and the active-expert list.
+//  * One or two tokens: gate+up and down as gathered GEMVs over every (token, slot) pair (the
+//    streaming GEMV skeleton), routing inside the first of the two launches and the combine in the
+//    second's store.
+//  * More tokens: the streaming MFMA kernel over active experts x tiles. An expert's gate and up
+//    rows are two tiles of the same workgroup, tokens are gathered through the pair list, and
+//    SwiGLU runs in the epilogue. Down works the same way and writes its rows in slot order. With
+//    up to 16 tokens every gate/up workgroup routes and places in its own LDS, so the route +
+//    place launch is skipped.
+//  * Combine: the weighted fp32 sum per token.
+// Only routed experts' blocks are ever read.
 #include <algorithm>
 #include <cstdlib>
 
