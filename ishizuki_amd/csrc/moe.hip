@@ -420,7 +420,8 @@ struct VMoeGateUpR : VMoeGateUp {
   uint32_t lds_off;  // byte offset of the routing scratch in the dynamic LDS (set at launch)
   // scratch (int32 words): routing rows, ids [P], w [P], counts [E], count, active [E],
   // offs [E + 1], pair_q [P]
-  static int rows_used(int T) { return T < 32 ? T : 32; }  // 16-lane rows of a 512-thread workgroup
+  // routing rows in LDS: one per token, at most the 32 16-lane rows of a 512-thread workgroup
+  __host__ __device__ static int rows_used(int T) { return T < 32 ? T : 32; }
   static size_t extra_lds(const VMoeGateUpR &p) {
     const size_t P = (size_t)p.T * p.k;
     return ((size_t)rows_used(p.T) * route_row_words(p.E, p.k) + 3 * P + 3 * (size_t)p.E + 2) * 4;
@@ -430,15 +431,15 @@ struct VMoeGateUpR : VMoeGateUp {
     return (int32_t *)((char *)vgsm + lds_off);
   }
   DEV MoeRoute lds_route() const {
-    const int P = T * k, nr = min(T, (int)(blockDim.x >> 4));
-    int32_t *b = scratch() + nr * route_row_words(E, k);
+    const int P = T * k;
+    int32_t *b = scratch() + rows_used(T) * route_row_words(E, k);
     int32_t *ids = b, *w = b + P, *cnt = w + P, *count = cnt + E, *active = count + 1, *offs = active + E;
     int32_t *pair_q = offs + E + 1;
     return MoeRoute{ids, (float *)w, count, active, offs, pair_q, nullptr, nullptr};
   }
   DEV void prologue() const {
     const MoeRoute L = lds_route();
-    const int nr = min(T, (int)(blockDim.x >> 4)), rw = route_row_words(E, k), row = threadIdx.x >> 4;
+    const int nr = min(rows_used(T), (int)(blockDim.x >> 4)), rw = route_row_words(E, k), row = threadIdx.x >> 4;
     if (row < nr)
       for (int t = row; t < T; t += nr) {
 #define ISHZ_CALL(NPL) route_token<NPL>(logits + (size_t)t * E, E, k, normalize, t, (uint32_t *)scratch() + row * rw, L, nullptr)
