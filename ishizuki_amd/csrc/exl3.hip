@@ -305,8 +305,8 @@ DEV void wht128_pair(float &v0, float &v1, int lane) {
 // adjacent column tiles of one K tile (1 KB contiguous), fetched with one 128-bit load per lane
 // and spread through LDS, so each wave keeps kilobytes in flight instead of the few hundred
 // bytes that per-lane word loads give. Lanes decode as in exl3_mm2 (32-bit windows, pairwise
-// codebook). The K tiles split over workgroups (blockIdx.y) and over a workgroup's waves; partial
-// outputs are summed into yh with atomic adds (yh zeroed first), in no fixed order.
+// codebook). The K tiles split over workgroups (blockIdx.y) and over a workgroup's waves; each K
+// split stores its partial outputs into its own [M][N] slice of yh (summed later in split order).
 //
 // ROT: xh is the unrotated x and suh its input scales; each workgroup rotates the 128-point blocks
 // that cover its K tiles, for every row, into LDS (after its first weight loads are issued) and
@@ -314,7 +314,7 @@ DEV void wht128_pair(float &v0, float &v1, int lane) {
 template <int KA, int CB, bool MF, int D, bool ROT = false>
 __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh, int M, int K,
                                                const uint32_t *__restrict__ trellis, int N,
-                                               float *__restrict__ yh, int tk_per_wg, int part,
+                                               float *__restrict__ yh, int tk_per_wg,
                                                const uint16_t *__restrict__ suh = nullptr) {
   using TR = Trellis<KA, false>;
   using T32 = Trellis32<KA, false>;
@@ -421,8 +421,8 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
       }
     }
   }
-  // partials: sum over the wave's lane groups (M = 1) and over the workgroup's waves in LDS,
-  // then one atomic add per output, or (part) a store into this split's own [M][N] slice
+  // partials: sum over the wave's lane groups (M = 1) and over the workgroup's waves in LDS, then
+  // a store into this split's own [M][N] slice
   if constexpr (MF) {
     // the waves add their tiles into LDS one after another (fixed order, no atomics)
     for (int v = 0; v < KS; v++) {
@@ -441,9 +441,7 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
       const int t = o >> 8, q = (o >> 6) & 3, l = o & 63;
       const int tk = 4 * (l >> 4) + q;
       if (tk < M) {
-        float *dst = yh + (part ? (size_t)blockIdx.y * M * N : 0) + (size_t)tk * N + (tn0 + t) * 16 + (l & 15);
-        if (part) *dst = red[o];
-        else atomicAdd(dst, red[o]);
+        yh[(size_t)blockIdx.y * M * N + (size_t)tk * N + (tn0 + t) * 16 + (l & 15)] = red[o];
       }
     }
   } else {
@@ -458,16 +456,11 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
     for (int o = threadIdx.x; o < TN * 16; o += blockDim.x) {
       float sum = 0.0f;
       for (int v = 0; v < KS; v++) sum += red[(v * TN + (o >> 4)) * 16 + (o & 15)];
-      float *dst = yh + (part ? (size_t)blockIdx.y * N : 0) + (tn0 + (o >> 4)) * 16 + (o & 15);
-      if (part) *dst = sum;
-      else atomicAdd(dst, sum);
+      yh[(size_t)blockIdx.y * N + (tn0 + (o >> 4)) * 16 + (o & 15)] = sum;
     }
   }
 }
 
-__global__ __launch_bounds__(256) void exl3_zero_kernel(float *__restrict__ p, size_t n) {
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0.0f;
-}
 
 // ------------------------------------------------------------------- dequantize
 template <int KA, bool HALF>
@@ -546,11 +539,15 @@ __global__ __launch_bounds__(256) void exl3_rotate_kernel(const void *__restrict
   store_act(y, base + 1, out_dt, v1);
 }
 
-// yh[m][n] *= rs[m] (the matvec's outputs for a rescaled activation image).
-__global__ __launch_bounds__(256) void exl3_scale_rows_kernel(float *__restrict__ yh, size_t n, int N,
-                                                              const float *__restrict__ rs) {
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-    yh[i] *= rs[i / N];
+// y[m][n] = the S K-split parts summed in split order, times rs[m] when the activations were
+// rescaled into their fp16 image (rs null: not).
+__global__ __launch_bounds__(256) void exl3_sum_parts_kernel(const float *__restrict__ part, int S, size_t n, int N,
+                                                             const float *__restrict__ rs, float *__restrict__ y) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    float s = 0.0f;
+    for (int k = 0; k < S; k++) s += part[(size_t)k * n + i];
+    y[i] = rs ? s * rs[i / N] : s;
+  }
 }
 
 // ------------------------------------------------------------------- host
@@ -627,18 +624,24 @@ extern "C" int ishz_exl3_rotate(const void *x, int in_dtype, int rows, int width
 
 // K splits of the wide-step kernel: about four workgroups per CU for one row, two with MFMA rows
 // (tn_blocks workgroups per split), at most 64.
+static int exl3_splits(int M, int K, int tn_blocks);
+// Floats the matvec's K-split parts take at most: the split count of the fewest column blocks (32
+// tiles per step at 1 bit) times M N.
+static size_t exl3_part_floats(int M, int K, int N) {
+  return (size_t)std::max(1, exl3_splits(M, K, std::max(1, N / 16 / 32))) * M * N;
+}
 static int exl3_splits(int M, int K, int tn_blocks) {
   const int tiles_k = K / 16;
   return std::max(1, std::min({tiles_k / 4, (M == 1 ? 4 : 2) * num_cu_e() / tn_blocks, 64}));
 }
 
-// The matvec. With `part` (a buffer of exl3_splits(..) * M * N floats) the wide-step kernel writes
-// each K split's partial product to its own slice and *nparts says how many; otherwise yh is the
-// result (zeroed, then summed into with atomics) and *nparts = 1.
+// The matvec into `part` (exl3_part_floats(M, K, N) floats): the wide-step kernel writes each K
+// split's partial product to its own [M][N] slice and *nparts says how many; the other kernels
+// write the whole product to the first slice and *nparts = 1.
 // With `suh` (exl3_fused_rotation(..) true) xh is the unrotated x and the wide-step kernel
 // rotates it itself.
 static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis, int N, int bits2, int codebook,
-                            float *yh, float *part, int *nparts, hipStream_t st, const uint16_t *suh = nullptr) {
+                            float *part, int *nparts, hipStream_t st, const uint16_t *suh = nullptr) {
   *nparts = 1;
   const int wgs = N / 16, tiles_k = K / 16;
   int ks = 1;
@@ -650,27 +653,23 @@ static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis
         const int tn_blocks = N / 16 / TN;
         const int per = (tiles_k + exl3_splits(M, K, tn_blocks) - 1) / exl3_splits(M, K, tn_blocks);
         const int nsplit = (tiles_k + per - 1) / per;
-        const size_t n = (size_t)M * N;
-        float *out = part ? part : yh;
-        if (part) *nparts = nsplit;
-        else
-          hipLaunchKernelGGL(exl3_zero_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 1024)), dim3(256), 0,
-                             st, yh, n);
+        float *out = part;
+        *nparts = nsplit;
         const size_t lds = (size_t)KS3 * 256 * 4 + (M == 1 ? (size_t)KS3 * TN * 16 * 4 : (size_t)TN * 256 * 4) +
                            (suh ? (size_t)M * (per * 16 + 256) * 2 : 0);  // ROT: the rotated K range of x
         auto go = [&]<int CB>() -> int {
           if (M == 1 && suh)
             hipLaunchKernelGGL((exl3_mm3<KA, CB, false, D, true>), dim3(tn_blocks, nsplit), dim3(64 * KS3), lds, st,
-                               (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per, part ? 1 : 0, suh);
+                               (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per, suh);
           else if (M == 1)
             hipLaunchKernelGGL((exl3_mm3<KA, CB, false, D>), dim3(tn_blocks, nsplit), dim3(64 * KS3), lds, st,
-                               (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per, part ? 1 : 0);
+                               (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per);
           else if (suh)
             hipLaunchKernelGGL((exl3_mm3<KA, CB, true, D, true>), dim3(tn_blocks, nsplit), dim3(64 * KS3), lds, st,
-                               (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per, part ? 1 : 0, suh);
+                               (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per, suh);
           else
             hipLaunchKernelGGL((exl3_mm3<KA, CB, true, D>), dim3(tn_blocks, nsplit), dim3(64 * KS3), lds, st,
-                               (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per, part ? 1 : 0);
+                               (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per);
           ISHZ_LAUNCH_CHECK("exl3 matvec launch");
           return ISHZ_OK;
         };
@@ -689,10 +688,10 @@ static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis
           auto launch = [&]<int D>() {
             if (M == 1)
               hipLaunchKernelGGL((exl3_mm2<KA, HALF, CB, false, TN, D>), dim3(N / 16 / TN), dim3(64 * KS2), lds,
-                                 st, (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, yh);
+                                 st, (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, part);
             else
               hipLaunchKernelGGL((exl3_mm2<KA, HALF, CB, true, TN, D>), dim3(N / 16 / TN), dim3(64 * KS2), lds,
-                                 st, (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, yh);
+                                 st, (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, part);
           };
           launch.template operator()<4>();
           ISHZ_LAUNCH_CHECK("exl3 matvec launch");
@@ -704,10 +703,10 @@ static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis
     }
     if (M == 1)
       hipLaunchKernelGGL((exl3_mm<KA, HALF, false>), dim3(wgs), dim3(64 * ks), (size_t)ks * 16 * 4,
-                         st, (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, codebook, yh);
+                         st, (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, codebook, part);
     else
       hipLaunchKernelGGL((exl3_mm<KA, HALF, true>), dim3(wgs), dim3(64 * ks), (size_t)ks * 256 * 4,
-                         st, (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, codebook, yh);
+                         st, (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, codebook, part);
     ISHZ_LAUNCH_CHECK("exl3 matvec launch");
     return ISHZ_OK;
   });
@@ -726,14 +725,16 @@ extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const
   const uint16_t *x16;
   const float *rs;
   if ((rc = act_prepare(xh, x_dtype, M, K, tmp.p, st, &x16, &rs))) return rc;
+  // the K splits' partial products, then their sum in split order: the same bits on every call
+  StreamTemp parts(st);
+  if ((rc = parts.get(exl3_part_floats(M, K, N) * 4))) return rc;
+  float *pp = (float *)parts.p;
   int np;
-  if ((rc = exl3_matvec_core(x16, M, K, trellis, N, bits2, codebook, yh, nullptr, &np, st))) return rc;
-  if (rs) {
-    const size_t n = (size_t)M * N;
-    hipLaunchKernelGGL(exl3_scale_rows_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 1024)), dim3(256), 0,
-                       st, yh, n, N, rs);
-    ISHZ_LAUNCH_CHECK("exl3 scale launch");
-  }
+  if ((rc = exl3_matvec_core(x16, M, K, trellis, N, bits2, codebook, pp, &np, st))) return rc;
+  const size_t n = (size_t)M * N;
+  hipLaunchKernelGGL(exl3_sum_parts_kernel, dim3((unsigned)std::min<size_t>((n + 255) / 256, 1024)), dim3(256), 0, st,
+                     pp, np, n, N, rs, yh);
+  ISHZ_LAUNCH_CHECK("exl3 sum launch");
   return ISHZ_OK;
 }
 
@@ -758,8 +759,7 @@ static bool exl3_fused_rotation(int M, int K, int N, int bits2) {
 // widest column step of any rate, 32 tiles).
 static size_t exl3_rot_bytes(int M, int K) { return ((size_t)M * K * 4 + 255) / 256 * 256; }
 extern "C" size_t ishz_exl3_workspace_size(int M, int K, int N) {
-  const int most = std::max(1, exl3_splits(M, K, std::max(1, N / 16 / 32)));
-  return exl3_rot_bytes(M, K) + act_image_bytes(M, K) + (size_t)most * M * N * 4;
+  return exl3_rot_bytes(M, K) + act_image_bytes(M, K) + exl3_part_floats(M, K, N) * 4;
 }
 
 // Device scratch of ishz_exl3_apply_static: every GPU the library runs on holds its own copy
@@ -810,14 +810,14 @@ extern "C" int ishz_exl3_apply(const void *x, int x_dtype, int M, int K, const i
   int np = 1;
   const float *rs = nullptr;
   if (x_dtype == ISHZ_DT_F16 && exl3_fused_rotation(M, K, N, bits2)) {  // the matvec rotates its own K range of x
-    if ((rc = exl3_matvec_core(x, M, K, trellis, N, bits2, codebook, yh, yh, &np, st, suh))) return rc;
+    if ((rc = exl3_matvec_core(x, M, K, trellis, N, bits2, codebook, yh, &np, st, suh))) return rc;
   } else {
     // rotated into x's dtype (EXL3Kernels.apply rotates `to: x.dtype`, Core/EXL3.swift:85), then
     // (bf16 / fp32) its fp16 image
     if ((rc = ishz_exl3_rotate(x, x_dtype, M, K, suh, 1, xr, x_dtype, stream))) return rc;
     const uint16_t *x16;
     if ((rc = act_prepare(xr, x_dtype, M, K, img, st, &x16, &rs))) return rc;
-    if ((rc = exl3_matvec_core(x16, M, K, trellis, N, bits2, codebook, yh, yh, &np, st))) return rc;
+    if ((rc = exl3_matvec_core(x16, M, K, trellis, N, bits2, codebook, yh, &np, st))) return rc;
   }
   const size_t blocks = (size_t)M * (N / 128);  // output rotation, summing the K-split partials
   hipLaunchKernelGGL(exl3_rotate_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, st, yh,

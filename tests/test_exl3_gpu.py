@@ -81,6 +81,21 @@ def test_matvec(M, bits2, cb):
     assert_close(y.cpu().numpy(), ref, bound=bd, what=f"exl3 matvec M={M} bits2={bits2} cb={cb}")
 
 
+@pytest.mark.parametrize("M", [1, 5])
+def test_matvec_is_deterministic(M):
+    """K split over many workgroups (K = 5120, N = 1024: dozens of parts): the parts are summed in
+    split order, so repeated calls give the same bits; the result matches the oracle."""
+    K, N = 5120, 1024
+    t, _, _, ten = make(K, N, 4, 0, seed=70 + M)
+    xh = torch.from_numpy(synth.fp16_normal((M, K), seed=71 + M)).to(DEV)
+    ys = [exl3.matvec(xh, ten) for _ in range(3)]
+    for y in ys[1:]:
+        assert torch.equal(y.view(torch.int32), ys[0].view(torch.int32))
+    w = oracle.exl3_dequant(t, 4, 0)
+    xf = xh.float().cpu().numpy()
+    assert_close(ys[0].cpu().numpy(), xf @ w, bound=np.abs(xf) @ np.abs(w), what=f"exl3 deterministic M={M}")
+
+
 @pytest.mark.parametrize("M", [1, 3])
 @pytest.mark.parametrize("bits2,N", [(2, 384), (4, 384), (2, 640), (8, 128)])
 def test_matvec_n_not_a_multiple_of_the_wide_step(M, bits2, N):
