@@ -68,23 +68,23 @@ def test_swiglu_small(T, type_):
     assert_close(y.float().cpu().numpy(), ref, bound=bd, elem=MOE_ELEM, what=f"moe T={T}")
 
 
-@pytest.mark.parametrize("T", [3, 16])
-def test_swiglu_routing_inside_gate_up(T):
+@pytest.mark.parametrize("T,E,k", [(3, 4, 2), (16, 4, 2), (16, 64, 16)])
+def test_swiglu_routing_inside_gate_up(T, E, k):
     """Three to sixteen tokens: every gate/up workgroup routes and places the pairs itself and
-    workgroup (0, 0) publishes them. Few experts (about T k / 4 pairs each) and a wide I (several
-    workgroups per expert, which must agree on the pair order); the published ids and weights are
-    checked too."""
-    E, H, I, k = 4, 512, 1024, 2
-    (g, u, d), ex = experts(E, H, I, ggml.Q4_K, seed=90 + T)
+    workgroup (0, 0) publishes them. Few experts (about T k / E pairs each) and a wide I (several
+    workgroups per expert, which must agree on the pair order), and the largest pair count this
+    path takes (T k = 256); the published ids and weights are checked too."""
+    H, I = 512, 1024
+    (g, u, d), ex = experts(E, H, I, ggml.Q4_K, seed=90 + T + k)
     x = synth.fp16_normal((T, H), seed=91 + T)
-    logits = np.random.default_rng(92 + T).standard_normal((T, E)).astype(np.float32)
+    logits = np.random.default_rng(92 + T + k).standard_normal((T, E)).astype(np.float32)
     y, ids, w = moe.swiglu(torch.from_numpy(x).to(DEV), torch.from_numpy(logits).to(DEV), ex, top_k=k,
                            return_routing=True)
     rid, rw = oracle.moe_route(logits, k)
     assert np.array_equal(ids.cpu().numpy(), rid)
     assert np.allclose(w.cpu().numpy(), rw, rtol=1e-6, atol=1e-7)
     ref, bd = moe_reference(ggml.Q4_K, x.astype(np.float32), rid, rw, g, u, d, E, I)
-    assert_close(y.float().cpu().numpy(), ref, bound=bd, elem=MOE_ELEM, what=f"moe routed in gate/up T={T}")
+    assert_close(y.float().cpu().numpy(), ref, bound=bd, elem=MOE_ELEM, what=f"moe routed in gate/up T={T} E={E} k={k}")
 
 
 def test_swiglu_many_tokens_per_expert():
