@@ -438,10 +438,11 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16 activations, 2-bit affine codes (fp32 accumulate)",
+        "dtype": "f16",  # the dot's operands (x and the decoded weights); sums in fp32, codes 2-bit
         "data": "synthetic (seeded): BASELINE configs[1] distributions",
         "config": {"workload": "MLX affine 2-bit g64 + 128-pt WHT GEMV, 17408x5120, M=1 (BASELINE configs[1])",
                    "N": NS, "K": KS, "M": 1, "group": 64, "hadamard_block": 128,
+                   "arith": "fp16 x and decoded weights, fp32 accumulation, 2-bit codes",
                    "weight_bytes": head["weight_bytes"], "cache_defeat_bytes": int(CACHE_DEFEAT)},
         # dominant (and only) kernel of the headline call: gemv_kernel<FAffine<64, false>>, HIP
         # events over graph replays; algorithmic bytes = codes + scales + biases. read_ceiling: a
