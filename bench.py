@@ -145,7 +145,7 @@ def main():
         return policy()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the kernels shard by "
-              "output rows; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "output rows, each GPU its own slice of y). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch
@@ -426,7 +426,7 @@ def main():
 
     us = head_sec * 1e6
     line = {
-        "metric": "weight-stream GB/s (% HBM peak) + us per quant matmul at M=1 and M=8",
+        "metric": "weight-stream GB/s (% HBM peak) + µs per quant matmul at M=1 and M=8",
         "value": head["GBps"],
         "unit": "GB/s",
         "n_gpus": 1,
