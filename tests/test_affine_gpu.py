@@ -189,14 +189,11 @@ def test_affine_random_shapes(N, K, M, group, block):
     assert_close(y.float().cpu().numpy(), ref, bound=bd, what=f"affine random N={N} K={K} M={M} g={group} b={block}")
 
 
-@pytest.mark.parametrize("block", [2, 32, 64, 128, 512])
+@pytest.mark.parametrize("block,K", [(b, K) for K in (1152, 5120) for b in (2, 32, 64, 128, 512) if K % b == 0])
 @pytest.mark.parametrize("prestage", [True, False])
-@pytest.mark.parametrize("K", [1152, 5120])
 def test_affine_rotated_gemv_staging(block, prestage, K):
     """M = 1 with x staged by the prestage kernel or inside every workgroup; K = 1152 leaves a
-    partial 512-value pass."""
-    if K % block:
-        pytest.skip("the rotation block must divide K")
+    partial 512-value pass (rotation blocks that divide K only)."""
     N = 700
     (x, w, s, b), signs, (ref, bd) = affine_case(N, K, 1, 64, seed=block + K, block=block, signs_seed=3)
     y = affine.linear(x, w, s, b, signs=torch.from_numpy(signs), block=block, group_size=64, _prestage=prestage)
