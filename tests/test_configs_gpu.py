@@ -86,3 +86,58 @@ def test_config3_exl3_2bpw():
         y = exl3.apply(torch.from_numpy(x[:M]).to(DEV), ten)
         assert y is not None
         assert_close(y.float().cpu().numpy(), ref[:M], bound=bound[:M], elem=APPLY_ELEM, what=f"exl3 5120->17408 M={M}")
+
+
+
+def _properties(f, x1, x2, bound_of, rel, what, exact_scale=True):
+    """Size-independent checks of a linear map at full size, no oracle product needed: doubling x
+    doubles y, and y(x1 + x2) = y(x1) + y(x2) within rel of the two products' per-element bounds
+    plus the fp16 roundings of the three outputs. exact_scale: scaling by 2 is exact through every
+    fp16 rounding and fp32 sum on the path (2^-22 absolute slack for subnormals); otherwise the
+    doubling is held to the same tolerance as the sum."""
+    y1, y2 = f(x1).float(), f(x2).float()
+    yd = f(x1 * 2).float()
+    y1n, y2n = y1.cpu().numpy(), y2.cpu().numpy()
+    if exact_scale:
+        assert (yd - 2 * y1).abs().max().item() <= 2.0 ** -22, f"{what}: y(2x) != 2 y(x)"
+    else:
+        err2 = np.abs(yd.cpu().numpy() - 2 * y1n)
+        assert np.all(err2 <= rel * 2 * bound_of(x1) + 2.0 ** -9 * 2 * np.abs(y1n) + 1e-6), f"{what}: y(2x) != 2 y(x)"
+    ys = f(x1 + x2).float()
+    err = np.abs(ys.cpu().numpy() - (y1n + y2n))
+    tol = rel * (bound_of(x1) + bound_of(x2)) + 2.0 ** -9 * (np.abs(y1n) + np.abs(y2n)) + 1e-6
+    assert np.all(err <= tol), f"{what}: not additive (worst {np.max(err / tol):.2f} of the tolerance)"
+
+
+@pytest.mark.parametrize("t", [ggml.Q4_K, ggml.IQ2_XS])
+@pytest.mark.parametrize("M", [1, 8])
+def test_north_star_linearity(t, M):
+    N, K = 17408, 5120
+    blk = synth.ggml_blocks(t, N, K, seed=77)
+    wb = torch.from_numpy(blk).to(DEV)
+    w_abs_t = np.abs(oracle.dequant_rows(t, blk, N, K)).T.copy()
+    x1 = torch.from_numpy(synth.fp16_normal((M, K), seed=78)).to(DEV)
+    x2 = torch.from_numpy(synth.fp16_normal((M, K), seed=79)).to(DEV)
+    bound_of = lambda x: np.abs(x.float().cpu().numpy()) @ w_abs_t
+    print(f"linearity ggml type={t} M={M}", flush=True)
+    # fp32 sums in another order and the fp16 output: 2e-4 of sum |x||w|
+    _properties(lambda x: ggml.matvec(x, wb, t, N), x1, x2, bound_of, 2e-4, f"type={t} M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 8])
+def test_config1_affine_linearity(M):
+    N, K = 17408, 5120
+    codes, sc, bi = synth.affine_pack(N, K, group=64, seed=80)
+    signs = synth.hadamard_signs(K, seed=81)
+    w_abs_t = np.abs(oracle.affine_dequant(codes, sc.view(np.uint16), bi.view(np.uint16), N, K, 2, 64)).T.copy()
+    wd, sd, bd = (torch.from_numpy(a).to(DEV) for a in (codes.view(np.int32), sc, bi))
+    x1 = torch.from_numpy(synth.fp16_normal((M, K), seed=82)).to(DEV)
+    x2 = torch.from_numpy(synth.fp16_normal((M, K), seed=83)).to(DEV)
+    rot = lambda x: oracle.hadamard(x.float().cpu().numpy(), 128, signs)
+    bound_of = lambda x: np.abs(rot(x)) @ w_abs_t
+    print(f"linearity affine M={M}", flush=True)
+    # each rotated x is rounded to fp16 on its own (three roundings of up to 2^-11): 2e-3 of the
+    # bound; the image holds x / 4^i (i < 5), subnormal for the smallest x, so doubling is exact
+    # only to that tolerance
+    _properties(lambda x: affine.linear(x, wd, sd, bd, signs=torch.from_numpy(signs), block=128, group_size=64),
+                x1, x2, bound_of, 2e-3, f"affine M={M}", exact_scale=False)
