@@ -311,6 +311,7 @@ struct FQ4_0 : GgmlGemv<FQ4_0> {
     off1 = 1024.0f * X;
   }
   static constexpr float voff() { return 1024.0f; }  // off1 of vstage, per unit of X
+  static constexpr float vkappa(int s) { return (s & 1) ? -128.0f : -8.0f; }  // mn = vkappa sc
   static DEV void vscale(const VRaw &r, int, int s, float &sc, float &mn) {
     const float d = h2f(s >> 1 ? r.b.x >> 16 : r.a.x & 0xffff);
     sc = (s & 1) ? 0.0625f * d : d;
@@ -611,6 +612,7 @@ struct FQ6_K : GgmlGemv<FQ6_K> {
     off1 = 1024.0f * X;
   }
   static constexpr float voff() { return 1024.0f; }  // off1 of vstage, per unit of X
+  static constexpr float vkappa(int) { return -32.0f; }  // mn = -32 sc
   static DEV void vscale(const VRaw &r, int g, int s, float &sc, float &mn) {
     const int bi = 8 * (g >> 1) + (g & 1) + 2 * s;  // scale byte
     const float d = h2f(r.d) * (float)(int8_t)(r.sc[bi >> 2] >> (8 * (bi & 3)));

@@ -29,6 +29,9 @@
 //   VPLAIN (optional, true)          off1 and mn are always zero: value = sc * C, so the epilogue
 //                                    reads no sums
 //   voff() (optional)                off1 is always voff() * X: the epilogue reads X only
+//   vkappa(s) (optional, with voff)  mn is always vkappa(s) * sc: staging stores the sub-unit's
+//                                    (vkappa - voff) X as the MFMA chain's initial C, and the
+//                                    epilogue is sc * C alone
 #pragma once
 #include <algorithm>
 #include <cstdlib>
@@ -41,6 +44,10 @@ template <class F>
 __host__ __device__ constexpr bool vgemm_plain() {
   if constexpr (requires { F::VPLAIN; }) return F::VPLAIN;
   else return false;
+}
+template <class F>
+__host__ __device__ constexpr bool vgemm_kappa() {
+  return requires { F::vkappa(0); };
 }
 
 // What is multiplied: a "problem" P supplies, per workgroup row blockIdx.y (a group: the whole
@@ -111,7 +118,8 @@ __global__ __launch_bounds__(64 * NW) void vgemm_kernel(P p, int K, int Kc, int 
           for (int b = 0; b < MPS; b++) dst[b] = A[b];
         }
         float *sp = sums + (((j * 4 + g) * NS + s) * 2) * MT;
-        sp[tk] = off1;
+        if constexpr (vgemm_kappa<F>()) sp[tk] = F::vkappa(s) * X - off1;  // the chain's initial C
+        else sp[tk] = off1;
         sp[MT + tk] = X;
       }
       __syncthreads();
@@ -172,9 +180,11 @@ __global__ __launch_bounds__(64 * NW) void vgemm_kernel(P p, int K, int Kc, int 
 #pragma unroll
             for (int s = 0; s < NS; s++) {
               f4 C = f4{0, 0, 0, 0};
+              if constexpr (vgemm_kappa<F>())  // (vkappa - voff) X: sc C is then the sub-unit's value
+                C = *(const f4 *)(sums + (((j * 4 + G) * NS + s) * 2) * MT + 4 * q);
 #pragma unroll
               for (int b = 0; b < MPS; b++) C = mfma32(as_h8(ab[s * MPS + b]), as_h8(B[s * MPS + b]), C);
-              if constexpr (vgemm_plain<F>()) {
+              if constexpr (vgemm_plain<F>() || vgemm_kappa<F>()) {
 #pragma unroll
                 for (int e = 0; e < 4; e++) acc[q][e] = fmaf(sc[s], C[e], acc[q][e]);
               } else if constexpr (requires { F::voff(); }) {
