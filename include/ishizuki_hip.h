@@ -27,13 +27,16 @@ typedef void *ishz_stream_t; /* hipStream_t */
 enum { ISHZ_OK = 0, ISHZ_DECLINED = 1, ISHZ_EINVAL = 2, ISHZ_EHIP = 3 };
 
 /* Element types of activations and outputs. The matmuls take x in any of them and write y in
-   x's dtype, as the reference's kernels templated on the activation type do. Their kernels
-   stage fp16: bf16 / fp32 x is first converted into an fp16 image with a power-of-two factor
-   per row (the row's largest value lands in [0.5, 1); outputs are multiplied back, exactly,
-   before their one narrowing to x's dtype). bf16 values convert exactly down to 2^-17 of their
-   row's largest; fp32 values round to fp16. The image lives in the call's workspace where the
-   entry point takes one, else in a stream-ordered temporary (hipMallocAsync). The MoE FFN takes
-   fp16 x only. */
+   x's dtype, as the reference's kernels templated on the activation type do.
+   - fp16 x: the fp16 kernels (x staged in fp16, fp32 accumulation).
+   - bf16 x: the same kernels on an fp16 image of x with a power-of-two factor per row (the
+     row's largest value lands in [0.5, 1); outputs are multiplied back, exactly, before their
+     one narrowing). bf16 values convert exactly down to 2^-17 of their row's largest. The image
+     lives in the call's workspace where the entry point takes one, else in a stream-ordered
+     temporary (hipMallocAsync).
+   - fp32 x: fp32 precision. Every weight is decoded to its exact fp32 value and dotted with the
+     fp32 x by fp32 FMAs (no image, no temporary), as the reference accumulates fp32 x in fp32.
+   The MoE FFN takes fp16 x only. */
 enum { ISHZ_DT_F32 = 0, ISHZ_DT_F16 = 1, ISHZ_DT_BF16 = 2 };
 
 /* GGML storage types, numbered as GGMLType's raw values (Config/GGUFFile.swift:13-43). */

@@ -18,6 +18,7 @@
 #include "affine_nbit.h"
 #include "common.h"
 #include "gemv.h"
+#include "precise.h"
 
 namespace ishz {
 // hadamardRotate as a kernel. Blocks up to 128: one wave per 128 contiguous values, two per
@@ -455,6 +456,39 @@ static int affine_verify_launch(const void *x, int M, int K, const uint32_t *cod
   return ISHZ_OK;
 }
 
+// fp32 activations (precise.h): w = s * q + b in fp32 (mul, then add: the oracle's and MLX's
+// dequantize), q the bits-wide field k of the row's little-endian u32 stream.
+struct AffDec {
+  struct Args {
+    const uint32_t *codes;
+    const uint16_t *scales, *biases;
+    int K, bits, group;
+    bool bf16s;
+  };
+  static DEV void decode(const Args &a, int row, int s, float *v) {
+    const size_t wpr = (size_t)a.K * a.bits / 32;
+    const uint32_t *rw = a.codes + (size_t)row * wpr;
+    const size_t g = (size_t)row * (a.K / a.group) + (size_t)(8 * s) / a.group;
+    const float sc = ld_scale(a.scales + g, a.bf16s), bi = ld_scale(a.biases + g, a.bf16s);
+    const uint32_t mask = (1u << a.bits) - 1;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const size_t bit = (size_t)(8 * s + i) * a.bits;
+      const size_t w = bit / 32;
+      const int off = (int)(bit % 32);
+      uint32_t q = rw[w] >> off;
+      if (off + a.bits > 32) q |= rw[w + 1] << (32 - off);
+      v[i] = __fadd_rn(__fmul_rn(sc, (float)(q & mask)), bi);
+    }
+  }
+};
+
+static int affine_precise(const float *x, int M, int K, const uint32_t *codes, const void *scales, const void *biases,
+                          int bf16s, int N, int bits, int group, void *y, hipStream_t st) {
+  const AffDec::Args a{codes, (const uint16_t *)scales, (const uint16_t *)biases, K, bits, group, bf16s != 0};
+  return launch_precise<AffDec>(a, x, M, K, N, y, ISHZ_DT_F32, st);
+}
+
 static int check_affine(const void *x, int x_dtype, int M, int K, const void *codes,
                         const void *scales, const void *biases, int scale_dtype, int N, int bits,
                         int group, const void *y) {
@@ -532,7 +566,10 @@ extern "C" int ishz_affine_matmul(const void *x, int x_dtype, int M, int K, cons
   int rc = check_affine(x, x_dtype, M, K, codes, scales, biases, scale_dtype, N, bits, group, y);
   if (rc) return rc;
   hipStream_t st = S(stream);
-  StreamTemp tmp(st);  // bf16 / fp32 activations: their fp16 image
+  if (x_dtype == ISHZ_DT_F32)
+    return affine_precise((const float *)x, M, K, codes, scales, biases, scale_dtype == ISHZ_DT_BF16, N, bits, group,
+                          y, st);
+  StreamTemp tmp(st);  // bf16 activations: their fp16 image
   if (x_dtype != ISHZ_DT_F16 && (rc = tmp.get(act_image_bytes(M, K)))) return rc;
   const uint16_t *xh;
   const float *rs;
@@ -575,6 +612,7 @@ extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, cons
       xr = workspace;
       img = (char *)workspace + (size_t)M * K * 4;
     }
+    if (x_dtype == ISHZ_DT_F32) return affine_precise((const float *)xr, M, K, codes, scales, biases, bf16s, N, bits, group, y, st);
     const uint16_t *xh;
     const float *rs;
     if ((rc = act_prepare(xr, x_dtype, M, K, img, st, &xh, &rs))) return rc;

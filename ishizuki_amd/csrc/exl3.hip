@@ -128,6 +128,58 @@ __global__ __launch_bounds__(1024) void exl3_mm(const uint16_t *__restrict__ xh,
   }
 }
 
+// fp32 activations at fp32 precision (EXL3Kernels.matvec templated on the activation type,
+// Core/EXL3.swift:286-330): each weight's exact fp16 decode, widened, times fp32 x in fp32 FMAs,
+// for up to 16 token rows. The work split of exl3_mm: a workgroup per column tile, its waves
+// taking K tiles round-robin; lane (j, g) holds rows 2g + {0, 1, 8, 9} of column j.
+template <int KA, bool HALF>
+__global__ __launch_bounds__(256) void exl3_mm_f32(const float *__restrict__ x, int M, int K,
+                                                   const uint32_t *__restrict__ trellis, int N, int cb,
+                                                   float *__restrict__ yh) {
+  using TR = Trellis<KA, HALF>;
+  __shared__ float red[4][16][16];
+  const int lane = threadIdx.x & 63, wave = wave_id(), KS = blockDim.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int tn = blockIdx.x, tiles_n = N / 16, tiles_k = K / 16;
+  const int p0 = 8 * (4 * (j & 7) + g) + 4 * (j >> 3);
+  const uint32_t *col = trellis + (size_t)tn * TR::WORDS;
+  const size_t tstride = (size_t)tiles_n * TR::WORDS;
+  float acc[16];
+#pragma unroll
+  for (int m = 0; m < 16; m++) acc[m] = 0.0f;
+  for (int tk = wave; tk < tiles_k; tk += KS) {
+    const u2 B = TR::decode4(col + tk * tstride, p0, cb);
+    const float w0 = h2f(B.x & 0xffffu), w1 = h2f(B.x >> 16), w2 = h2f(B.y & 0xffffu), w3 = h2f(B.y >> 16);
+    const float *xr = x + 16 * tk + 2 * g;
+#pragma unroll
+    for (int m = 0; m < 16; m++) {
+      if (m >= M) continue;
+      const float2 a = *(const float2 *)(xr + (size_t)m * K), b = *(const float2 *)(xr + (size_t)m * K + 8);
+      float t = acc[m];
+      t = __builtin_fmaf(w0, a.x, t);
+      t = __builtin_fmaf(w1, a.y, t);
+      t = __builtin_fmaf(w2, b.x, t);
+      t = __builtin_fmaf(w3, b.y, t);
+      acc[m] = t;
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 16; m++) {
+    if (m >= M) continue;
+    float v = acc[m];
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    if (g == 0) red[wave][m][j] = v;
+  }
+  __syncthreads();
+  for (int o = threadIdx.x; o < M * 16; o += blockDim.x) {
+    const int m = o >> 4, jj = o & 15;
+    float v = 0.0f;
+    for (int w = 0; w < KS; w++) v += red[w][m][jj];
+    yh[(size_t)m * N + tn * 16 + jj] = v;
+  }
+}
+
 // ------------------------------------------------------------------- streaming matvec / verify
 // For rates whose four lane states span at most 32 bits: a lane's window is one v_alignbit of
 // two tile words, each state one bit-field extract, and two weights are decoded per packed fp16
@@ -712,6 +764,17 @@ static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis
   });
 }
 
+// y [M][N] fp32 from fp32 x (one slice, no K split).
+static int exl3_matvec_f32(const float *x, int M, int K, const int16_t *trellis, int N, int bits2, int cb,
+                           float *yh, hipStream_t st) {
+  return by_rate(bits2, [&]<int KA, bool HALF>() -> int {
+    hipLaunchKernelGGL((exl3_mm_f32<KA, HALF>), dim3(N / 16), dim3(256), 0, st, x, M, K, (const uint32_t *)trellis,
+                       N, cb, yh);
+    ISHZ_LAUNCH_CHECK("exl3 fp32 matvec launch");
+    return ISHZ_OK;
+  });
+}
+
 extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const int16_t *trellis,
                                 int N, int bits2, int codebook, float *yh, ishz_stream_t stream) {
   int rc = check_exl3(K, N, bits2, codebook);
@@ -720,7 +783,8 @@ extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const
   if (M < 1 || M > 16) return decline("row count outside 1..16");
   if (!xh || !trellis || !yh) return einval("null pointer");
   hipStream_t st = S(stream);
-  StreamTemp tmp(st);  // bf16 / fp32 activations: their fp16 image
+  if (x_dtype == ISHZ_DT_F32) return exl3_matvec_f32((const float *)xh, M, K, trellis, N, bits2, codebook, yh, st);
+  StreamTemp tmp(st);  // bf16 activations: their fp16 image
   if (x_dtype != ISHZ_DT_F16 && (rc = tmp.get(act_image_bytes(M, K)))) return rc;
   const uint16_t *x16;
   const float *rs;
@@ -815,9 +879,13 @@ extern "C" int ishz_exl3_apply(const void *x, int x_dtype, int M, int K, const i
     // rotated into x's dtype (EXL3Kernels.apply rotates `to: x.dtype`, Core/EXL3.swift:85), then
     // (bf16 / fp32) its fp16 image
     if ((rc = ishz_exl3_rotate(x, x_dtype, M, K, suh, 1, xr, x_dtype, stream))) return rc;
-    const uint16_t *x16;
-    if ((rc = act_prepare(xr, x_dtype, M, K, img, st, &x16, &rs))) return rc;
-    if ((rc = exl3_matvec_core(x16, M, K, trellis, N, bits2, codebook, yh, &np, st))) return rc;
+    if (x_dtype == ISHZ_DT_F32) {  // fp32 precision: exact weights, fp32 FMAs
+      if ((rc = exl3_matvec_f32((const float *)xr, M, K, trellis, N, bits2, codebook, yh, st))) return rc;
+    } else {
+      const uint16_t *x16;
+      if ((rc = act_prepare(xr, x_dtype, M, K, img, st, &x16, &rs))) return rc;
+      if ((rc = exl3_matvec_core(x16, M, K, trellis, N, bits2, codebook, yh, &np, st))) return rc;
+    }
   }
   const size_t blocks = (size_t)M * (N / 128);  // output rotation, summing the K-split partials
   hipLaunchKernelGGL(exl3_rotate_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, st, yh,

@@ -2,6 +2,7 @@
 // gather writers. Replaces GGMLKernels (Sources/IshizukiKit/Core/GGMLKernels.swift).
 #include "ggml_formats.h"
 #include "vgemm.h"
+#include "precise.h"
 
 #include <cstdlib>
 
@@ -270,6 +271,18 @@ __global__ __launch_bounds__(256) void gather_kernel(const int32_t *__restrict__
   }
 }
 
+// fp32 activations (precise.h): a row's slices decoded by decode8, the CPU decoder's values.
+template <uint32_t TYPE, int BS, int TS>
+struct GgmlDec {
+  struct Args {
+    const uint8_t *w;
+    size_t rb;  // bytes per row
+  };
+  static DEV void decode(const Args &a, int row, int s, float *v) {
+    decode8<TYPE>(a.w + (size_t)row * a.rb + (size_t)(s * 8 / BS) * TS, s % (BS / 8), v);
+  }
+};
+
 // ----------------------------------------------------------------------------- host
 // The types with a GPU decoder (GGMLDequant.supported, Core/GGMLDequant.swift:19-24, plus Q4_0).
 #define ISHZ_GGML_FORMATS(X)                                                                     \
@@ -394,6 +407,17 @@ extern "C" size_t ishz_ggml_workspace_size(uint32_t type, int M, int K, int N) {
 // x (any activation dtype) -> fp16 image; then the product with outputs in x's dtype.
 static int ggml_call(uint32_t type, const void *x, int x_dtype, int M, int K, const void *blocks, int N, void *y,
                      void *workspace, size_t workspace_bytes, hipStream_t st, bool few) {
+  if (x_dtype == ISHZ_DT_F32) {  // fp32 x at fp32 precision: exact fp32 weights, fp32 FMAs
+    switch (type) {
+#define X(T, F)                                                                                              \
+  case T:                                                                                                    \
+    return launch_precise<GgmlDec<T, F::BS, F::TS>>({(const uint8_t *)blocks, (size_t)(K / F::BS) * F::TS},   \
+                                                    (const float *)x, M, K, N, y, ISHZ_DT_F32, st);
+      ISHZ_GGML_FORMATS(X)
+#undef X
+    }
+    return decline("unsupported GGML type");
+  }
   StreamTemp tmp(st);
   void *img = workspace;
   size_t left = workspace_bytes;

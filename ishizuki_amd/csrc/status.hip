@@ -35,8 +35,13 @@ __global__ __launch_bounds__(256) void act_half_kernel(const void *__restrict__ 
   if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
   __syncthreads();
   m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  // m = f 2^e, f in [0.5, 1), for every finite non-zero m; e capped at 127 so that 2^e stays a
+  // finite fp32 factor (a row whose largest value lies in (2^127, FLT_MAX] lands in [0.5, 2))
   int e = 0;
-  if (m > 0.0f && m <= 3.0e38f) (void)frexpf(m, &e);  // m = f 2^e, f in [0.5, 1)
+  if (m > 0.0f && __builtin_isfinite(m)) {
+    (void)frexpf(m, &e);
+    e = e > 127 ? 127 : e;
+  }
   const float down = ldexpf(1.0f, -e);
   for (int k = threadIdx.x; k < K; k += blockDim.x) xh[row + k] = f2h(load_act(x, row + k, dt) * down);
   if (threadIdx.x == 0) rs[blockIdx.x] = ldexpf(1.0f, e);
