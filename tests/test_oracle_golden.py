@@ -105,6 +105,51 @@ def test_exl3_projection_reproduces_checkpoint(golden_exl3, name, cb):
     assert err < 0.12
 
 
+def _f16_round_pinned(pre, err):
+    """fp16(v) for v within err of pre, where that rounding is determined (no fp16 rounding boundary
+    inside [pre - err, pre + err]); NaN where either neighbour may come out."""
+    lo = (pre - err).astype(np.float16).astype(np.float64)
+    hi = (pre + err).astype(np.float16).astype(np.float64)
+    return np.where(lo == hi, lo, np.nan)
+
+
+@pytest.mark.parametrize("name,cb", [("qwen3", 0), ("qwen38", 2)])
+def test_exl3_apply_composition_pinned(golden_exl3, name, cb):
+    """oracle.exl3_apply against a float64 numpy restatement of EXL3Kernels.apply
+    (Core/EXL3.swift:82-100): xr = fp16(H(x * suh) / sqrt(128)), yh = xr @ W (W the golden-pinned
+    decode), y = fp16(H(yh) / sqrt(128) * svh), H the Sylvester matrix from its closed form (not the
+    oracle's butterflies). The oracle's fp32 sums of 128 products and its fp32 butterflies differ
+    from float64 by far less than 2^-20 of each output's bound sum |xr||W| (sqrt(128) times fp32's
+    2^-24 per level at most); every output whose final fp16 rounding that difference cannot flip
+    (about half of them) must equal the restatement's exactly, and every output lies within half an
+    fp16 ulp plus that difference. A missing fp16 rounding of xr (about half an fp16 ulp of y, since
+    |y| is about bound / 128) or svh applied before the transform fails. The reference's own
+    criterion for the product, 1e-5 of the bound (EXL3Tests.swift:57-72), is 10x looser."""
+    t = golden_exl3[name + ".trellis"]
+    bits2 = t.shape[2] // 8
+    suh = golden_exl3[name + ".suh"].astype(np.float64)
+    svh = golden_exl3[name + ".svh"].astype(np.float64)
+    W = oracle.exl3_dequant(t, bits2, cb).astype(np.float64)
+    K, N = W.shape
+    i = np.arange(128)
+    H = np.where(np.bitwise_count(i[:, None] & i[None, :]) % 2, -1.0, 1.0) / np.sqrt(128.0)
+    x = np.random.default_rng(11).standard_normal((12, K)).astype(np.float16).astype(np.float64)
+    xr = ((x * suh).reshape(12, K // 128, 128) @ H).reshape(12, K).astype(np.float16).astype(np.float64)
+    yh = xr @ W
+    pre = (yh.reshape(12, N // 128, 128) @ H).reshape(12, N) * svh
+    bh = np.abs(xr) @ np.abs(W)
+    bound = np.repeat(bh.reshape(12, N // 128, 128).sum(2), 128, 1) / np.sqrt(128.0) * np.abs(svh)
+    err = 2.0 ** -20 * bound
+    y = oracle.exl3_apply(x.astype(np.float32), t, suh.astype(np.float32), svh.astype(np.float32), bits2,
+                          cb).astype(np.float64)
+    assert np.array_equal(y, y.astype(np.float16).astype(np.float64)), "outputs are not fp16 values"
+    want = _f16_round_pinned(pre, err)
+    fixed = ~np.isnan(want)
+    assert fixed.mean() > 0.3
+    assert np.array_equal(y[fixed], want[fixed])
+    assert np.all(np.abs(y - pre) <= err + np.abs(pre) * 2.0 ** -11)
+
+
 @pytest.mark.parametrize("block", [2, 8, 128, 512])
 def test_hadamard_closed_form(block):
     # Sylvester order: H[i][j] = (-1)^popcount(i & j) / sqrt(b); orthonormal and symmetric.
