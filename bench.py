@@ -42,6 +42,9 @@ def parse():
                                                        "affine experts")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of family names to run (debug)")
+    ap.add_argument("--ceiling", action="store_true",
+                    help="only the read ceiling: a plain streaming read (ishz_stream_read) of 16 MB .. 600 MB, "
+                         "one JSON line")
     ap.add_argument("--policy", action="store_true",
                     help="measure the row-count dispatch policy (VerifyMatmul.minimumRows, ggmlApply's "
                          "row ranges) instead of the benchmark")
@@ -345,6 +348,24 @@ def main():
         torch.cuda.empty_cache()
         return r, sec, n
 
+    ceilings = {}
+
+    def ceiling(nbytes, steps):
+        """(us, GB/s) of a plain streaming read of nbytes (cached per byte count)."""
+        if nbytes not in ceilings:
+            r, _, _ = measure("stream_read", lambda: read_case(nbytes), 1, steps, args.warmup)
+            ceilings[nbytes] = (r["us"], r["GBps"])
+        return ceilings[nbytes]
+
+    if args.ceiling:
+        rows = []
+        for mb in (16, 22.28, 25.76, 27.85, 50.14, 65.5, 73.11, 100, 131.1, 200, 340, 600):
+            us_, gbps = ceiling(int(mb * 1e6) // 16 * 16, args.steps)
+            rows.append({"MB": mb, "us": us_, "GBps": gbps, "hbm_frac": round(gbps * 1e9 / HBM_PEAK, 4)})
+        print(json.dumps({"metric": "read ceiling: ishz_stream_read per byte count (graph replay, >= 600 MB "
+                                    "of copies)", "rows": rows}), flush=True)
+        return
+
     only = set(filter(None, args.only.split(",")))
     NS, KS = 17408, 5120
     families = []
@@ -353,6 +374,7 @@ def main():
     # the call is the roofline kernel; beside it a plain read of the same bytes
     head, head_sec, head_n = measure("affine2_g64_wht128", lambda: affine_case(NS, KS, 1), 1, args.steps, args.warmup)
     rd, rd_sec, _ = measure("stream_read", lambda: read_case(head["weight_bytes"]), 1, args.steps, args.warmup)
+    ceilings[int(head["weight_bytes"]) // 16 * 16] = (rd["us"], rd["GBps"])
 
     fam_steps = max(50, args.steps // 2)
 
@@ -362,6 +384,10 @@ def main():
         r, _, _ = measure(name, builder, M, fam_steps, args.warmup, nk=nk, extra=extra)
         r["config"] = tag
         r["shape"] = shape
+        # the practical ceiling at this family's byte count: a plain streaming read of as many bytes
+        cu, cg = ceiling(int(r["weight_bytes"]) // 16 * 16, fam_steps)
+        r["read_ceiling_us"], r["read_ceiling_GBps"] = cu, cg
+        r["frac_of_read_ceiling"] = round(cu / r["us"], 4)
         families.append(r)
 
     # cfg0: GGUF Q4_0 4096x4096
