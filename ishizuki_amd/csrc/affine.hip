@@ -188,6 +188,10 @@ __global__ __launch_bounds__(512) void affine_vgemm(const uint16_t *__restrict__
   float *accb = (float *)(zero + 128);                 // [wave][tile][quad][lane] partials
   const uint32_t mg = vconst(0x64006400u);
 
+#ifdef ISHZ_TIMING
+  uint64_t ts[5];
+  ts[0] = __builtin_amdgcn_s_memrealtime();
+#endif
   for (int i = threadIdx.x; i < 128; i += blockDim.x) zero[i] = u4{0, 0, 0, 0};
   for (int i = threadIdx.x; i < nw * tiles_per_wg * NQ * 64; i += blockDim.x) accb[i] = 0.0f;
   // A row of this lane: token tt = n / 4 of each quad, unit group gg = n % 4; only gg == G holds x.
@@ -195,19 +199,69 @@ __global__ __launch_bounds__(512) void affine_vgemm(const uint16_t *__restrict__
 
   for (int kc0 = 0; kc0 < K; kc0 += Kc) {
     const int klen = min(Kc, K - kc0), ucs = klen / 64, steps = ucs / 4;
+    // ---- stream: this wave's (tile, step) sequence, steps wave, wave + nw, ... of each tile.
+    // Load and consume cursors (tile, step) advance in step; loads past the end re-read the
+    // wave's last step (always in range) and are dropped. Ring of D steps: the main loop consumes
+    // D steps per pass and loads as many, with no exit in between, so the waits are for the step
+    // being consumed; the last (total % D) steps are already in the ring.
+    struct Raw {
+      u4 q;
+      uint32_t s[2], b[2];
+    };
+    const bool active = wave < steps && tb < te;
+    const int j_last = wave + (steps - 1 - wave) / nw * nw;  // this wave's last step of a tile
+    auto load = [&](int tile, int j, Raw &r) {
+      const int row = min(min(tile, te - 1) * 16 + n, N - 1);
+      const int u = kc0 / 64 + 4 * min(j, j_last);  // first unit of the step
+      r.q = *(const u4 *)(codes + (size_t)row * (K / 16) + 4 * (u + G));
+      if constexpr (GS == 64) {
+        const u2 sv = *(const u2 *)(scales + (size_t)row * gpr + u), bv = *(const u2 *)(biases + (size_t)row * gpr + u);
+        r.s[0] = sv.x, r.s[1] = sv.y, r.b[0] = bv.x, r.b[1] = bv.y;
+      } else {
+        r.s[0] = scales[(size_t)row * gpr + u / 2] | (uint32_t)scales[(size_t)row * gpr + u / 2 + 1] << 16;
+        r.b[0] = biases[(size_t)row * gpr + u / 2] | (uint32_t)biases[(size_t)row * gpr + u / 2 + 1] << 16;
+        r.s[1] = r.s[0], r.b[1] = r.b[0];
+      }
+    };
+    auto advance = [&](int &tile, int &j) {
+      j += nw;
+      if (j > j_last) {
+        j = wave;
+        tile++;
+      }
+    };
+    Raw ring[D];
+    int lt = tb, lj = wave;
+    const int total = active ? (te - tb) * ((j_last - wave) / nw + 1) : 0;
+    // the first weight steps go out before the staging when x comes from the prestaged image (its
+    // copy then overlaps their latency: M = 8 at 17408 x 5120, 13.5 -> 12.9 us), after it when the
+    // workgroup rotates x itself (the rotation's loads would queue behind them: M = 2, 12.5 -> 12.1)
+    if (active && img) {
+#pragma unroll
+      for (int d = 0; d < D - 1; d++) {
+        load(lt, lj, ring[d]);
+        advance(lt, lj);
+      }
+    }
     // ---- stage x[tk][kc0 .. kc0 + klen) of every token: copied from the prestaged images (Kc a
     // multiple of 1024, so a chunk's slots and sums are two runs of each image), or computed
     // (rotated first when block > 0), 8 values per lane per item
     if (img) {
       const int IWf = F::img_words(K), ugf = (K / 64 + 15) / 16, g0 = kc0 / 1024;
       const int ugt = (ucs + 15) / 16;  // groups in this chunk (the last may be short)
-      const int ns = ugt * 16 * R, nq = ugt * 16 * F::Q / 4, per = ns + nq;
-      for (int i = threadIdx.x; i < M * per; i += blockDim.x) {
-        const int tk = i / per, o = i % per;
-        const u4 *src = img + (size_t)tk * IWf + (o < ns ? g0 * 16 * R + o : ugf * 16 * R + g0 * 16 * F::Q / 4 + (o - ns));
-        vlds[tk * IW + (o < ns ? o : ugc * 16 * R + (o - ns))] = *src;
+      const int ns = ugt * 16 * R, nq = ugt * 16 * F::Q / 4;
+      // straight into LDS (global_load_lds_dwordx4), every wave's chunks of 64 words in flight at
+      // once: a loop of load-then-store copies waits out one memory latency per word a thread copies
+      const int cs = (ns + 63) / 64, cpt = cs + (nq + 63) / 64;
+      for (int c = wave; c < M * cpt; c += nw) {
+        const int tk = c / cpt, cc = c % cpt;
+        const bool sl = cc < cs;
+        const int o = (sl ? cc : cc - cs) * 64, len = min(64, (sl ? ns : nq) - o);
+        const u4 *src = img + (size_t)tk * IWf + (sl ? g0 * 16 * R : ugf * 16 * R + g0 * 16 * F::Q / 4) + o;
+        u4 *dst = vlds + tk * IW + (sl ? 0 : ugc * 16 * R) + o;
+        if (lane < len) __builtin_amdgcn_global_load_lds(src + lane, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
       }
-      __syncthreads();
+      __syncthreads();  // (waits for the wave's loads, then the barrier)
     } else {
       const int per_tok = (klen + 511) / 512, items = M * per_tok;
       const float scale = block > 1 ? 1.0f / __builtin_sqrtf((float)block) : 1.0f;
@@ -245,41 +299,10 @@ __global__ __launch_bounds__(512) void affine_vgemm(const uint16_t *__restrict__
       __syncthreads();
     }
 
-    // ---- stream: this wave's (tile, step) sequence, steps wave, wave + nw, ... of each tile.
-    // Load and consume cursors (tile, step) advance in step; loads past the end re-read the
-    // wave's last step (always in range) and are dropped. Ring of D steps: the main loop consumes
-    // D steps per pass and loads as many, with no exit in between, so the waits are for the step
-    // being consumed; the last (total % D) steps are already in the ring.
-    struct Raw {
-      u4 q;
-      uint32_t s[2], b[2];
-    };
-    const bool active = wave < steps && tb < te;
-    const int j_last = wave + (steps - 1 - wave) / nw * nw;  // this wave's last step of a tile
-    auto load = [&](int tile, int j, Raw &r) {
-      const int row = min(min(tile, te - 1) * 16 + n, N - 1);
-      const int u = kc0 / 64 + 4 * min(j, j_last);  // first unit of the step
-      r.q = *(const u4 *)(codes + (size_t)row * (K / 16) + 4 * (u + G));
-      if constexpr (GS == 64) {
-        const u2 sv = *(const u2 *)(scales + (size_t)row * gpr + u), bv = *(const u2 *)(biases + (size_t)row * gpr + u);
-        r.s[0] = sv.x, r.s[1] = sv.y, r.b[0] = bv.x, r.b[1] = bv.y;
-      } else {
-        r.s[0] = scales[(size_t)row * gpr + u / 2] | (uint32_t)scales[(size_t)row * gpr + u / 2 + 1] << 16;
-        r.b[0] = biases[(size_t)row * gpr + u / 2] | (uint32_t)biases[(size_t)row * gpr + u / 2 + 1] << 16;
-        r.s[1] = r.s[0], r.b[1] = r.b[0];
-      }
-    };
-    auto advance = [&](int &tile, int &j) {
-      j += nw;
-      if (j > j_last) {
-        j = wave;
-        tile++;
-      }
-    };
-    Raw ring[D];
-    int lt = tb, lj = wave;
-    const int total = active ? (te - tb) * ((j_last - wave) / nw + 1) : 0;
-    if (active) {
+#ifdef ISHZ_TIMING
+    ts[1] = ts[2] = __builtin_amdgcn_s_memrealtime();
+#endif
+    if (active && !img) {
 #pragma unroll
       for (int d = 0; d < D - 1; d++) {
         load(lt, lj, ring[d]);
@@ -347,8 +370,16 @@ __global__ __launch_bounds__(512) void affine_vgemm(const uint16_t *__restrict__
 #pragma unroll
     for (int d = 0; d < D - 1; d++)
       if (c + d < total) consume(ring[d]);
+#ifdef ISHZ_TIMING
+    ts[3] = __builtin_amdgcn_s_memrealtime();
+#endif
     __syncthreads();  // partials written; x image free for the next chunk
   }
+#ifdef ISHZ_TIMING
+  ts[4] = __builtin_amdgcn_s_memrealtime();
+  if (lane == 0)
+    for (int i = 0; i < 5; i++) ishz_timing[(blockIdx.x * 8 + wave) * 5 + i] = ts[i];
+#endif
   // ---- sum the waves' partials and write y
   for (int o = threadIdx.x; o < (te - tb) * NQ * 64; o += blockDim.x) {
     const int tl = o / (NQ * 64), q = (o / 64) % NQ, l = o % 64;
