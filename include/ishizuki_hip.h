@@ -160,8 +160,14 @@ int ishz_exl3_rotate(const void *x, int in_dtype, int rows, int width, const uin
 
 /* EXL3Kernels.matvec (Core/EXL3.swift:149-164, kernel :286-330): yh[M][N] (fp32) = xh[M][K]
    (fp16, bf16 or fp32) . W, W decoded in-kernel. M in 1..16 (the reference: 1..8, 9..16 as two
-   launches). The K-split partial products go to a stream-ordered temporary (hipMallocAsync) and
-   are summed in split order: the same bits on every call. */
+   launches). The K-split partial products are summed in split order: the same bits on every
+   call. ishz_exl3_matvec_ws takes them (and bf16 x's fp16 image) in a caller workspace of
+   ishz_exl3_matvec_workspace_size(M, K, N) bytes and allocates nothing; ishz_exl3_matvec is the
+   same call with stream-ordered temporaries (hipMallocAsync) instead. fp32 x needs neither. */
+size_t ishz_exl3_matvec_workspace_size(int M, int K, int N);
+int ishz_exl3_matvec_ws(const void *xh, int x_dtype, int M, int K, const int16_t *trellis, int N,
+                        int bits2, int codebook, float *yh, void *workspace, size_t workspace_bytes,
+                        ishz_stream_t stream);
 int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const int16_t *trellis, int N,
                      int bits2, int codebook, float *yh, ishz_stream_t stream);
 

@@ -33,6 +33,8 @@ _SIGS = {
     "ishz_exl3_dequant": (I, [P, I, I, I, I, P, I, P]),
     "ishz_exl3_rotate": (I, [P, I, I, I, P, I, P, I, P]),
     "ishz_exl3_matvec": (I, [P, I, I, I, P, I, I, I, P, P]),
+    "ishz_exl3_matvec_workspace_size": (SZ, [I, I, I]),
+    "ishz_exl3_matvec_ws": (I, [P, I, I, I, P, I, I, I, P, P, SZ, P]),
     "ishz_exl3_workspace_size": (SZ, [I, I, I]),
     "ishz_exl3_apply": (I, [P, I, I, I, P, P, P, I, I, I, P, P, SZ, P]),
     "ishz_exl3_apply_static": (I, [P, I, I, I, P, P, P, I, I, I, P, P]),

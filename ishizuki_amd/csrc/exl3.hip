@@ -775,8 +775,16 @@ static int exl3_matvec_f32(const float *x, int M, int K, const int16_t *trellis,
   });
 }
 
-extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const int16_t *trellis,
-                                int N, int bits2, int codebook, float *yh, ishz_stream_t stream) {
+// The matvec's device temporaries: the fp16 image of bf16 activations, then the K splits'
+// fp32 partial products.
+extern "C" size_t ishz_exl3_matvec_workspace_size(int M, int K, int N) {
+  if (M <= 0 || K <= 0 || N <= 0) return 0;
+  return act_image_bytes(M, K) + exl3_part_floats(M, K, N) * 4;
+}
+
+extern "C" int ishz_exl3_matvec_ws(const void *xh, int x_dtype, int M, int K, const int16_t *trellis, int N,
+                                   int bits2, int codebook, float *yh, void *workspace, size_t workspace_bytes,
+                                   ishz_stream_t stream) {
   int rc = check_exl3(K, N, bits2, codebook);
   if (rc) return rc;
   if (x_dtype < ISHZ_DT_F32 || x_dtype > ISHZ_DT_BF16) return decline("activations must be fp16, bf16 or fp32");
@@ -784,15 +792,23 @@ extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const
   if (!xh || !trellis || !yh) return einval("null pointer");
   hipStream_t st = S(stream);
   if (x_dtype == ISHZ_DT_F32) return exl3_matvec_f32((const float *)xh, M, K, trellis, N, bits2, codebook, yh, st);
-  StreamTemp tmp(st);  // bf16 activations: their fp16 image
-  if (x_dtype != ISHZ_DT_F16 && (rc = tmp.get(act_image_bytes(M, K)))) return rc;
+  // with a workspace of ishz_exl3_matvec_workspace_size bytes nothing is allocated; without one
+  // (ishz_exl3_matvec) the image and the parts are stream-ordered temporaries
+  const bool own = workspace && workspace_bytes >= ishz_exl3_matvec_workspace_size(M, K, N);
+  if (workspace && !own) return einval("workspace too small (ishz_exl3_matvec_workspace_size)");
+  StreamTemp tmp(st), parts(st);
+  void *img = own ? workspace : nullptr;
+  float *pp = own ? (float *)((char *)workspace + act_image_bytes(M, K)) : nullptr;
+  if (!own) {
+    if (x_dtype != ISHZ_DT_F16 && (rc = tmp.get(act_image_bytes(M, K)))) return rc;
+    if ((rc = parts.get(exl3_part_floats(M, K, N) * 4))) return rc;
+    img = tmp.p;
+    pp = (float *)parts.p;
+  }
   const uint16_t *x16;
   const float *rs;
-  if ((rc = act_prepare(xh, x_dtype, M, K, tmp.p, st, &x16, &rs))) return rc;
+  if ((rc = act_prepare(xh, x_dtype, M, K, img, st, &x16, &rs))) return rc;
   // the K splits' partial products, then their sum in split order: the same bits on every call
-  StreamTemp parts(st);
-  if ((rc = parts.get(exl3_part_floats(M, K, N) * 4))) return rc;
-  float *pp = (float *)parts.p;
   int np;
   if ((rc = exl3_matvec_core(x16, M, K, trellis, N, bits2, codebook, pp, &np, st))) return rc;
   const size_t n = (size_t)M * N;
@@ -800,6 +816,11 @@ extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const
                      pp, np, n, N, rs, yh);
   ISHZ_LAUNCH_CHECK("exl3 sum launch");
   return ISHZ_OK;
+}
+
+extern "C" int ishz_exl3_matvec(const void *xh, int x_dtype, int M, int K, const int16_t *trellis,
+                                int N, int bits2, int codebook, float *yh, ishz_stream_t stream) {
+  return ishz_exl3_matvec_ws(xh, x_dtype, M, K, trellis, N, bits2, codebook, yh, nullptr, 0, stream);
 }
 
 // Whether exl3_matvec_core takes the wide-step kernel, which can rotate x itself, and the

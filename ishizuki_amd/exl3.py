@@ -54,15 +54,25 @@ def rotate(x, scales, before, out_dtype):
     return y
 
 
-def matvec(xh, t):
-    """xh [M, K] fp16 (already rotated) -> fp32 [M, N]."""
+def matvec(xh, t, workspace=None):
+    """xh [M, K] (already rotated; fp16, bf16 or fp32) -> fp32 [M, N]. With `workspace` (a uint8
+    device tensor of matvec_workspace_size bytes) the call allocates nothing."""
     require_cuda(xh, t.trellis)
     xh = xh.contiguous()
     M = xh.shape[0]
     y = torch.empty((M, t.output_dim), dtype=torch.float32, device=xh.device)
-    rc = _lib.lib().ishz_exl3_matvec(ptr(xh), DTYPES.get(xh.dtype, -1), M, t.input_dim, ptr(t.trellis),
-                                     t.output_dim, t.bits2, t.codebook, ptr(y), stream())
+    L = _lib.lib()
+    if workspace is None:
+        rc = L.ishz_exl3_matvec(ptr(xh), DTYPES.get(xh.dtype, -1), M, t.input_dim, ptr(t.trellis), t.output_dim,
+                                t.bits2, t.codebook, ptr(y), stream())
+    else:
+        rc = L.ishz_exl3_matvec_ws(ptr(xh), DTYPES.get(xh.dtype, -1), M, t.input_dim, ptr(t.trellis), t.output_dim,
+                                   t.bits2, t.codebook, ptr(y), ptr(workspace), workspace.numel(), stream())
     return y if _lib.check(rc, "exl3_matvec") else None
+
+
+def matvec_workspace_size(M, t):
+    return _lib.lib().ishz_exl3_matvec_workspace_size(M, t.input_dim, t.output_dim)
 
 
 def apply(x, t):

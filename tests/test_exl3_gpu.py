@@ -12,7 +12,7 @@ import torch
 
 import oracle
 from conftest import assert_close, bits_equal
-from ishizuki_amd import exl3, synth
+from ishizuki_amd import _lib, exl3, synth
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -44,7 +44,6 @@ def test_dequant_matches_exllamav3(golden_exl3, name, cb):
     t = golden_exl3[name + ".trellis"]
     K, N = t.shape[0] * 16, t.shape[1] * 16
     out = torch.empty((K, N), dtype=torch.float32, device=DEV)
-    from ishizuki_amd import _lib
     from ishizuki_amd._torch import ptr
     rc = _lib.lib().ishz_exl3_dequant(ptr(torch.from_numpy(t).to(DEV)), K, N, t.shape[2] // 8, cb, ptr(out),
                                       _lib.DT_F32, None)
@@ -94,6 +93,24 @@ def test_matvec_is_deterministic(M):
     w = oracle.exl3_dequant(t, 4, 0)
     xf = xh.float().cpu().numpy()
     assert_close(ys[0].cpu().numpy(), xf @ w, bound=np.abs(xf) @ np.abs(w), what=f"exl3 deterministic M={M}")
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M", [1, 5])
+def test_matvec_workspace_matches_temporaries(M, dt):
+    """ishz_exl3_matvec_ws (caller workspace, no allocation) gives the bits of ishz_exl3_matvec
+    (stream-ordered temporaries); a workspace one byte short is refused."""
+    K, N = 5120, 1024
+    t, _, _, ten = make(K, N, 4, 0, seed=80 + M)
+    xh = torch.from_numpy(synth.fp16_normal((M, K), seed=81 + M)).to(DEV).to(dt)
+    nb = exl3.matvec_workspace_size(M, ten)
+    ws = torch.empty(nb, dtype=torch.uint8, device=DEV)
+    y0 = exl3.matvec(xh, ten)
+    y1 = exl3.matvec(xh, ten, workspace=ws)
+    assert y0 is not None and y1 is not None
+    assert torch.equal(y0.view(torch.int32), y1.view(torch.int32))
+    with pytest.raises(_lib.IshzError):
+        exl3.matvec(xh, ten, workspace=ws[: nb - 1])
 
 
 @pytest.mark.parametrize("M", [1, 3])
