@@ -126,8 +126,11 @@ int ishz_hadamard(const void *x, int dtype, int rows, int width, int block, cons
    the streaming GEMV (MLX
    quantizedMM's qmv, called at Core/Hadamard.swift:228-230); M = 2..16 the MFMA verify kernel
    (VerifyMatmul.applyAny, Core/VerifyMatmul.swift:73-120: its fast path takes 2, 4 and 8 bits,
-   :89, its generic path the other widths, :273-290). Declines: group not 64/128, K % 128 (and
-   K % 256 for verify rows of packs other than 2-bit), other dtypes. */
+   :89, its generic path the other widths, :273-290). Groups of 64 and 128 take those kernels;
+   any other multiple of 32 dividing K (applyAny's groupSize % 32, :84) takes the exact-weight
+   kernel (w = s * q + b in fp32, fp32 sums; one wave per output row). Declines: groups that are
+   not a multiple of 32, K % 128 (and K % 256 for verify rows of packs other than 2-bit), other
+   dtypes. */
 int ishz_affine_matmul(const void *x, int x_dtype, int M, int K, const uint32_t *codes,
                        const void *scales, const void *biases, int scale_dtype, int N, int bits,
                        int group, void *y, ishz_stream_t stream);

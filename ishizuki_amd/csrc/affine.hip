@@ -514,10 +514,12 @@ struct AffDec {
   }
 };
 
-static int affine_precise(const float *x, int M, int K, const uint32_t *codes, const void *scales, const void *biases,
-                          int bf16s, int N, int bits, int group, void *y, hipStream_t st) {
+// Exact weights, fp32 sums: fp32 x (its precision), and fp16 / bf16 x with groups other than 64 /
+// 128 (the fp16 kernels' layouts). y in x's dtype.
+static int affine_precise(const void *x, int xdt, int M, int K, const uint32_t *codes, const void *scales,
+                          const void *biases, int bf16s, int N, int bits, int group, void *y, hipStream_t st) {
   const AffDec::Args a{codes, (const uint16_t *)scales, (const uint16_t *)biases, K, bits, group, bf16s != 0};
-  return launch_precise<AffDec>(a, x, M, K, N, y, ISHZ_DT_F32, st);
+  return launch_precise<AffDec>(a, x, xdt, M, K, N, y, st);
 }
 
 static int check_affine(const void *x, int x_dtype, int M, int K, const void *codes,
@@ -526,7 +528,7 @@ static int check_affine(const void *x, int x_dtype, int M, int K, const void *co
   if (x_dtype != ISHZ_DT_F16 && x_dtype != ISHZ_DT_BF16 && x_dtype != ISHZ_DT_F32)
     return decline("activations must be fp16, bf16 or fp32");
   if (bits < 2 || bits > 8) return decline("packs of 2 to 8 bits are decoded in-kernel");
-  if (group != 64 && group != 128) return decline("group size must be 64 or 128");
+  if (group < 32 || group % 32 || K % group) return decline("group size must be a multiple of 32 dividing K");
   if (scale_dtype != ISHZ_DT_F16 && scale_dtype != ISHZ_DT_BF16) return decline("scales must be fp16 or bf16");
   if (M < 1 || M > 16) return decline("row count outside 1..16");
   if (K <= 0 || K % 128 || N <= 0) return decline("K must be a positive multiple of 128");
@@ -597,9 +599,8 @@ extern "C" int ishz_affine_matmul(const void *x, int x_dtype, int M, int K, cons
   int rc = check_affine(x, x_dtype, M, K, codes, scales, biases, scale_dtype, N, bits, group, y);
   if (rc) return rc;
   hipStream_t st = S(stream);
-  if (x_dtype == ISHZ_DT_F32)
-    return affine_precise((const float *)x, M, K, codes, scales, biases, scale_dtype == ISHZ_DT_BF16, N, bits, group,
-                          y, st);
+  if (x_dtype == ISHZ_DT_F32 || (group != 64 && group != 128))
+    return affine_precise(x, x_dtype, M, K, codes, scales, biases, scale_dtype == ISHZ_DT_BF16, N, bits, group, y, st);
   StreamTemp tmp(st);  // bf16 activations: their fp16 image
   if (x_dtype != ISHZ_DT_F16 && (rc = tmp.get(act_image_bytes(M, K)))) return rc;
   const uint16_t *xh;
@@ -643,7 +644,8 @@ extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, cons
       xr = workspace;
       img = (char *)workspace + (size_t)M * K * 4;
     }
-    if (x_dtype == ISHZ_DT_F32) return affine_precise((const float *)xr, M, K, codes, scales, biases, bf16s, N, bits, group, y, st);
+    if (x_dtype == ISHZ_DT_F32 || (group != 64 && group != 128))
+      return affine_precise(xr, x_dtype, M, K, codes, scales, biases, bf16s, N, bits, group, y, st);
     const uint16_t *xh;
     const float *rs;
     if ((rc = act_prepare(xr, x_dtype, M, K, img, st, &xh, &rs))) return rc;
@@ -652,6 +654,13 @@ extern "C" int ishz_affine_linear(const void *x, int x_dtype, int M, int K, cons
     return affine_dispatch(xh, M, K, nullptr, 0, codes, scales, biases, bf16s, N, group, o, st);
   }
   const Out o{y, ISHZ_DT_F16, nullptr};
+  if (group != 64 && group != 128) {  // other groups: x rotated once into the workspace, exact weights
+    if (block == 0) return affine_precise(x, ISHZ_DT_F16, M, K, codes, scales, biases, bf16s, N, bits, group, y, st);
+    if (!workspace || workspace_bytes < ishz_affine_workspace_size(M, K))
+      return einval("workspace too small (ishz_affine_workspace_size)");
+    if ((rc = ishz_hadamard(x, ISHZ_DT_F16, M, K, block, signs, 0, workspace, stream))) return rc;
+    return affine_precise(workspace, ISHZ_DT_F16, M, K, codes, scales, biases, bf16s, N, bits, group, y, st);
+  }
   if (bits != 2) {  // 3- to 8-bit packs: rotate x once into the workspace, then the matmul
     if (block == 0) return affine_nbit_dispatch(x, M, K, codes, scales, biases, bf16s, N, bits, group, o, st);
     if (!workspace || workspace_bytes < ishz_affine_workspace_size(M, K))

@@ -412,7 +412,7 @@ static int ggml_call(uint32_t type, const void *x, int x_dtype, int M, int K, co
 #define X(T, F)                                                                                              \
   case T:                                                                                                    \
     return launch_precise<GgmlDec<T, F::BS, F::TS>>({(const uint8_t *)blocks, (size_t)(K / F::BS) * F::TS},   \
-                                                    (const float *)x, M, K, N, y, ISHZ_DT_F32, st);
+                                                    x, ISHZ_DT_F32, M, K, N, y, st);
       ISHZ_GGML_FORMATS(X)
 #undef X
     }

@@ -3,7 +3,9 @@
 // checked at 1e-5 of sum |x||w|, Tests/IshizukiKitTests/GGMLKernelTests.swift:131-137). The fp16
 // kernels cannot meet that: they stage x in fp16 and carry a 1024-times offset in their fp32 sums.
 // So an fp32 call takes this path instead: every weight is decoded to its exact fp32 value (the CPU
-// decoder's operations in its order) and dotted with the fp32 x by fp32 FMAs.
+// decoder's operations in its order) and dotted with the fp32 x by fp32 FMAs. The same kernel, with
+// fp16 / bf16 x widened exactly, also serves layouts the fp16 kernels do not take (affine groups of
+// 32 or other multiples of 32 than 64 and 128).
 //
 // One wave per output row (four per workgroup); lane l takes the row's 8-weight slices l, l + 64,
 // ..., in order, and the 64 lane partials meet in a fixed DPP / shuffle tree. Up to 16 token rows
@@ -15,8 +17,24 @@
 
 namespace ishz {
 
-template <class D>
-__global__ __launch_bounds__(256) void precise_kernel(typename D::Args a, const float *__restrict__ x, int M, int K,
+// Eight activations of token row m from slice s: fp32 as they are, fp16 / bf16 widened exactly.
+template <int XDT>
+DEV void x8(const void *x, size_t o, float *v) {
+  if constexpr (XDT == ISHZ_DT_F32) {
+    const f4 a = *(const f4 *)((const float *)x + o), b = *(const f4 *)((const float *)x + o + 4);
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  } else {
+    const u4 h = *(const u4 *)((const uint16_t *)x + o);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t b = (h[i >> 1] >> (16 * (i & 1))) & 0xffffu;
+      v[i] = XDT == ISHZ_DT_F16 ? h2f(b) : __builtin_bit_cast(float, b << 16);
+    }
+  }
+}
+
+template <class D, int XDT>
+__global__ __launch_bounds__(256) void precise_kernel(typename D::Args a, const void *__restrict__ x, int M, int K,
                                                       int N, void *__restrict__ y, int dt) {
   const int row = blockIdx.x * 4 + wave_id();
   if (row >= N) return;
@@ -30,16 +48,11 @@ __global__ __launch_bounds__(256) void precise_kernel(typename D::Args a, const 
 #pragma unroll
     for (int m = 0; m < 16; m++) {
       if (m >= M) continue;  // uniform; a break would stop the unrolling (acc in scratch)
-      const f4 x0 = *(const f4 *)(x + (size_t)m * K + 8 * s), x1 = *(const f4 *)(x + (size_t)m * K + 8 * s + 4);
+      float xv[8];
+      x8<XDT>(x, (size_t)m * K + 8 * s, xv);
       float t = acc[m];
-      t = __builtin_fmaf(v[0], x0.x, t);
-      t = __builtin_fmaf(v[1], x0.y, t);
-      t = __builtin_fmaf(v[2], x0.z, t);
-      t = __builtin_fmaf(v[3], x0.w, t);
-      t = __builtin_fmaf(v[4], x1.x, t);
-      t = __builtin_fmaf(v[5], x1.y, t);
-      t = __builtin_fmaf(v[6], x1.z, t);
-      t = __builtin_fmaf(v[7], x1.w, t);
+#pragma unroll
+      for (int i = 0; i < 8; i++) t = __builtin_fmaf(v[i], xv[i], t);
       acc[m] = t;
     }
   }
@@ -51,13 +64,19 @@ __global__ __launch_bounds__(256) void precise_kernel(typename D::Args a, const 
   }
 }
 
-// y [M][N] (dtype dt) = x [M][K] (fp32) times the decoded weights. K % 8 == 0, M <= 16.
+// y [M][N] (in x's dtype xdt) = x [M][K] times the decoded weights. K % 8 == 0, M <= 16.
 template <class D>
-static int launch_precise(const typename D::Args &a, const float *x, int M, int K, int N, void *y, int dt,
+static int launch_precise(const typename D::Args &a, const void *x, int xdt, int M, int K, int N, void *y,
                           hipStream_t st) {
-  if (M < 1 || M > 16 || K % 8) return decline("fp32 path: 1..16 rows and K a multiple of 8");
-  hipLaunchKernelGGL(precise_kernel<D>, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, a, x, M, K, N, y, dt);
-  ISHZ_LAUNCH_CHECK("fp32 matmul launch");
+  if (M < 1 || M > 16 || K % 8) return decline("exact-weight path: 1..16 rows and K a multiple of 8");
+  const dim3 grid((unsigned)((N + 3) / 4));
+  if (xdt == ISHZ_DT_F32)
+    hipLaunchKernelGGL((precise_kernel<D, ISHZ_DT_F32>), grid, dim3(256), 0, st, a, x, M, K, N, y, xdt);
+  else if (xdt == ISHZ_DT_F16)
+    hipLaunchKernelGGL((precise_kernel<D, ISHZ_DT_F16>), grid, dim3(256), 0, st, a, x, M, K, N, y, xdt);
+  else
+    hipLaunchKernelGGL((precise_kernel<D, ISHZ_DT_BF16>), grid, dim3(256), 0, st, a, x, M, K, N, y, xdt);
+  ISHZ_LAUNCH_CHECK("exact-weight matmul launch");
   return ISHZ_OK;
 }
 

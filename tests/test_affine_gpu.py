@@ -69,6 +69,46 @@ def test_affine_matmul(M, group):
     assert_close(y.float().cpu().numpy(), ref, bound=bd, what=f"affine M={M} g={group}")
 
 
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M", [1, 5, 16])
+@pytest.mark.parametrize("bits,group", [(2, 32), (4, 32), (8, 32), (3, 96), (2, 96)])
+def test_affine_other_groups(bits, group, M, dt):
+    """Groups other than 64 and 128 (applyAny accepts any multiple of 32 dividing K,
+    Core/VerifyMatmul.swift:84): the exact-weight kernel, x in its own dtype, against the oracle."""
+    N, K = 300, 3072
+    codes, s, b = synth.affine_pack_bits(N, K, bits, group=group, seed=bits + group + M)
+    x = torch.from_numpy(synth.fp16_normal((M, K), seed=M + 3)).to(dt)
+    xf = x.float().numpy()
+    print(f"affine group={group} bits={bits} M={M} {dt}", flush=True)
+    y = affine.quantized_matmul(x.to(DEV), torch.from_numpy(codes.view(np.int32)).to(DEV), torch.from_numpy(s).to(DEV),
+                                torch.from_numpy(b).to(DEV), group_size=group, bits=bits)
+    assert y is not None and y.dtype == dt
+    ref = oracle.affine_matmul(xf, codes, s.view(np.uint16), b.view(np.uint16), N, bits, group)
+    bd = affine_bound(xf, codes, s, b, N, K, bits, group)
+    # fp32 sums of exact weights: 1e-5 of the bound, plus the output's one rounding to x's dtype
+    yv = y.float().cpu().numpy().astype(np.float64)
+    lim = 1e-5 * bd + 2.0 ** (-11 if dt == torch.float16 else -8) * np.abs(ref)
+    assert np.all(np.abs(yv - ref) <= lim), f"worst {np.max(np.abs(yv - ref) / lim):.3g}x"
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_affine_group32_rotated_linear(M):
+    """PackedLinear's rotated forward with group 32: x rotated once into the workspace (fp16, the
+    reference's rounding), then the exact-weight kernel."""
+    N, K, bits = 256, 2048, 2
+    codes, s, b = synth.affine_pack(N, K, group=32, seed=M + 40)
+    signs = synth.hadamard_signs(K, seed=41)
+    x = synth.fp16_normal((M, K), seed=M + 42)
+    y = affine.linear(torch.from_numpy(x).to(DEV), torch.from_numpy(codes.view(np.int32)).to(DEV),
+                      torch.from_numpy(s).to(DEV), torch.from_numpy(b).to(DEV), signs=torch.from_numpy(signs),
+                      block=128, group_size=32, bits=bits)
+    assert y is not None
+    xr = oracle.hadamard(x.astype(np.float32), 128, signs).astype(np.float16).astype(np.float32)
+    ref = oracle.affine_matmul(xr, codes, s.view(np.uint16), b.view(np.uint16), N, bits, 32)
+    assert_close(y.float().cpu().numpy(), ref, bound=affine_bound(xr, codes, s, b, N, K, bits, 32),
+                 what=f"affine g32 rotated M={M}")
+
+
 @pytest.mark.parametrize("group", [64, 128])
 @pytest.mark.parametrize("block", [0, 128])
 def test_affine_long_k_gemv(group, block):
@@ -239,6 +279,6 @@ def test_affine_declines():
     x = torch.zeros((1, 256), dtype=torch.float16, device=DEV)
     w = torch.zeros((4, 16), dtype=torch.int32, device=DEV)
     s = torch.zeros((4, 8), dtype=torch.float16, device=DEV)
-    assert affine.quantized_matmul(x, w, s, s, group_size=32) is None        # group 32
+    assert affine.quantized_matmul(x, w, s, s, group_size=48) is None        # group not a multiple of 32
     assert affine.quantized_matmul(x.to(torch.int16), w, s, s, group_size=64) is None  # integer x
     assert affine.verify_apply(torch.zeros((1, 256), dtype=torch.float16, device=DEV), w, s, s) is None
