@@ -215,7 +215,7 @@ size_t ishz_moe_workspace_size(int T, int H, int E, int I, int topk);
 /* The same FFN over MLX affine stacked experts, the reference's own expert format
    (StackedExperts, Text/MoEBlock.swift:22-50, multiplied through gatherQuantizedMM at :45-49):
    gate and up packs hold E experts of [I][H] weights, down E experts of [H][I]; codes u32
-   [E][rows][K * bits / 32], scales / biases [E][rows][K / group] in scale_dtype. bits 4 or 8,
+   [E][rows][K * bits / 32], scales / biases [E][rows][K / group] in scale_dtype. bits 2 to 8,
    group 64 or 128, H and I multiples of 256. Routing, workspace and outputs as ishz_moe_swiglu. */
 int ishz_moe_swiglu_affine(const void *x, int x_dtype, int T, int H, const float *logits, int E,
                            int topk, int normalize, const uint32_t *gate_codes, const void *gate_scales,

@@ -1,4 +1,5 @@
-// MLX affine packs of 3 to 8 bits per weight (VerifyMatmul.applyAny: the 4- and 8-bit fast paths
+// MLX affine packs of 3 to 8 bits per weight (2 bits too, for the MoE experts; the 2-bit matmul
+// has its own format, FAffine) (VerifyMatmul.applyAny: the 4- and 8-bit fast paths
 // and the generic one for 3, 5, 6 and 7 bits, Core/VerifyMatmul.swift:83-89,
 // 273-290; pack layout Quantize/WeightedAffineQuantizer.swift:142-153): w[n][k] = s[n][k/gs] * q +
 // b[n][k/gs], q the bits-wide field k of the row's little-endian u32 stream, so a word holds 8
@@ -58,7 +59,7 @@ struct VAffineN {
 
 template <int BITS, int GS, bool BF16S>
 struct FAffineN : GgmlGemv<FAffineN<BITS, GS, BF16S>> {
-  static_assert(BITS >= 3 && BITS <= 8, "3- to 8-bit packs");
+  static_assert(BITS >= 2 && BITS <= 8, "2- to 8-bit packs");
   using Base = GgmlGemv<FAffineN<BITS, GS, BF16S>>;
   struct Args {
     const uint32_t *codes;

@@ -176,7 +176,7 @@ DEV void route_token(const float *__restrict__ l, int E, int k, int normalize, i
   } while (0)
 
 // Routing alone: a 16-lane row per token, blockDim / 16 tokens per workgroup.
-__global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict__ logits, int T, int E,
+static __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict__ logits, int T, int E,
                                                         int k, int normalize, MoeRoute R) {
   extern __shared__ uint32_t rrows[];
   const int rw = threadIdx.x >> 4, t = blockIdx.x * (blockDim.x >> 4) + rw;
@@ -240,14 +240,14 @@ DEV void place_pairs(int T, int E, int k, const MoeRoute &R, const int32_t *ids,
   }
 }
 
-__global__ __launch_bounds__(1024) void moe_place_kernel(int T, int E, int k, MoeRoute R) {
+static __global__ __launch_bounds__(1024) void moe_place_kernel(int T, int E, int k, MoeRoute R) {
   extern __shared__ int32_t cnt[];  // E counts, then fill cursors
   place_pairs(T, E, k, R, R.ids, cnt);
 }
 
 // Routing and placement in one workgroup (up to 64 tokens routed at once, a 16-lane row each):
 // one launch instead of two when the rows, the counts and the ids fit in LDS.
-__global__ __launch_bounds__(1024) void moe_route_place_kernel(const float *__restrict__ logits, int T, int E,
+static __global__ __launch_bounds__(1024) void moe_route_place_kernel(const float *__restrict__ logits, int T, int E,
                                                                int k, int normalize, MoeRoute R) {
   extern __shared__ uint32_t rrows[];  // [rows][route_row_words] , E counts, then the T k ids
   const int nr = blockDim.x >> 4, rw = threadIdx.x >> 4;
@@ -345,7 +345,7 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(const uint16_t *__restri
   }
 }
 
-__global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__restrict__ o, int H,
+static __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t *__restrict__ o, int H,
                                                           int T, int k, MoeRoute R,
                                                           const uint16_t *__restrict__ shared,
                                                           const uint16_t *__restrict__ shared_gate,
@@ -962,8 +962,20 @@ static int moe_ffn_affine(const void *x, int T, int H, int E, int I, int k, cons
   return ISHZ_OK;
 }
 
+// The affine experts of the widths other than 4 and 8 bits (2, 3 and 5 to 7): instantiated in
+// moe_affine_w23.hip and moe_affine_w567.hip, which include this file's body, so that the three
+// translation units compile in parallel.
+#define ISHZ_MOE_AFFINE_ARGS                                                                                  \
+  const void *x, int T, int H, int E, int I, int k, const AffPack &gate, const AffPack &up, const AffPack &down, \
+      const MoeTokens &rt, uint16_t *h, uint16_t *gu, uint16_t *o, const uint16_t *shared,                     \
+      const uint16_t *shared_gate, void *y, hipStream_t st
+#define ISHZ_MOE_AFFINE_PASS x, T, H, E, I, k, gate, up, down, rt, h, gu, o, shared, shared_gate, y, st
+int moe_affine_w23(int bits, int group, bool bf16s, ISHZ_MOE_AFFINE_ARGS);
+int moe_affine_w567(int bits, int group, bool bf16s, ISHZ_MOE_AFFINE_ARGS);
+
 }  // namespace ishz
 
+#ifndef ISHZ_MOE_BODY_ONLY
 using namespace ishz;
 
 extern "C" size_t ishz_moe_workspace_size(int T, int H, int E, int I, int topk) {
@@ -1029,7 +1041,7 @@ extern "C" int ishz_moe_swiglu_affine(const void *x, int x_dtype, int T, int H, 
                                       const void *shared, const void *shared_gate, void *y, int32_t *ids_out,
                                       float *weights_out, void *workspace, size_t workspace_bytes,
                                       ishz_stream_t stream) {
-  if (bits != 4 && bits != 8) return decline("affine experts of 4 or 8 bits are decoded in-kernel");
+  if (bits < 2 || bits > 8) return decline("affine experts of 2 to 8 bits are decoded in-kernel");
   if (group != 64 && group != 128) return decline("group size must be 64 or 128");
   if (scale_dtype != ISHZ_DT_F16 && scale_dtype != ISHZ_DT_BF16) return decline("scales must be fp16 or bf16");
   if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
@@ -1066,7 +1078,12 @@ extern "C" int ishz_moe_swiglu_affine(const void *x, int x_dtype, int T, int H, 
     if (group == 64) ISHZ_MA(4, 64);
     ISHZ_MA(4, 128);
   }
-  if (group == 64) ISHZ_MA(8, 64);
-  ISHZ_MA(8, 128);
+  if (bits == 8) {
+    if (group == 64) ISHZ_MA(8, 64);
+    ISHZ_MA(8, 128);
+  }
 #undef ISHZ_MA
+  if (bits <= 3) return moe_affine_w23(bits, group, bf, x, T, H, E, I, topk, gp, upk, dp, rt, h, gu, o, sh, sg, y, st);
+  return moe_affine_w567(bits, group, bf, x, T, H, E, I, topk, gp, upk, dp, rt, h, gu, o, sh, sg, y, st);
 }
+#endif  // ISHZ_MOE_BODY_ONLY

@@ -219,11 +219,14 @@ def test_swiglu_shared_expert(T, type_):
                    shared=torch.from_numpy(sh).to(DEV))
 
 
-@pytest.mark.parametrize("bits,group,T", [(4, 64, 1), (8, 128, 2), (4, 128, 5), (8, 64, 3), (4, 64, 20)])
+@pytest.mark.parametrize("bits,group,T", [(4, 64, 1), (8, 128, 2), (4, 128, 5), (8, 64, 3), (4, 64, 20),
+                                          (2, 64, 1), (3, 128, 2), (5, 64, 4), (6, 128, 1), (7, 64, 9), (2, 128, 20),
+                                          (3, 64, 1), (6, 64, 6)])
 def test_swiglu_affine_experts(bits, group, T):
-    """StackedExperts as MLX affine packs (the reference's expert format), 4 and 8 bits."""
+    """StackedExperts as MLX affine packs (the reference's expert format, any width its
+    gatherQuantizedMM takes, Text/MoEBlock.swift:27,48): 2 to 8 bits, weights of about 0.05."""
     E, H, I, k = 16, 512, 256, 4
-    packs, ex = affine_experts(E, H, I, bits, group, seed=bits * 10 + T, scale=0.01 if bits == 4 else 0.0008)
+    packs, ex = affine_experts(E, H, I, bits, group, seed=bits * 10 + T, scale=0.087 / 2 ** (bits - 1))
     x = synth.fp16_normal((T, H), seed=T + 70)
     logits = np.random.default_rng(T + 71).standard_normal((T, E)).astype(np.float32)
     y, ids, w = moe.swiglu_affine(torch.from_numpy(x).to(DEV), torch.from_numpy(logits).to(DEV), ex, top_k=k,
