@@ -36,7 +36,7 @@ enum { ISHZ_OK = 0, ISHZ_DECLINED = 1, ISHZ_EINVAL = 2, ISHZ_EHIP = 3 };
      temporary (hipMallocAsync).
    - fp32 x: fp32 precision. Every weight is decoded to its exact fp32 value and dotted with the
      fp32 x by fp32 FMAs (no image, no temporary), as the reference accumulates fp32 x in fp32.
-   The MoE FFN takes fp16 x only. */
+   The MoE FFN takes fp16 or bf16 x (its intermediates are rounded to x's dtype). */
 enum { ISHZ_DT_F32 = 0, ISHZ_DT_F16 = 1, ISHZ_DT_BF16 = 2 };
 
 /* GGML storage types, numbered as GGMLType's raw values (Config/GGUFFile.swift:13-43). */
@@ -201,11 +201,13 @@ int ishz_moe_route(const float *logits, int T, int E, int topk, int normalize, i
 
 /* The MoE FFN (MoEBlock.callAsFunction + ResidentExperts.swiglu, Text/MoEBlock.swift:124-171)
    over GGML-block experts: route (as ishz_moe_route), then for each routed (token, expert)
-   down(silu(gate(x)) * up(x)) with fp16 intermediates, weighted and summed in fp32 into
-   y [T][H] (fp16). gate/up hold E experts of [I][H] blocks back to back, down E experts of
+   down(silu(gate(x)) * up(x)) with intermediates in x's dtype, weighted and summed in fp32 into
+   y [T][H] (x's dtype). x fp16 or bf16 (MoEBlock runs in the model's dtype; bf16 x and h are
+   staged from fp16 images with a power-of-two factor per row, exact for bf16 values down to
+   2^-17 of their row's largest). gate/up hold E experts of [I][H] blocks back to back, down E experts of
    [H][I]; expert_bytes is the size of one expert's matrix. Only routed experts' blocks are
    read. type: Q4_K (also Q4_0, Q6_K). shared / shared_gate (optional, both or neither): the
-   shared expert's output shared(x) [T][H] and gate logit sharedGate(x) [T], fp16, computed by
+   shared expert's output shared(x) [T][H] and gate logit sharedGate(x) [T], in x's dtype, computed by
    the caller's own projections; sigmoid(gate) * shared is added in fp32 before the one cast
    (:158-160). ids_out / weights_out (optional, [T][topk]) receive the routing. workspace:
    ishz_moe_workspace_size bytes. (The reference runs this through MLX's gatherQuantizedMM over

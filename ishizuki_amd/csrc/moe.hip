@@ -4,7 +4,9 @@
 // MoEBlock.swift:124-171) over GGML-block experts: softmax over all E experts in fp32, top-k
 // (ties to the lower index), optional renormalisation, then per (token, expert)
 // down(silu(gate(x)) * up(x)), the k outputs weighted and summed in fp32, narrowed once.
-// Activations between stages are fp16 as the reference's gatherQuantizedMM outputs x.dtype.
+// Activations between stages are rounded to x's dtype (fp16 or bf16) as the reference's
+// gatherQuantizedMM outputs x.dtype; bf16 x and h are staged from fp16 images with a power-of-two
+// factor per row.
 //
 // Kernels:
 //  * Route + place: one workgroup, a 16-lane row per token. Top-k by rounds of a row-wide argmax,
@@ -262,13 +264,32 @@ static __global__ __launch_bounds__(1024) void moe_route_place_kernel(const floa
 }
 
 DEV float r16(float v) { return (float)(_Float16)v; }
+// The model's 16-bit activation type (fp16, or bf16 with bf): a value rounded to it, its bits,
+// and the value of its bits. Every activation the reference materialises between the MoE
+// stages (projection outputs, the SwiGLU ops, the shared expert's terms) takes this rounding.
+DEV float bf16_round(float v) {
+  uint32_t u = __builtin_bit_cast(uint32_t, v);
+  u = ((u & 0x7fffffffu) > 0x7f800000u) ? (u | 0x400000u) : u + 0x7fffu + ((u >> 16) & 1u);
+  return __builtin_bit_cast(float, u & 0xffff0000u);
+}
+DEV float rnd(float v, bool bf) { return bf ? bf16_round(v) : r16(v); }
+DEV uint16_t bits16(float v, bool bf) { return bf ? (uint16_t)(__builtin_bit_cast(uint32_t, bf16_round(v)) >> 16) : f2h(v); }
+DEV float from16(uint32_t b, bool bf) { return bf ? __builtin_bit_cast(float, b << 16) : h2f(b); }
+// h = silu(g) * u with the reference's roundings (Text/MoEBlock.swift:168-171): g and u the
+// projections' outputs, sigmoid, g * sigmoid and the product each rounded to the activation type.
+DEV uint16_t swiglu16(float gs, float us, bool bf) {
+  const float g = rnd(gs, bf), u = rnd(us, bf);
+  const float sg = rnd(1.0f / (1.0f + __expf(-g)), bf);
+  return bits16(rnd(g * sg, bf) * u, bf);
+}
 
 // gate + up for one 16-row tile of I of one active expert, 16 routed tokens at a time.
 template <class F>
 __global__ __launch_bounds__(1024) void moe_gate_up_kernel(const uint16_t *__restrict__ x, int H,
                                                            const uint8_t *__restrict__ gate,
                                                            const uint8_t *__restrict__ up, int I, int k,
-                                                           MoeRoute R, uint16_t *__restrict__ h) {
+                                                           MoeRoute R, uint16_t *__restrict__ h,
+                                                           const float *__restrict__ rs, bool bf) {
   extern __shared__ __align__(16) float red[];
   const int a = blockIdx.y;
   if (a >= R.count[0]) return;
@@ -299,9 +320,8 @@ __global__ __launch_bounds__(1024) void moe_gate_up_kernel(const uint16_t *__res
       }
       const int t = 4 * (l >> 4) + r, i = i0 + (l & 15);
       if (c0 + t < p1 && i < I) {
-        const float g16 = r16(gs), u16 = r16(us);
-        const float sg = r16(1.0f / (1.0f + __expf(-g16)));
-        h[(size_t)(c0 + t) * I + i] = f2h(r16(g16 * sg) * u16);
+        const float f = rs ? rs[R.pair_q[c0 + t] / k] : 1.0f;  // x's row factor (bf16 x)
+        h[(size_t)(c0 + t) * I + i] = swiglu16(gs * f, us * f, bf);
       }
     }
     __syncthreads();
@@ -312,7 +332,8 @@ __global__ __launch_bounds__(1024) void moe_gate_up_kernel(const uint16_t *__res
 template <class F>
 __global__ __launch_bounds__(1024) void moe_down_kernel(const uint16_t *__restrict__ h, int I,
                                                         const uint8_t *__restrict__ down, int H,
-                                                        MoeRoute R, uint16_t *__restrict__ o) {
+                                                        MoeRoute R, uint16_t *__restrict__ o,
+                                                        const float *__restrict__ rs, bool bf) {
   extern __shared__ __align__(16) float red[];
   const int a = blockIdx.y;
   if (a >= R.count[0]) return;
@@ -339,7 +360,8 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(const uint16_t *__restri
       float s = 0.0f;
       for (int v = 0; v < KS; v++) s += red[((v * 2 + t2) * 4 + r) * 64 + l];
       const int t = 4 * (l >> 4) + r, n = n0 + 16 * t2 + (l & 15);
-      if (c0 + t < p1 && n < H) o[(size_t)R.pair_q[c0 + t] * H + n] = f2h(s);  // slot order
+      if (c0 + t < p1 && n < H)  // slot order; h's row factor (bf16)
+        o[(size_t)R.pair_q[c0 + t] * H + n] = bits16(rs ? s * rs[c0 + t] : s, bf);
     }
     __syncthreads();
   }
@@ -349,20 +371,20 @@ static __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t 
                                                           int T, int k, MoeRoute R,
                                                           const uint16_t *__restrict__ shared,
                                                           const uint16_t *__restrict__ shared_gate,
-                                                          uint16_t *__restrict__ y) {
+                                                          uint16_t *__restrict__ y, bool bf) {
   const size_t total = (size_t)T * H;
   for (size_t q = blockIdx.x * (size_t)blockDim.x + threadIdx.x; q < total;
        q += (size_t)gridDim.x * blockDim.x) {
     const int t = (int)(q / H), n = (int)(q % H);
     float acc = 0.0f;
     for (int s = 0; s < k; s++) {
-      acc += h2f(o[((size_t)t * k + s) * H + n]) * R.w[t * k + s];  // o rows in slot order
+      acc += from16(o[((size_t)t * k + s) * H + n], bf) * R.w[t * k + s];  // o rows in slot order
     }
     if (shared) {  // the shared expert, widened and added before the one narrowing
-      const float sg = (float)(_Float16)(1.0f / (1.0f + __expf(-h2f(shared_gate[t]))));
-      acc += (float)(_Float16)(sg * h2f(shared[q]));
+      const float sg = rnd(1.0f / (1.0f + __expf(-from16(shared_gate[t], bf))), bf);
+      acc += rnd(sg * from16(shared[q], bf), bf);
     }
-    y[q] = f2h(acc);
+    y[q] = bits16(acc, bf);
   }
 }
 
@@ -380,6 +402,8 @@ struct VMoeGateUp {
   MoeRoute R;
   uint16_t *h;
   int k;
+  const float *rs;  // x's row factors (bf16 x, staged from its fp16 image), or null
+  bool bf;          // bf16 activations
   struct Group {
     int e, p0, p1;
   };
@@ -398,13 +422,18 @@ struct VMoeGateUp {
     return ((tile & 1) ? up : gate) + ((size_t)g.e * I + i) * rb;
   }
   DEV void finish(const Group &g, int c0, int m, int tb, int te, const float *out) const {
+    finish_pairs(g, c0, m, tb, te, out, R.pair_q);
+  }
+  // pq: the sorted pairs' slot indices as this launch knows them (global, or the workgroup's own
+  // LDS copy when it routes itself)
+  DEV void finish_pairs(const Group &g, int c0, int m, int tb, int te, const float *out, const int32_t *pq) const {
     for (int o = threadIdx.x; o < (te - tb) / 2 * 256; o += blockDim.x) {
       const int pr = o >> 8, tk = (o >> 4) & 15, nn = o & 15;
       const int i = ((tb >> 1) + pr) * 16 + nn;
       if (tk < m && i < I) {
-        const float g16 = r16(out[(2 * pr) * 256 + tk * 16 + nn]), u16 = r16(out[(2 * pr + 1) * 256 + tk * 16 + nn]);
-        const float sg = r16(1.0f / (1.0f + __expf(-g16)));
-        h[(size_t)(g.p0 + c0 + tk) * I + i] = f2h(r16(g16 * sg) * u16);
+        const float f = rs ? rs[pq[g.p0 + c0 + tk] / k] : 1.0f;
+        h[(size_t)(g.p0 + c0 + tk) * I + i] =
+            swiglu16(out[(2 * pr) * 256 + tk * 16 + nn] * f, out[(2 * pr + 1) * 256 + tk * 16 + nn] * f, bf);
       }
     }
   }
@@ -475,6 +504,10 @@ struct VMoeGateUpR : VMoeGateUp {
     return true;
   }
   DEV const uint16_t *xrow(const Group &g, int tk) const { return x + (size_t)(lds_route().pair_q[g.p0 + tk] / k) * H; }
+  // the global pair list is written by workgroup (0, 0) during this launch: read the LDS copy
+  DEV void finish(const Group &g, int c0, int m, int tb, int te, const float *out) const {
+    finish_pairs(g, c0, m, tb, te, out, lds_route().pair_q);
+  }
 };
 
 // down: o[pair][H] = h[pair] . down_e^T (fp16).
@@ -485,6 +518,8 @@ struct VMoeDown {
   int I, H;
   MoeRoute R;
   uint16_t *o;
+  const float *rs;  // h's row factors (bf16 h, staged from its fp16 image), or null
+  bool bf;
   struct Group {
     int e, p0, p1;
   };
@@ -502,7 +537,8 @@ struct VMoeDown {
   DEV void finish(const Group &g, int c0, int m, int tb, int te, const float *out) const {
     for (int q = threadIdx.x; q < (te - tb) * 256; q += blockDim.x) {
       const int tk = (q >> 4) & 15, row = (tb + (q >> 8)) * 16 + (q & 15);
-      if (tk < m && row < H) o[(size_t)R.pair_q[g.p0 + c0 + tk] * H + row] = f2h(out[q]);  // slot order
+      if (tk < m && row < H)  // slot order
+        o[(size_t)R.pair_q[g.p0 + c0 + tk] * H + row] = bits16(rs ? out[q] * rs[g.p0 + c0 + tk] : out[q], bf);
     }
   }
 };
@@ -552,7 +588,9 @@ struct FMoeGateUp : F {
     int K, N;  // K = H, N = P 2I
     int I, k;
     MoeTokens rt;
-    const uint16_t *x;  // [T][H]
+    const uint16_t *x;  // [T][H] (bf16 x: its fp16 image)
+    const float *rs;    // the image's row factors, or null
+    bool bf;
   };
   struct XPre {};
   struct Prep {
@@ -615,9 +653,8 @@ struct FMoeGateUp : F {
     for (int q = threadIdx.x; q < nrows / 2; q += blockDim.x) {
       const int blk = q >> 2, i4 = q & 3, j = row0 + 8 * blk;
       const int p = j / (2 * a.I), i = wrow(j - p * 2 * a.I) + i4;
-      const float g16 = h2f(f2h(vals[8 * blk + i4])), u16 = h2f(f2h(vals[8 * blk + 4 + i4]));
-      const float sg = r16(1.0f / (1.0f + __expf(-g16)));
-      h[(size_t)p * a.I + i] = f2h(r16(g16 * sg) * u16);
+      const float f = a.rs ? a.rs[p / a.k] : 1.0f;
+      h[(size_t)p * a.I + i] = swiglu16(vals[8 * blk + i4] * f, vals[8 * blk + 4 + i4] * f, a.bf);
     }
   }
 };
@@ -633,6 +670,8 @@ struct FMoeDown : F {
     const float *w;      // [T k] routing weights
     const uint16_t *shared, *shared_gate;  // optional: shared expert output [T][H] and gate logit [T]
     const uint16_t *h;   // [P][I] SwiGLU outputs of the gate/up launch: the x images
+    const float *rs;     // h's row factors (bf16: h staged from its fp16 image), or null
+    bool bf;
   };
   struct XPre {};
   struct Prep {
@@ -693,12 +732,15 @@ struct FMoeDown : F {
       const int blk = q >> 2, rr = q & 3, j0 = row0 + blk * run;
       const int t = j0 / (a.H * a.k), r = out_of(a, j0) + rr;
       float acc = 0.0f;
-      for (int s = 0; s < a.k; s++) acc += h2f(f2h(vals[blk * run + 4 * s + rr])) * pp.w[t * a.k + s];
-      if (a.shared) {
-        const float sg = r16(1.0f / (1.0f + __expf(-h2f(a.shared_gate[t]))));
-        acc += r16(sg * h2f(a.shared[(size_t)t * a.H + r]));
+      for (int s = 0; s < a.k; s++) {
+        const float v = vals[blk * run + 4 * s + rr] * (a.rs ? a.rs[t * a.k + s] : 1.0f);
+        acc += rnd(v, a.bf) * pp.w[t * a.k + s];
       }
-      y[(size_t)t * a.H + r] = f2h(acc);
+      if (a.shared) {
+        const float sg = rnd(1.0f / (1.0f + __expf(-from16(a.shared_gate[t], a.bf))), a.bf);
+        acc += rnd(sg * from16(a.shared[(size_t)t * a.H + r], a.bf), a.bf);
+      }
+      y[(size_t)t * a.H + r] = bits16(acc, a.bf);
     }
   }
 };
@@ -729,7 +771,7 @@ static int route_launch(const float *logits, int T, int E, int k, int normalize,
 }
 
 struct MoeLayout {
-  size_t ids, w, count, active, offs, pair_q, h, gu, o, total;
+  size_t ids, w, count, active, offs, pair_q, h, gu, o, ximg, himg, total;
 };
 static MoeLayout moe_layout(int T, int H, int E, int I, int k) {
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
@@ -745,6 +787,8 @@ static MoeLayout moe_layout(int T, int H, int E, int I, int k) {
   L.h = off; off += al(P * I * 2);
   L.gu = off; off += al(P * 2 * I * 2);
   L.o = off; off += al(P * H * 2);
+  L.ximg = off; off += al(act_image_bytes(T, H));      // bf16 x: its fp16 image
+  L.himg = off; off += al(act_image_bytes((int)P, I));  // bf16 h: its fp16 image
   L.total = off;
   return L;
 }
@@ -776,11 +820,32 @@ static bool route_in_gate_up(int T, int H, int E, int I, int k) {
          T * k <= 256;
 }
 
+// The activation type of an FFN call: fp16, or bf16 (bf). bf16 x and h are staged from fp16
+// images with a power-of-two factor per row (act_prepare: exact for bf16 values down to 2^-17 of
+// their row's largest), and the projections' sums are multiplied back before their roundings.
+struct MoeAct {
+  bool bf;
+  const float *rsx;  // x's row factors (bf16), or null
+  void *himg;        // workspace for h's image (bf16)
+};
+// h's fp16 image and row factors for the down projection (bf16), or h itself.
+static int moe_h_image(const MoeAct &ma, const uint16_t *h, int P, int I, hipStream_t st, const uint16_t **h16,
+                       const float **rsh) {
+  if (!ma.bf) {
+    *h16 = h;
+    *rsh = nullptr;
+    return ISHZ_OK;
+  }
+  return act_prepare(h, ISHZ_DT_BF16, P, I, ma.himg, st, h16, rsh);
+}
+
 template <class F>
 static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void *gate,
                    const void *up, const void *down, const MoeTokens &rt, uint16_t *h, uint16_t *gu, uint16_t *o,
-                   const uint16_t *shared, const uint16_t *shared_gate, void *y, hipStream_t st) {
+                   const uint16_t *shared, const uint16_t *shared_gate, void *y, hipStream_t st, const MoeAct &ma) {
   const MoeRoute &R = rt.R;
+  const uint16_t *h16;
+  const float *rsh;
   const int amax = std::min(E, T * k);
   const size_t total = (size_t)T * H;
   // one or two tokens: every (token, slot) pair is a GEMV; two launches of the streaming GEMV
@@ -788,12 +853,13 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
   if (gathered_gemv(T, H, I, k)) {
     const int P = T * k;
     const typename FMoeGateUp<F>::Args ga{(const uint8_t *)gate, (const uint8_t *)up, (size_t)(H / F::BS) * F::TS,
-                                          H, P * 2 * I, I, k, rt, (const uint16_t *)x};
+                                          H, P * 2 * I, I, k, rt, (const uint16_t *)x, ma.rsx, ma.bf};
     int rc = launch_gemv<FMoeGateUp<F>>(ga, x, gu, st);
     if (rc) return rc;
+    if ((rc = moe_h_image(ma, gu, P, I, st, &h16, &rsh))) return rc;
     const typename FMoeDown<F>::Args da{(const uint8_t *)down, (size_t)(I / F::BS) * F::TS, I, P * H, H, k,
-                                        R.ids, R.w, shared, shared_gate, gu};
-    return launch_gemv<FMoeDown<F>>(da, gu, y, st);
+                                        R.ids, R.w, shared, shared_gate, h16, rsh, ma.bf};
+    return launch_gemv<FMoeDown<F>>(da, h16, y, st);
   }
   // streaming MFMA kernels from 3 tokens up; one or two tokens (a GEMV per expert) run faster on
   // the per-block kernels below, which start streaming without staging x
@@ -811,7 +877,7 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
       return t;
     };
     const VMoeGateUp gu{(const uint16_t *)x, (const uint8_t *)gate, (const uint8_t *)up,
-                        (size_t)(H / F::BS) * F::TS, H, I, R, h, k};
+                        (size_t)(H / F::BS) * F::TS, H, I, R, h, k, ma.rsx, ma.bf};
     int rc;
     if (route_in_gate_up(T, H, E, I, k)) {
       VMoeGateUpR gr{};
@@ -825,21 +891,24 @@ static int moe_ffn(const void *x, int T, int H, int E, int I, int k, const void 
       rc = moe_vgemm<F>(gu, T, E, k, H, tiles_gu * 16, amax, pick(tiles_gu, 1), st);
     }
     if (rc) return rc;
-    const VMoeDown dn{h, (const uint8_t *)down, (size_t)(I / F::BS) * F::TS, I, H, R, o};
+    if ((rc = moe_h_image(ma, h, T * k, I, st, &h16, &rsh))) return rc;
+    const VMoeDown dn{h16, (const uint8_t *)down, (size_t)(I / F::BS) * F::TS, I, H, R, o, rsh, ma.bf};
     rc = moe_vgemm<F>(dn, T, E, k, I, H, amax, pick(tiles_dn, 0), st);
     if (rc) return rc;
   } else {
     int ks = ks_for((I / 16) * amax, H / F::BS);
     hipLaunchKernelGGL((moe_gate_up_kernel<F>), dim3(I / 16, amax), dim3(64 * ks), (size_t)ks * 2 * 256 * 4, st,
-                       (const uint16_t *)x, H, (const uint8_t *)gate, (const uint8_t *)up, I, k, R, h);
+                       (const uint16_t *)x, H, (const uint8_t *)gate, (const uint8_t *)up, I, k, R, h, ma.rsx, ma.bf);
     ISHZ_LAUNCH_CHECK("moe gate/up launch");
+    int rc = moe_h_image(ma, h, T * k, I, st, &h16, &rsh);
+    if (rc) return rc;
     ks = ks_for((H / 32) * amax, I / F::BS);
     hipLaunchKernelGGL((moe_down_kernel<F>), dim3((H + 31) / 32, amax), dim3(64 * ks), (size_t)ks * 2 * 256 * 4,
-                       st, h, I, (const uint8_t *)down, H, R, o);
+                       st, h16, I, (const uint8_t *)down, H, R, o, rsh, ma.bf);
     ISHZ_LAUNCH_CHECK("moe down launch");
   }
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)std::min<size_t>((total + 255) / 256, 4096)), dim3(256), 0,
-                     st, o, H, T, k, R, shared, shared_gate, (uint16_t *)y);
+                     st, o, H, T, k, R, shared, shared_gate, (uint16_t *)y, ma.bf);
   ISHZ_LAUNCH_CHECK("moe combine launch");
   return ISHZ_OK;
 }
@@ -919,24 +988,28 @@ struct FMoeDownA : FMoeDown<F> {
 template <class F>
 static int moe_ffn_affine(const void *x, int T, int H, int E, int I, int k, const AffPack &gate, const AffPack &up,
                           const AffPack &down, const MoeTokens &rt, uint16_t *h, uint16_t *gu, uint16_t *o,
-                          const uint16_t *shared, const uint16_t *shared_gate, void *y, hipStream_t st) {
+                          const uint16_t *shared, const uint16_t *shared_gate, void *y, hipStream_t st,
+                          const MoeAct &ma) {
   const MoeRoute &R = rt.R;
+  const uint16_t *h16;
+  const float *rsh;
   const int amax = std::min(E, T * k);
   const size_t total = (size_t)T * H;
   if (gathered_gemv(T, H, I, k)) {  // as moe_ffn: every (token, slot) pair a GEMV, two launches
     const int P = T * k;
     typename FMoeGateUpA<F>::Args ga{};
-    static_cast<typename FMoeGateUp<F>::Args &>(ga) = typename FMoeGateUp<F>::Args{nullptr, nullptr, 0, H, P * 2 * I, I, k, rt,
-                                                                                    (const uint16_t *)x};
+    static_cast<typename FMoeGateUp<F>::Args &>(ga) = typename FMoeGateUp<F>::Args{
+        nullptr, nullptr, 0, H, P * 2 * I, I, k, rt, (const uint16_t *)x, ma.rsx, ma.bf};
     ga.g = gate;
     ga.u = up;
     int rc = launch_gemv<FMoeGateUpA<F>>(ga, x, gu, st);
     if (rc) return rc;
+    if ((rc = moe_h_image(ma, gu, P, I, st, &h16, &rsh))) return rc;
     typename FMoeDownA<F>::Args da{};
     static_cast<typename FMoeDown<F>::Args &>(da) =
-        typename FMoeDown<F>::Args{nullptr, 0, I, P * H, H, k, R.ids, R.w, shared, shared_gate, gu};
+        typename FMoeDown<F>::Args{nullptr, 0, I, P * H, H, k, R.ids, R.w, shared, shared_gate, h16, rsh, ma.bf};
     da.d = down;
-    return launch_gemv<FMoeDownA<F>>(da, gu, y, st);
+    return launch_gemv<FMoeDownA<F>>(da, h16, y, st);
   }
   const int tiles_gu = 2 * ((I + 15) / 16), tiles_dn = (H + 15) / 16;
   const int act = std::min(amax, 128);
@@ -946,18 +1019,19 @@ static int moe_ffn_affine(const void *x, int T, int H, int E, int I, int k, cons
     return t;
   };
   VMoeGateUpA pgu{};
-  static_cast<VMoeGateUp &>(pgu) = VMoeGateUp{(const uint16_t *)x, nullptr, nullptr, 0, H, I, R, h, k};
+  static_cast<VMoeGateUp &>(pgu) = VMoeGateUp{(const uint16_t *)x, nullptr, nullptr, 0, H, I, R, h, k, ma.rsx, ma.bf};
   pgu.g = gate;
   pgu.u = up;
   int rc = moe_vgemm<F>(pgu, T, E, k, H, tiles_gu * 16, amax, pick(tiles_gu, 1), st);
   if (rc) return rc;
+  if ((rc = moe_h_image(ma, h, T * k, I, st, &h16, &rsh))) return rc;
   VMoeDownA dn{};
-  static_cast<VMoeDown &>(dn) = VMoeDown{h, nullptr, 0, I, H, R, o};
+  static_cast<VMoeDown &>(dn) = VMoeDown{h16, nullptr, 0, I, H, R, o, rsh, ma.bf};
   dn.d = down;
   rc = moe_vgemm<F>(dn, T, E, k, I, H, amax, pick(tiles_dn, 0), st);
   if (rc) return rc;
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)std::min<size_t>((total + 255) / 256, 4096)), dim3(256), 0,
-                     st, o, H, T, k, R, shared, shared_gate, (uint16_t *)y);
+                     st, o, H, T, k, R, shared, shared_gate, (uint16_t *)y, ma.bf);
   ISHZ_LAUNCH_CHECK("moe combine launch");
   return ISHZ_OK;
 }
@@ -968,8 +1042,8 @@ static int moe_ffn_affine(const void *x, int T, int H, int E, int I, int k, cons
 #define ISHZ_MOE_AFFINE_ARGS                                                                                  \
   const void *x, int T, int H, int E, int I, int k, const AffPack &gate, const AffPack &up, const AffPack &down, \
       const MoeTokens &rt, uint16_t *h, uint16_t *gu, uint16_t *o, const uint16_t *shared,                     \
-      const uint16_t *shared_gate, void *y, hipStream_t st
-#define ISHZ_MOE_AFFINE_PASS x, T, H, E, I, k, gate, up, down, rt, h, gu, o, shared, shared_gate, y, st
+      const uint16_t *shared_gate, void *y, hipStream_t st, const MoeAct &ma
+#define ISHZ_MOE_AFFINE_PASS x, T, H, E, I, k, gate, up, down, rt, h, gu, o, shared, shared_gate, y, st, ma
 int moe_affine_w23(int bits, int group, bool bf16s, ISHZ_MOE_AFFINE_ARGS);
 int moe_affine_w567(int bits, int group, bool bf16s, ISHZ_MOE_AFFINE_ARGS);
 
@@ -1000,7 +1074,7 @@ extern "C" int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T,
   const int bs = ishz_ggml_block_size(type);
   if (type != ISHZ_GGML_Q4_K && type != ISHZ_GGML_Q6_K && type != ISHZ_GGML_Q4_0)
     return decline("MoE experts must be Q4_0, Q4_K or Q6_K");
-  if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
+  if (x_dtype != ISHZ_DT_F16 && x_dtype != ISHZ_DT_BF16) return decline("activations must be fp16 or bf16");
   if (T <= 0 || E <= 0 || topk <= 0 || topk > E || E > 4096) return decline("bad routing shape");
   if (topk > 64 || (size_t)4 * route_row_words(E, topk) * 4 > 160 * 1024)
     return decline("too many experts for one routing workgroup");
@@ -1025,10 +1099,17 @@ extern "C" int ishz_moe_swiglu(uint32_t type, const void *x, int x_dtype, int T,
   uint16_t *h = (uint16_t *)((uint8_t *)workspace + L.h), *o = (uint16_t *)((uint8_t *)workspace + L.o);
   uint16_t *gu = (uint16_t *)((uint8_t *)workspace + L.gu);
   const uint16_t *sh = (const uint16_t *)shared, *sg = (const uint16_t *)shared_gate;
+  MoeAct ma{x_dtype == ISHZ_DT_BF16, nullptr, (uint8_t *)workspace + L.himg};
+  if (ma.bf) {  // the model's activations in bf16 (MoEBlock runs in x.dtype): x's fp16 image
+    const uint16_t *x16;
+    const int rc = act_prepare(x, ISHZ_DT_BF16, T, H, (uint8_t *)workspace + L.ximg, st, &x16, &ma.rsx);
+    if (rc) return rc;
+    x = x16;
+  }
   switch (type) {
-  case ISHZ_GGML_Q4_K: return moe_ffn<FQ4_K>(x, T, H, E, I, topk, gate, up, down, rt, h, gu, o, sh, sg, y, st);
-  case ISHZ_GGML_Q6_K: return moe_ffn<FQ6_K>(x, T, H, E, I, topk, gate, up, down, rt, h, gu, o, sh, sg, y, st);
-  default: return moe_ffn<FQ4_0>(x, T, H, E, I, topk, gate, up, down, rt, h, gu, o, sh, sg, y, st);
+  case ISHZ_GGML_Q4_K: return moe_ffn<FQ4_K>(x, T, H, E, I, topk, gate, up, down, rt, h, gu, o, sh, sg, y, st, ma);
+  case ISHZ_GGML_Q6_K: return moe_ffn<FQ6_K>(x, T, H, E, I, topk, gate, up, down, rt, h, gu, o, sh, sg, y, st, ma);
+  default: return moe_ffn<FQ4_0>(x, T, H, E, I, topk, gate, up, down, rt, h, gu, o, sh, sg, y, st, ma);
   }
 }
 
@@ -1044,7 +1125,7 @@ extern "C" int ishz_moe_swiglu_affine(const void *x, int x_dtype, int T, int H, 
   if (bits < 2 || bits > 8) return decline("affine experts of 2 to 8 bits are decoded in-kernel");
   if (group != 64 && group != 128) return decline("group size must be 64 or 128");
   if (scale_dtype != ISHZ_DT_F16 && scale_dtype != ISHZ_DT_BF16) return decline("scales must be fp16 or bf16");
-  if (x_dtype != ISHZ_DT_F16) return decline("activations must be fp16");
+  if (x_dtype != ISHZ_DT_F16 && x_dtype != ISHZ_DT_BF16) return decline("activations must be fp16 or bf16");
   if (T <= 0 || E <= 0 || topk <= 0 || topk > E || E > 4096) return decline("bad routing shape");
   if (topk > 64 || (size_t)4 * route_row_words(E, topk) * 4 > 160 * 1024)
     return decline("too many experts for one routing workgroup");
@@ -1071,9 +1152,17 @@ extern "C" int ishz_moe_swiglu_affine(const void *x, int x_dtype, int T, int H, 
   const AffPack upk{up_codes, (const uint16_t *)up_scales, (const uint16_t *)up_biases, H * bits / 32, H / group};
   const AffPack dp{down_codes, (const uint16_t *)down_scales, (const uint16_t *)down_biases, I * bits / 32, I / group};
   const bool bf = scale_dtype == ISHZ_DT_BF16;
-#define ISHZ_MA(B, G)                                                                                        \
-  return bf ? moe_ffn_affine<FAffineN<B, G, true>>(x, T, H, E, I, topk, gp, upk, dp, rt, h, gu, o, sh, sg, y, st) \
-            : moe_ffn_affine<FAffineN<B, G, false>>(x, T, H, E, I, topk, gp, upk, dp, rt, h, gu, o, sh, sg, y, st)
+  MoeAct ma{x_dtype == ISHZ_DT_BF16, nullptr, (uint8_t *)workspace + L.himg};
+  if (ma.bf) {  // bf16 activations: x's fp16 image
+    const uint16_t *x16;
+    const int rc = act_prepare(x, ISHZ_DT_BF16, T, H, (uint8_t *)workspace + L.ximg, st, &x16, &ma.rsx);
+    if (rc) return rc;
+    x = x16;
+  }
+#define ISHZ_MA(B, G)                                                                                          \
+  return bf ? moe_ffn_affine<FAffineN<B, G, true>>(x, T, H, E, I, topk, gp, upk, dp, rt, h, gu, o, sh, sg, y, st, \
+                                                   ma)                                                        \
+            : moe_ffn_affine<FAffineN<B, G, false>>(x, T, H, E, I, topk, gp, upk, dp, rt, h, gu, o, sh, sg, y, st, ma)
   if (bits == 4) {
     if (group == 64) ISHZ_MA(4, 64);
     ISHZ_MA(4, 128);
@@ -1083,7 +1172,8 @@ extern "C" int ishz_moe_swiglu_affine(const void *x, int x_dtype, int T, int H, 
     ISHZ_MA(8, 128);
   }
 #undef ISHZ_MA
-  if (bits <= 3) return moe_affine_w23(bits, group, bf, x, T, H, E, I, topk, gp, upk, dp, rt, h, gu, o, sh, sg, y, st);
-  return moe_affine_w567(bits, group, bf, x, T, H, E, I, topk, gp, upk, dp, rt, h, gu, o, sh, sg, y, st);
+  if (bits <= 3)
+    return moe_affine_w23(bits, group, bf, x, T, H, E, I, topk, gp, upk, dp, rt, h, gu, o, sh, sg, y, st, ma);
+  return moe_affine_w567(bits, group, bf, x, T, H, E, I, topk, gp, upk, dp, rt, h, gu, o, sh, sg, y, st, ma);
 }
 #endif  // ISHZ_MOE_BODY_ONLY

@@ -253,3 +253,107 @@ def test_swiglu_affine_shared_expert(T):
     ref = affine_moe_reference(x.astype(np.float32), rid, rw, packs, E, H, I, bits, group,
                                shared=sh.astype(np.float32), shared_gate=sg.astype(np.float32))
     assert_close(y.float().cpu().numpy(), ref, what=f"moe affine shared T={T}")
+
+
+def bf16r(a):
+    """Values rounded to bf16 (round to nearest even), as float32."""
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16).float().numpy()
+
+
+def moe_reference_bf16(x, rid, rw, Wg, Wu, Wd, shared=None, shared_gate=None):
+    """MoEBlock.callAsFunction + ResidentExperts.swiglu in bf16 (Text/MoEBlock.swift:124-171):
+    every projection output and SwiGLU op rounded to bf16, the k slots weighted and summed in
+    fp32 in slot order, the shared expert's bf16 term added in fp32, narrowed once. Returns
+    (ref, bound) with bound_t = sum_s w_s |Wd[e_s]| @ |h_s| (+ |shared|)."""
+    T, k = rid.shape
+    ref = np.zeros((T, Wd.shape[1]), np.float32)
+    bound = np.zeros((T, Wd.shape[1]), np.float64)
+    for t in range(T):
+        acc = np.zeros(Wd.shape[1], np.float32)
+        for s in range(k):
+            e = rid[t, s]
+            g = bf16r(Wg[e] @ x[t].astype(np.float64))
+            u = bf16r(Wu[e] @ x[t].astype(np.float64))
+            with np.errstate(over="ignore"):  # exp(-g) = inf for very negative g: sigmoid 0
+                sg = bf16r(1.0 / (1.0 + np.exp(-g.astype(np.float64))))
+            h = bf16r(bf16r(g * sg) * u)
+            o = bf16r(Wd[e] @ h.astype(np.float64))
+            acc = (acc + o * np.float32(rw[t, s])).astype(np.float32)
+            bound[t] += float(rw[t, s]) * (np.abs(Wd[e]) @ np.abs(h.astype(np.float64)))
+        if shared is not None:
+            sgt = bf16r(1.0 / (1.0 + np.exp(-np.float64(shared_gate[t]))))
+            acc = (acc + bf16r(sgt * shared[t])).astype(np.float32)
+            bound[t] += np.abs(shared[t])
+        ref[t] = bf16r(acc)
+    return ref, bound
+
+
+def check_bf16(y, ref, bound, what):
+    """bf16 intermediates formed in another summation order may round one bf16 ulp (2^-8) the
+    other way: 2^-7 of the bound leaves room for a few such flips; plus the output's own rounding."""
+    y = y.float().cpu().numpy().astype(np.float64)
+    lim = 2.0 ** -7 * bound + 2.0 ** -8 * np.abs(ref) + 1e-30
+    assert np.all(np.isfinite(y)), f"{what}: non-finite"
+    bad = np.abs(y - ref) > lim
+    assert not bad.any(), f"{what}: {int(bad.sum())} outside; worst {np.max(np.abs(y - ref) / lim):.3g}x"
+
+
+@pytest.mark.parametrize("T,type_", [(1, ggml.Q4_K), (2, ggml.Q6_K), (5, ggml.Q4_K), (20, ggml.Q4_0), (3, ggml.Q6_K)])
+def test_swiglu_bf16(T, type_):
+    """The MoE FFN in bf16 (MoEBlock runs in the model's dtype): every stage's bf16 roundings,
+    bf16 x and h staged from fp16 images with a factor per row, against a bf16 restatement."""
+    E, H, I, k = 16, 512, 256, 4
+    (g, u, d), ex = experts(E, H, I, type_, seed=T + 100, scale=0.002)
+    x = torch.from_numpy(synth.fp16_normal((T, H), seed=T + 101).astype(np.float32) * 30.0).to(torch.bfloat16)
+    logits = np.random.default_rng(T + 102).standard_normal((T, E)).astype(np.float32)
+    print(f"moe bf16 T={T} type={type_}", flush=True)
+    y, ids, w = moe.swiglu(x.to(DEV), torch.from_numpy(logits).to(DEV), ex, top_k=k, return_routing=True)
+    assert y is not None and y.dtype == torch.bfloat16
+    rid, rw = oracle.moe_route(logits, k)
+    assert np.array_equal(ids.cpu().numpy(), rid)
+    Wg = oracle.dequant_rows(type_, g, E * I, H).reshape(E, I, H).astype(np.float64)
+    Wu = oracle.dequant_rows(type_, u, E * I, H).reshape(E, I, H).astype(np.float64)
+    Wd = oracle.dequant_rows(type_, d, E * H, I).reshape(E, H, I).astype(np.float64)
+    ref, bd = moe_reference_bf16(x.float().numpy(), rid, rw, Wg, Wu, Wd)
+    check_bf16(y, ref, bd, f"moe bf16 T={T}")
+
+
+@pytest.mark.parametrize("T,bits", [(1, 4), (2, 8), (6, 4), (17, 3)])
+def test_swiglu_affine_bf16(T, bits):
+    """Affine experts (bf16 scales, as a bf16 MLX model ships them) with bf16 activations and the
+    shared expert, against the bf16 restatement."""
+    E, H, I, k, group = 16, 512, 256, 4, 64
+    packs = []
+    for i, (rows, K) in enumerate(((I, H), (I, H), (H, I))):
+        c, sc, b = synth.affine_pack_bits(E * rows, K, bits, group=group, seed=T + 110 + i, scale=0.087 / 2 ** (bits - 1))
+        packs.append((c, bf16r(sc.astype(np.float32)), bf16r(b.astype(np.float32))))
+    dev = lambda a: torch.from_numpy(a).to(DEV)
+    tens = [(dev(c.view(np.int32)), dev(sc).to(torch.bfloat16), dev(b).to(torch.bfloat16)) for c, sc, b in packs]
+    ex = moe.AffineExperts(tens[0], tens[1], tens[2], bits, group, E, H, I)
+    x = torch.from_numpy(synth.fp16_normal((T, H), seed=T + 111)).to(torch.bfloat16)
+    logits = np.random.default_rng(T + 112).standard_normal((T, E)).astype(np.float32)
+    sh = torch.from_numpy(synth.fp16_normal((T, H), seed=T + 113).astype(np.float32) * 0.05).to(torch.bfloat16)
+    sg = torch.from_numpy(synth.fp16_normal((T,), seed=T + 114)).to(torch.bfloat16)
+    print(f"moe affine bf16 T={T} bits={bits}", flush=True)
+    y = moe.swiglu_affine(x.to(DEV), torch.from_numpy(logits).to(DEV), ex, top_k=k, shared=sh.to(DEV),
+                          shared_gate=sg.to(DEV))
+    assert y is not None and y.dtype == torch.bfloat16
+    rid, rw = oracle.moe_route(logits, k)
+    bf16bits = lambda a: torch.from_numpy(a).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    W = []
+    for (c, sc, b), (rows, K) in zip(packs, ((I, H), (I, H), (H, I))):
+        # bf16 scales: the oracle's dequantizer takes fp16 bits, so dequantize in numpy
+        q = np.zeros((E * rows, K), np.float64)
+        words = c.view(np.uint32).reshape(E * rows, -1).astype(np.uint64)
+        for kk in range(K):
+            bit = kk * bits
+            wv = words[:, bit // 32]
+            if bit // 32 + 1 < words.shape[1]:
+                wv = wv | (words[:, bit // 32 + 1] << np.uint64(32))
+            q[:, kk] = ((wv >> np.uint64(bit % 32)) & np.uint64((1 << bits) - 1)).astype(np.float64)
+        s_ = np.repeat(sc.astype(np.float64), group, axis=1)
+        b_ = np.repeat(b.astype(np.float64), group, axis=1)
+        W.append((s_ * q + b_).astype(np.float32).astype(np.float64).reshape(E, rows, K))
+    ref, bd = moe_reference_bf16(x.float().numpy(), rid, rw, *W, shared=sh.float().numpy(),
+                                 shared_gate=sg.float().numpy())
+    check_bf16(y, ref, bd, f"moe affine bf16 T={T} bits={bits}")
