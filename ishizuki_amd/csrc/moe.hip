@@ -272,15 +272,26 @@ DEV float bf16_round(float v) {
   u = ((u & 0x7fffffffu) > 0x7f800000u) ? (u | 0x400000u) : u + 0x7fffu + ((u >> 16) & 1u);
   return __builtin_bit_cast(float, u & 0xffff0000u);
 }
-DEV float rnd(float v, bool bf) { return bf ? bf16_round(v) : r16(v); }
-DEV uint16_t bits16(float v, bool bf) { return bf ? (uint16_t)(__builtin_bit_cast(uint32_t, bf16_round(v)) >> 16) : f2h(v); }
-DEV float from16(uint32_t b, bool bf) { return bf ? __builtin_bit_cast(float, b << 16) : h2f(b); }
+template <bool BF>
+DEV float rnd(float v) { return BF ? bf16_round(v) : r16(v); }
+template <bool BF>
+DEV uint16_t bits16(float v) { return BF ? (uint16_t)(__builtin_bit_cast(uint32_t, bf16_round(v)) >> 16) : f2h(v); }
+template <bool BF>
+DEV float from16(uint32_t b) { return BF ? __builtin_bit_cast(float, b << 16) : h2f(b); }
 // h = silu(g) * u with the reference's roundings (Text/MoEBlock.swift:168-171): g and u the
 // projections' outputs, sigmoid, g * sigmoid and the product each rounded to the activation type.
-DEV uint16_t swiglu16(float gs, float us, bool bf) {
-  const float g = rnd(gs, bf), u = rnd(us, bf);
-  const float sg = rnd(1.0f / (1.0f + __expf(-g)), bf);
-  return bits16(rnd(g * sg, bf) * u, bf);
+template <bool BF>
+DEV uint16_t swiglu16(float gs, float us) {
+  const float g = rnd<BF>(gs), u = rnd<BF>(us);
+  const float sg = rnd<BF>(1.0f / (1.0f + __expf(-g)));
+  return bits16<BF>(rnd<BF>(g * sg) * u);
+}
+// fn<BF>() with the activation type fixed at compile time: the fp16 epilogues carry no trace of
+// the bf16 path (no factor loads, no per-value dtype tests).
+template <class Fn>
+DEV void by_act(bool bf, Fn &&fn) {
+  if (bf) fn.template operator()<true>();
+  else fn.template operator()<false>();
 }
 
 // gate + up for one 16-row tile of I of one active expert, 16 routed tokens at a time.
@@ -311,19 +322,21 @@ __global__ __launch_bounds__(1024) void moe_gate_up_kernel(const uint16_t *__res
 #pragma unroll
       for (int r = 0; r < 4; r++) red[((wave * 2 + t) * 4 + r) * 64 + lane] = acc[t][r];
     __syncthreads();
-    for (int o = threadIdx.x; o < 256; o += blockDim.x) {
-      const int r = o >> 6, l = o & 63;
-      float gs = 0.0f, us = 0.0f;
-      for (int v = 0; v < KS; v++) {
-        gs += red[((v * 2 + 0) * 4 + r) * 64 + l];
-        us += red[((v * 2 + 1) * 4 + r) * 64 + l];
+    by_act(bf, [&]<bool BF>() {
+      for (int o = threadIdx.x; o < 256; o += blockDim.x) {
+        const int r = o >> 6, l = o & 63;
+        float gs = 0.0f, us = 0.0f;
+        for (int v = 0; v < KS; v++) {
+          gs += red[((v * 2 + 0) * 4 + r) * 64 + l];
+          us += red[((v * 2 + 1) * 4 + r) * 64 + l];
+        }
+        const int t = 4 * (l >> 4) + r, i = i0 + (l & 15);
+        if (c0 + t < p1 && i < I) {
+          const float f = BF ? rs[R.pair_q[c0 + t] / k] : 1.0f;  // x's row factor (bf16 x)
+          h[(size_t)(c0 + t) * I + i] = swiglu16<BF>(gs * f, us * f);
+        }
       }
-      const int t = 4 * (l >> 4) + r, i = i0 + (l & 15);
-      if (c0 + t < p1 && i < I) {
-        const float f = rs ? rs[R.pair_q[c0 + t] / k] : 1.0f;  // x's row factor (bf16 x)
-        h[(size_t)(c0 + t) * I + i] = swiglu16(gs * f, us * f, bf);
-      }
-    }
+    });
     __syncthreads();
   }
 }
@@ -355,14 +368,16 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(const uint16_t *__restri
 #pragma unroll
       for (int r = 0; r < 4; r++) red[((wave * 2 + t) * 4 + r) * 64 + lane] = acc[t][r];
     __syncthreads();
-    for (int q = threadIdx.x; q < 512; q += blockDim.x) {
-      const int t2 = q >> 8, r = (q >> 6) & 3, l = q & 63;
-      float s = 0.0f;
-      for (int v = 0; v < KS; v++) s += red[((v * 2 + t2) * 4 + r) * 64 + l];
-      const int t = 4 * (l >> 4) + r, n = n0 + 16 * t2 + (l & 15);
-      if (c0 + t < p1 && n < H)  // slot order; h's row factor (bf16)
-        o[(size_t)R.pair_q[c0 + t] * H + n] = bits16(rs ? s * rs[c0 + t] : s, bf);
-    }
+    by_act(bf, [&]<bool BF>() {
+      for (int q = threadIdx.x; q < 512; q += blockDim.x) {
+        const int t2 = q >> 8, r = (q >> 6) & 3, l = q & 63;
+        float s = 0.0f;
+        for (int v = 0; v < KS; v++) s += red[((v * 2 + t2) * 4 + r) * 64 + l];
+        const int t = 4 * (l >> 4) + r, n = n0 + 16 * t2 + (l & 15);
+        if (c0 + t < p1 && n < H)  // slot order; h's row factor (bf16)
+          o[(size_t)R.pair_q[c0 + t] * H + n] = bits16<BF>(BF ? s * rs[c0 + t] : s);
+      }
+    });
     __syncthreads();
   }
 }
@@ -373,19 +388,21 @@ static __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t 
                                                           const uint16_t *__restrict__ shared_gate,
                                                           uint16_t *__restrict__ y, bool bf) {
   const size_t total = (size_t)T * H;
-  for (size_t q = blockIdx.x * (size_t)blockDim.x + threadIdx.x; q < total;
-       q += (size_t)gridDim.x * blockDim.x) {
-    const int t = (int)(q / H), n = (int)(q % H);
-    float acc = 0.0f;
-    for (int s = 0; s < k; s++) {
-      acc += from16(o[((size_t)t * k + s) * H + n], bf) * R.w[t * k + s];  // o rows in slot order
+  by_act(bf, [&]<bool BF>() {
+    for (size_t q = blockIdx.x * (size_t)blockDim.x + threadIdx.x; q < total;
+         q += (size_t)gridDim.x * blockDim.x) {
+      const int t = (int)(q / H), n = (int)(q % H);
+      float acc = 0.0f;
+      for (int s = 0; s < k; s++) {
+        acc += from16<BF>(o[((size_t)t * k + s) * H + n]) * R.w[t * k + s];  // o rows in slot order
+      }
+      if (shared) {  // the shared expert, widened and added before the one narrowing
+        const float sg = rnd<BF>(1.0f / (1.0f + __expf(-from16<BF>(shared_gate[t]))));
+        acc += rnd<BF>(sg * from16<BF>(shared[q]));
+      }
+      y[q] = bits16<BF>(acc);
     }
-    if (shared) {  // the shared expert, widened and added before the one narrowing
-      const float sg = rnd(1.0f / (1.0f + __expf(-from16(shared_gate[t], bf))), bf);
-      acc += rnd(sg * from16(shared[q], bf), bf);
-    }
-    y[q] = bits16(acc, bf);
-  }
+  });
 }
 
 // ------------------------------------------------------------------- streaming (MFMA) FFN
@@ -427,15 +444,17 @@ struct VMoeGateUp {
   // pq: the sorted pairs' slot indices as this launch knows them (global, or the workgroup's own
   // LDS copy when it routes itself)
   DEV void finish_pairs(const Group &g, int c0, int m, int tb, int te, const float *out, const int32_t *pq) const {
-    for (int o = threadIdx.x; o < (te - tb) / 2 * 256; o += blockDim.x) {
-      const int pr = o >> 8, tk = (o >> 4) & 15, nn = o & 15;
-      const int i = ((tb >> 1) + pr) * 16 + nn;
-      if (tk < m && i < I) {
-        const float f = rs ? rs[pq[g.p0 + c0 + tk] / k] : 1.0f;
-        h[(size_t)(g.p0 + c0 + tk) * I + i] =
-            swiglu16(out[(2 * pr) * 256 + tk * 16 + nn] * f, out[(2 * pr + 1) * 256 + tk * 16 + nn] * f, bf);
+    by_act(bf, [&]<bool BF>() {
+      for (int o = threadIdx.x; o < (te - tb) / 2 * 256; o += blockDim.x) {
+        const int pr = o >> 8, tk = (o >> 4) & 15, nn = o & 15;
+        const int i = ((tb >> 1) + pr) * 16 + nn;
+        if (tk < m && i < I) {
+          const float f = BF ? rs[pq[g.p0 + c0 + tk] / k] : 1.0f;
+          h[(size_t)(g.p0 + c0 + tk) * I + i] =
+              swiglu16<BF>(out[(2 * pr) * 256 + tk * 16 + nn] * f, out[(2 * pr + 1) * 256 + tk * 16 + nn] * f);
+        }
       }
-    }
+    });
   }
 };
 
@@ -535,11 +554,13 @@ struct VMoeDown {
   DEV const uint16_t *xrow(const Group &g, int tk) const { return h + (size_t)(g.p0 + tk) * I; }
   DEV const uint8_t *wrow(const Group &g, int row) const { return down + ((size_t)g.e * H + row) * rb; }
   DEV void finish(const Group &g, int c0, int m, int tb, int te, const float *out) const {
-    for (int q = threadIdx.x; q < (te - tb) * 256; q += blockDim.x) {
-      const int tk = (q >> 4) & 15, row = (tb + (q >> 8)) * 16 + (q & 15);
-      if (tk < m && row < H)  // slot order
-        o[(size_t)R.pair_q[g.p0 + c0 + tk] * H + row] = bits16(rs ? out[q] * rs[g.p0 + c0 + tk] : out[q], bf);
-    }
+    by_act(bf, [&]<bool BF>() {
+      for (int q = threadIdx.x; q < (te - tb) * 256; q += blockDim.x) {
+        const int tk = (q >> 4) & 15, row = (tb + (q >> 8)) * 16 + (q & 15);
+        if (tk < m && row < H)  // slot order
+          o[(size_t)R.pair_q[g.p0 + c0 + tk] * H + row] = bits16<BF>(BF ? out[q] * rs[g.p0 + c0 + tk] : out[q]);
+      }
+    });
   }
 };
 
@@ -650,12 +671,14 @@ struct FMoeGateUp : F {
   }
   // rows row0 .. row0 + nrows: whole eight-row blocks; h [P][I] fp16
   static DEV void store(const Args &a, uint16_t *h, int row0, int nrows, const float *vals) {
-    for (int q = threadIdx.x; q < nrows / 2; q += blockDim.x) {
-      const int blk = q >> 2, i4 = q & 3, j = row0 + 8 * blk;
-      const int p = j / (2 * a.I), i = wrow(j - p * 2 * a.I) + i4;
-      const float f = a.rs ? a.rs[p / a.k] : 1.0f;
-      h[(size_t)p * a.I + i] = swiglu16(vals[8 * blk + i4] * f, vals[8 * blk + 4 + i4] * f, a.bf);
-    }
+    by_act(a.bf, [&]<bool BF>() {
+      for (int q = threadIdx.x; q < nrows / 2; q += blockDim.x) {
+        const int blk = q >> 2, i4 = q & 3, j = row0 + 8 * blk;
+        const int p = j / (2 * a.I), i = wrow(j - p * 2 * a.I) + i4;
+        const float f = BF ? a.rs[p / a.k] : 1.0f;
+        h[(size_t)p * a.I + i] = swiglu16<BF>(vals[8 * blk + i4] * f, vals[8 * blk + 4 + i4] * f);
+      }
+    });
   }
 };
 
@@ -728,20 +751,22 @@ struct FMoeDown : F {
   // position, its k slots' fp16 rows weighted in fp32 in slot order, then the shared term.
   static DEV void store(const Args &a, uint16_t *y, int row0, int nrows, const float *vals, const Prep &pp) {
     const int run = 4 * a.k;
-    for (int q = threadIdx.x; q < nrows / a.k; q += blockDim.x) {
-      const int blk = q >> 2, rr = q & 3, j0 = row0 + blk * run;
-      const int t = j0 / (a.H * a.k), r = out_of(a, j0) + rr;
-      float acc = 0.0f;
-      for (int s = 0; s < a.k; s++) {
-        const float v = vals[blk * run + 4 * s + rr] * (a.rs ? a.rs[t * a.k + s] : 1.0f);
-        acc += rnd(v, a.bf) * pp.w[t * a.k + s];
+    by_act(a.bf, [&]<bool BF>() {
+      for (int q = threadIdx.x; q < nrows / a.k; q += blockDim.x) {
+        const int blk = q >> 2, rr = q & 3, j0 = row0 + blk * run;
+        const int t = j0 / (a.H * a.k), r = out_of(a, j0) + rr;
+        float acc = 0.0f;
+        for (int s = 0; s < a.k; s++) {
+          const float v = vals[blk * run + 4 * s + rr];
+          acc += rnd<BF>(BF ? v * a.rs[t * a.k + s] : v) * pp.w[t * a.k + s];
+        }
+        if (a.shared) {
+          const float sg = rnd<BF>(1.0f / (1.0f + __expf(-from16<BF>(a.shared_gate[t]))));
+          acc += rnd<BF>(sg * from16<BF>(a.shared[(size_t)t * a.H + r]));
+        }
+        y[(size_t)t * a.H + r] = bits16<BF>(acc);
       }
-      if (a.shared) {
-        const float sg = rnd(1.0f / (1.0f + __expf(-from16(a.shared_gate[t], a.bf))), a.bf);
-        acc += rnd(sg * from16(a.shared[(size_t)t * a.H + r], a.bf), a.bf);
-      }
-      y[(size_t)t * a.H + r] = bits16(acc, a.bf);
-    }
+    });
   }
 };
 
