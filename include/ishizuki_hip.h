@@ -188,7 +188,9 @@ int ishz_exl3_apply(const void *x, int x_dtype, int M, int K, const int16_t *tre
    until the process ends. Shapes whose ishz_exl3_workspace_size exceeds it give ISHZ_EINVAL.
    `stream` must belong to the current device. Calls that overlap on one GPU share the scratch
    and race: serialise them (one stream, or events). Same results as ishz_exl3_apply. */
+#ifndef ISHZ_EXL3_STATIC_SCRATCH_BYTES /* a build of the library may set it smaller (-D) */
 #define ISHZ_EXL3_STATIC_SCRATCH_BYTES (32u << 20)
+#endif
 int ishz_exl3_apply_static(const void *x, int x_dtype, int M, int K, const int16_t *trellis,
                            const uint16_t *suh, const uint16_t *svh, int N, int bits2, int codebook,
                            void *y, ishz_stream_t stream);
