@@ -141,3 +141,50 @@ def test_config1_affine_linearity(M):
     # only to that tolerance
     _properties(lambda x: affine.linear(x, wd, sd, bd, signs=torch.from_numpy(signs), block=128, group_size=64),
                 x1, x2, bound_of, 2e-3, f"affine M={M}", exact_scale=False)
+
+
+@pytest.mark.parametrize("t", [ggml.Q4_K, ggml.Q6_K])
+def test_north_star_fp32(t):
+    """fp32 activations at the north-star shape: the exact-weight fp32 path against the oracle's
+    dequantize-then-fp32-dot, per element within 1e-5 of sum |x||w| (the reference's fp32
+    criterion, GGMLKernelTests.swift:131-137), M = 1 and 8."""
+    N, K = 17408, 5120
+    blk = synth.ggml_blocks(t, N, K, seed=90 + t)
+    x = np.random.default_rng(91).standard_normal((8, K)).astype(np.float32)
+    ref, bound = ggml_reference(t, x, blk, N)
+    wb = torch.from_numpy(blk).to(DEV)
+    for M in (1, 8):
+        print(f"north-star fp32 type={t} M={M}", flush=True)
+        y = ggml.matvec(torch.from_numpy(x[:M]).to(DEV), wb, t, N)
+        assert y is not None and y.dtype == torch.float32
+        err = np.abs(y.cpu().numpy().astype(np.float64) - ref[:M])
+        assert np.all(err <= 1e-5 * bound[:M]), f"worst {np.max(err / (1e-5 * bound[:M])):.3g}x"
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_config1_affine_rotated_act_dtypes(dt):
+    """BASELINE configs[1] (17408x5120, g64, 128-point rotation) with bf16 and fp32 activations,
+    M = 1 and 8: rotated in x's dtype, then the product (fp32: exact weights, 1e-5 of the bound;
+    bf16: the fp16 kernels' bound plus bf16's own roundings of x, the rotation and y)."""
+    N, K = 17408, 5120
+    codes, s, b = synth.affine_pack(N, K, group=64, seed=0xA1)
+    signs = synth.hadamard_signs(K, seed=0xA2)
+    xt = torch.from_numpy(np.random.default_rng(0xA3).standard_normal((8, K)).astype(np.float32)).to(dt)
+    xf = xt.float().numpy()
+    xr = oracle.hadamard(xf, 128, signs)
+    if dt == torch.bfloat16:
+        xr = torch.from_numpy(xr).to(torch.bfloat16).float().numpy()
+    ref = oracle.affine_matmul(xr, codes, s.view(np.uint16), b.view(np.uint16), N, 2, 64)
+    W = oracle.affine_dequant(codes, s.view(np.uint16), b.view(np.uint16), N, K, 2, 64)
+    bound = np.abs(xr) @ np.abs(W).T
+    args = [torch.from_numpy(a).to(DEV) for a in (codes.view(np.int32), s, b)]
+    for M in (1, 8):
+        print(f"config1 {dt} M={M}", flush=True)
+        y = affine.linear(xt[:M].to(DEV), *args, signs=torch.from_numpy(signs), block=128, group_size=64, bits=2)
+        assert y is not None and y.dtype == dt
+        yv = y.float().cpu().numpy().astype(np.float64)
+        if dt == torch.float32:
+            lim = 1e-5 * bound[:M]
+        else:  # a rotated value's bf16 rounding may go the other way (fp32 butterfly order): 40x slack
+            lim = 40 * 1e-4 * bound[:M] + 2.0 ** -8 * np.abs(ref[:M])
+        assert np.all(np.abs(yv - ref[:M]) <= lim), f"{dt} M={M}: worst {np.max(np.abs(yv - ref[:M]) / lim):.3g}x"

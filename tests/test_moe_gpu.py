@@ -266,10 +266,11 @@ def moe_reference_bf16(x, rid, rw, Wg, Wu, Wd, shared=None, shared_gate=None):
     fp32 in slot order, the shared expert's bf16 term added in fp32, narrowed once. Returns
     (ref, bound) with bound_t = sum_s w_s |Wd[e_s]| @ |h_s| (+ |shared|)."""
     T, k = rid.shape
-    ref = np.zeros((T, Wd.shape[1]), np.float32)
-    bound = np.zeros((T, Wd.shape[1]), np.float64)
+    H = x.shape[1]
+    ref = np.zeros((T, H), np.float32)
+    bound = np.zeros((T, H), np.float64)
     for t in range(T):
-        acc = np.zeros(Wd.shape[1], np.float32)
+        acc = np.zeros(H, np.float32)
         for s in range(k):
             e = rid[t, s]
             g = bf16r(Wg[e] @ x[t].astype(np.float64))
@@ -357,3 +358,27 @@ def test_swiglu_affine_bf16(T, bits):
     ref, bd = moe_reference_bf16(x.float().numpy(), rid, rw, *W, shared=sh.float().numpy(),
                                  shared_gate=sg.float().numpy())
     check_bf16(y, ref, bd, f"moe affine bf16 T={T} bits={bits}")
+
+
+@pytest.mark.parametrize("T", [1, 8, 64])
+def test_config4_qwen_moe_bf16(T):
+    """BASELINE configs[4] (128 Q4_K experts, H 2048, I 768, top-8) with bf16 activations at
+    T = 1, 8 and 64: the gathered GEMVs, the routing-in-gate/up MFMA path, and the routed one
+    (routing launch first)."""
+    E, H, I, k = 128, 2048, 768, 8
+    (g, u, d), ex = experts(E, H, I, ggml.Q4_K, seed=0xB0, scale=4e-4)
+    x = torch.from_numpy(synth.fp16_normal((T, H), seed=0xB1 + T)).to(torch.bfloat16)
+    logits = np.random.default_rng(0xB2 + T).standard_normal((T, E)).astype(np.float32)
+    print(f"config4 bf16 T={T}", flush=True)
+    y = moe.swiglu(x.to(DEV), torch.from_numpy(logits).to(DEV), ex, top_k=k)
+    assert y is not None and y.dtype == torch.bfloat16
+    rid, rw = oracle.moe_route(logits, k)
+    bs, ts = 256, 144
+    gb, db = I * (H // bs) * ts, H * (I // bs) * ts
+    Wg, Wu, Wd = {}, {}, {}  # the routed experts only, float32
+    for e in sorted(set(int(e) for e in rid.ravel())):
+        Wg[e] = oracle.dequant_rows(ggml.Q4_K, g[e * gb:(e + 1) * gb], I, H)
+        Wu[e] = oracle.dequant_rows(ggml.Q4_K, u[e * gb:(e + 1) * gb], I, H)
+        Wd[e] = oracle.dequant_rows(ggml.Q4_K, d[e * db:(e + 1) * db], H, I)
+    ref, bd = moe_reference_bf16(x.float().numpy(), rid, rw, Wg, Wu, Wd)
+    check_bf16(y, ref, bd, f"config4 bf16 T={T}")
