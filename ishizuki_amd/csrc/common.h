@@ -156,6 +156,13 @@ struct Out {
   }
 };
 
+#ifdef ISHZ_TIMING
+// Measurement builds only (-DISHZ_TIMING, never in the library): per-wave s_memrealtime stamps
+// (100 MHz) at a kernel's phase boundaries, for a timeline of its phases; read back from the host
+// with hipMemcpyFromSymbol.
+__device__ uint64_t ishz_timing[4096 * 5];
+#endif
+
 // ---------------------------------------------------------------- MFMA
 // C[i][j] += sum_k A[i][k] B[k][j], 16x16 fp32 tile. Lane l holds A row l%16 and B column l%16
 // (k slots chosen by l/16; any consistent k order works) and C rows 4*(l/16)+r, column l%16.

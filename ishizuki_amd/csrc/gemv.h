@@ -115,12 +115,6 @@ __host__ __device__ constexpr int gemv_threads() {
   else return 256;
 }
 
-#ifdef ISHZ_TIMING
-// Measurement builds only (-DISHZ_TIMING, never in the library): per-wave s_memrealtime stamps
-// (100 MHz) at kernel entry, after x is staged, and after the weight loop, for a timeline of the
-// phases; read back from the host with hipMemcpyFromSymbol.
-__device__ uint64_t ishz_timing[4096 * 5];
-#endif
 template <class F, int LPR, int D, bool RAGGED>
 __global__ __launch_bounds__((gemv_threads<F, LPR>())) void gemv_kernel(typename F::Args args, const uint16_t *__restrict__ x,
                                                    Out out, int nwg, int part_off) {
