@@ -250,16 +250,20 @@ __global__ __launch_bounds__(512) void affine_vgemm(const uint16_t *__restrict__
       const int IWf = F::img_words(K), ugf = (K / 64 + 15) / 16, g0 = kc0 / 1024;
       const int ugt = (ucs + 15) / 16;  // groups in this chunk (the last may be short)
       const int ns = ugt * 16 * R, nq = ugt * 16 * F::Q / 4;
-      // straight into LDS (global_load_lds_dwordx4), every wave's chunks of 64 words in flight at
-      // once: a loop of load-then-store copies waits out one memory latency per word a thread copies
-      const int cs = (ns + 63) / 64, cpt = cs + (nq + 63) / 64;
-      for (int c = wave; c < M * cpt; c += nw) {
-        const int tk = c / cpt, cc = c % cpt;
-        const bool sl = cc < cs;
-        const int o = (sl ? cc : cc - cs) * 64, len = min(64, (sl ? ns : nq) - o);
-        const u4 *src = img + (size_t)tk * IWf + (sl ? g0 * 16 * R : ugf * 16 * R + g0 * 16 * F::Q / 4) + o;
-        u4 *dst = vlds + tk * IW + (sl ? 0 : ugc * 16 * R) + o;
-        if (lane < len) __builtin_amdgcn_global_load_lds(src + lane, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+      // straight into LDS (global_load_lds_dwordx4), one token image per wave, all its runs of 64
+      // words in flight at once: a loop of load-then-store copies waits out one memory latency per
+      // word a thread copies. The loop is kept to a few scalar instructions per load: a wave issues
+      // about one instruction per 1.7 ns, so per-chunk index arithmetic (a division by the chunk
+      // count, 64-bit offsets) cost more than the loads' latency.
+      for (int tk = wave; tk < M; tk += nw) {
+        const u4 *src = img + (size_t)tk * IWf + g0 * 16 * R + lane;
+        u4 *dst = vlds + tk * IW;
+        for (int o = 0; o < ns; o += 64, src += 64, dst += 64)
+          if (o + lane < ns) __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+        src = img + (size_t)tk * IWf + ugf * 16 * R + g0 * 16 * F::Q / 4 + lane;
+        dst = vlds + tk * IW + ugc * 16 * R;
+        for (int o = 0; o < nq; o += 64, src += 64, dst += 64)
+          if (o + lane < nq) __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
       }
       __syncthreads();  // (waits for the wave's loads, then the barrier)
     } else {

@@ -63,7 +63,10 @@ struct FAffine {
   static constexpr int R = 8, Q = 2, RING = 3, GRID_ENTRIES = 0;
   // 512 threads: eight waves share one staged (and rotated) x, so at most two 512-element
   // rotation passes per wave at K = 5120.
-  static constexpr int WG = 512;
+#ifndef ISHZ_AFF_WG
+#define ISHZ_AFF_WG 512
+#endif
+  static constexpr int WG = ISHZ_AFF_WG;
   static __host__ __device__ int units(int K) { return K / 64; }
   // 16-byte words of the staged x: slots, then the two sums per unit.
   static __host__ __device__ int img_words(int K) { return (units(K) + 15) / 16 * (16 * R + 4 * Q); }
@@ -161,15 +164,17 @@ struct FAffine {
   }
 
   // Butterfly across lanes: partner = lane ^ m (m = 1, 2, 4, 8 within a 16-lane row, from DPP
-  // quad permutes and row mirrors); the lower lane keeps a + b, the upper b's partner - b.
+  // quad permutes and row mirrors); the lower lane keeps a + b, the upper b's partner - b, both as
+  // fma(v, +-1, partner) (exact products, so one rounding, as the add or subtract): one DPP move
+  // and one FMA per value instead of an add, a subtract and a select. sgn = -1 on the upper lanes.
   template <int M>
-  static DEV float xbfly(float v, int lane) {
+  static DEV float xbfly(float v, float sgn) {
     float t;
     if constexpr (M == 1) t = ISHZ_DPP(v, 0xB1);
     else if constexpr (M == 2) t = ISHZ_DPP(v, 0x4E);
     else if constexpr (M == 4) t = ISHZ_DPP(ISHZ_DPP(v, 0x141), 0x1B);  // half mirror, quad reverse
     else t = ISHZ_DPP(ISHZ_DPP(v, 0x141), 0x140);                      // half mirror, mirror
-    return (lane & M) ? t - v : v + t;
+    return __builtin_fmaf(v, sgn, t);
   }
 
   // hadamardRotate on a lane's eight consecutive values: sign flip, butterflies (h = 1, 2, 4
@@ -178,21 +183,23 @@ struct FAffine {
     if (sg)
 #pragma unroll
       for (int e = 0; e < 8; e++) v[e] *= sg[e >> 2][e & 3];
+    const float sg1 = lane & 1 ? -1.0f : 1.0f, sg2 = lane & 2 ? -1.0f : 1.0f;
+    const float sg4 = lane & 4 ? -1.0f : 1.0f, sg8 = lane & 8 ? -1.0f : 1.0f;
     if (bl > 1) lbfly<1>(v);
     if (bl > 2) lbfly<2>(v);
     if (bl > 4) lbfly<4>(v);
     if (bl > 8)
 #pragma unroll
-      for (int e = 0; e < 8; e++) v[e] = xbfly<1>(v[e], lane);
+      for (int e = 0; e < 8; e++) v[e] = xbfly<1>(v[e], sg1);
     if (bl > 16)
 #pragma unroll
-      for (int e = 0; e < 8; e++) v[e] = xbfly<2>(v[e], lane);
+      for (int e = 0; e < 8; e++) v[e] = xbfly<2>(v[e], sg2);
     if (bl > 32)
 #pragma unroll
-      for (int e = 0; e < 8; e++) v[e] = xbfly<4>(v[e], lane);
+      for (int e = 0; e < 8; e++) v[e] = xbfly<4>(v[e], sg4);
     if (bl > 64)
 #pragma unroll
-      for (int e = 0; e < 8; e++) v[e] = xbfly<8>(v[e], lane);
+      for (int e = 0; e < 8; e++) v[e] = xbfly<8>(v[e], sg8);
 #pragma unroll
     for (int e = 0; e < 8; e++) v[e] = (float)(_Float16)(v[e] * scale);
   }
@@ -269,6 +276,13 @@ struct FAffine {
     stage_group(a, xs, xsum, wave, nw, pre);  // first group: loads issued by stage_load
     for (int c0 = wave + PF * nw; c0 < npass; c0 += PF * nw)
       stage_group(a, xs, xsum, c0, nw, load_group(a, x, c0, nw));
+#ifdef ISHZ_TIMING_ISSUE
+    {
+      uint64_t t;
+      asm volatile("s_memrealtime %0\n s_waitcnt lgkmcnt(0)" : "=s"(t)::"memory");
+      if (lane == 0) ishz_timing2[blockIdx.x * nw + wave] = t;
+    }
+#endif
     __syncthreads();
   }
 

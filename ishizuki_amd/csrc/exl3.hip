@@ -20,6 +20,7 @@
 
 #include "common.h"
 
+
 namespace ishz {
 
 // exl3_decode (EXL3.swift:136-147): 3INST / MCG / MUL1 codebooks, fp16 single rounding.
@@ -225,9 +226,10 @@ DEV uint32_t exl3_decode2(uint32_t sa, uint32_t sb) {
 }
 
 // 3INST / MCG image of one state as the two fp16 halves whose sum is the weight (exl3_decode
-// before its final add). A GEMV lane dots them against (x, x): the halves meet x in fp32, so the
-// weight's fp16 rounding of their sum is skipped (a difference of at most half an fp16 ulp per
-// weight, inside the matmul tolerance; dequantization keeps the exact decode).
+// before its final add). The M = 1 matvec multiplies them by (x, x) as two MFMA k-entries: the
+// halves meet x in fp32, so the weight's fp16 rounding of their sum is skipped (a difference of
+// at most half an fp16 ulp per weight, inside the matmul tolerance; dequantization keeps the
+// exact decode).
 template <int CB>
 DEV uint32_t exl3_halves(uint32_t s) {
   static_assert(CB != 2, "MUL1 decodes to one fp16 directly");
@@ -398,10 +400,16 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
       r.xb = *(const uint32_t *)(xr + 16 * tk + 8);
     }
   };
-  using Acc = typename std::conditional<MF, f4, float>::type;
-  Acc acc[TN];
+  // HM (M = 1, 3INST / MCG): the dots on MFMA 16x16x32. In MFMA i of tile quad q, lane group g
+  // decodes tile 4q + (g + i) % 4 and A holds x (each value twice, against the two halves of a
+  // weight) only in row (g + i) % 4, so C row e collects tile 4q + e alone: lanes 0..15 end with
+  // the quad's four tiles' column sums in their four C registers.
+  constexpr bool HM = !MF && CB != 2;
+  using Acc = typename std::conditional<MF || HM, f4, float>::type;
+  constexpr int NACC = HM ? TN / 4 : TN;
+  Acc acc[NACC];
 #pragma unroll
-  for (int t = 0; t < TN; t++) acc[t] = Acc{};
+  for (int t = 0; t < NACC; t++) acc[t] = Acc{};
   Raw ring[D];
   if (nsteps > 0) {
 #pragma unroll
@@ -440,35 +448,39 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
         r.xb = *(const uint32_t *)(xl + xo + 8);
       }
       *(u4 *)(stage + 4 * lane) = r.w;  // the wave's own buffer: its LDS operations stay in order
-      constexpr bool HALVES = !MF && CB != 2;
-      uint32_t xd[4];  // (x, x) pairs for the halves form
-      if constexpr (HALVES) {
-        xd[0] = dup_lo(r.xa);
-        xd[1] = dup_hi(r.xa);
-        xd[2] = dup_lo(r.xb);
-        xd[3] = dup_hi(r.xb);
-      }
+      if constexpr (HM) {
+        // A of MFMA i: x of this lane group's rows, each value twice, on the lanes of row (g + i) % 4
+        const u4 X = {dup_lo(r.xa), dup_hi(r.xa), dup_lo(r.xb), dup_hi(r.xb)};
+        u4 A[4];
 #pragma unroll
-      for (int t = 0; t < TN; t++) {
-        const uint32_t w0 = stage[t * W + wn.ja], w1 = stage[t * W + wn.jb];
-        const uint32_t win = __builtin_amdgcn_alignbit(w0, w1, wn.amt);
-        const uint32_t s0 = __builtin_amdgcn_ubfe(win, T32::field(0), 16);
-        const uint32_t s1 = __builtin_amdgcn_ubfe(win, T32::field(1), 16);
-        const uint32_t s2 = __builtin_amdgcn_ubfe(win, T32::field(2), 16);
-        const uint32_t s3 = __builtin_amdgcn_ubfe(win, T32::field(3), 16);
-        if constexpr (HALVES) {
-          float a = dot2(exl3_halves<CB>(s0), xd[0], acc[t]);
-          a = dot2(exl3_halves<CB>(s1), xd[1], a);
-          a = dot2(exl3_halves<CB>(s2), xd[2], a);
-          acc[t] = dot2(exl3_halves<CB>(s3), xd[3], a);
-          continue;
-        }
-        const uint32_t b01 = exl3_decode2<CB>(s0, s1), b23 = exl3_decode2<CB>(s2, s3);
-        if constexpr (MF) {
-          const u2 A = live ? u2{r.xa, r.xb} : u2{0, 0};
-          acc[t] = mfma16(as_h4(A), as_h4(u2{b01, b23}), acc[t]);
-        } else {
-          acc[t] = dot2(b23, r.xb, dot2(b01, r.xa, acc[t]));
+        for (int i = 0; i < 4; i++) A[i] = j < 4 && ((j - g) & 3) == i ? X : u4{0, 0, 0, 0};
+#pragma unroll
+        for (int q = 0; q < TN / 4; q++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const int t = 4 * q + ((g + i) & 3);
+            const uint32_t win = __builtin_amdgcn_alignbit(stage[t * W + wn.ja], stage[t * W + wn.jb], wn.amt);
+            const u4 B = {exl3_halves<CB>(__builtin_amdgcn_ubfe(win, T32::field(0), 16)),
+                          exl3_halves<CB>(__builtin_amdgcn_ubfe(win, T32::field(1), 16)),
+                          exl3_halves<CB>(__builtin_amdgcn_ubfe(win, T32::field(2), 16)),
+                          exl3_halves<CB>(__builtin_amdgcn_ubfe(win, T32::field(3), 16))};
+            acc[q] = mfma32(as_h8(A[i]), as_h8(B), acc[q]);
+          }
+      } else {
+#pragma unroll
+        for (int t = 0; t < TN; t++) {
+          const uint32_t win = __builtin_amdgcn_alignbit(stage[t * W + wn.ja], stage[t * W + wn.jb], wn.amt);
+          const uint32_t s0 = __builtin_amdgcn_ubfe(win, T32::field(0), 16);
+          const uint32_t s1 = __builtin_amdgcn_ubfe(win, T32::field(1), 16);
+          const uint32_t s2 = __builtin_amdgcn_ubfe(win, T32::field(2), 16);
+          const uint32_t s3 = __builtin_amdgcn_ubfe(win, T32::field(3), 16);
+          const uint32_t b01 = exl3_decode2<CB>(s0, s1), b23 = exl3_decode2<CB>(s2, s3);
+          if constexpr (MF) {
+            const u2 A = live ? u2{r.xa, r.xb} : u2{0, 0};
+            acc[t] = mfma16(as_h4(A), as_h4(u2{b01, b23}), acc[t]);
+          } else {
+            acc[t] = dot2(b23, r.xb, dot2(b01, r.xa, acc[t]));
+          }
         }
       }
     }
@@ -497,12 +509,20 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
       }
     }
   } else {
+    if constexpr (HM) {
+      if (g == 0)
 #pragma unroll
-    for (int t = 0; t < TN; t++) {
-      float a = acc[t];
-      a += __shfl_xor(a, 16, 64);
-      a += __shfl_xor(a, 32, 64);
-      if (g == 0) red[(wave * TN + t) * 16 + j] = a;
+        for (int q = 0; q < TN / 4; q++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) red[(wave * TN + 4 * q + e) * 16 + j] = acc[q][e];
+    } else {
+#pragma unroll
+      for (int t = 0; t < NACC; t++) {
+        float a = acc[t];
+        a += __shfl_xor(a, 16, 64);
+        a += __shfl_xor(a, 32, 64);
+        if (g == 0) red[(wave * TN + t) * 16 + j] = a;
+      }
     }
     __syncthreads();
     for (int o = threadIdx.x; o < TN * 16; o += blockDim.x) {
