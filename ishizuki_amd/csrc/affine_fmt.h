@@ -63,10 +63,7 @@ struct FAffine {
   static constexpr int R = 8, Q = 2, RING = 3, GRID_ENTRIES = 0;
   // 512 threads: eight waves share one staged (and rotated) x, so at most two 512-element
   // rotation passes per wave at K = 5120.
-#ifndef ISHZ_AFF_WG
-#define ISHZ_AFF_WG 512
-#endif
-  static constexpr int WG = ISHZ_AFF_WG;
+  static constexpr int WG = 512;
   static __host__ __device__ int units(int K) { return K / 64; }
   // 16-byte words of the staged x: slots, then the two sums per unit.
   static __host__ __device__ int img_words(int K) { return (units(K) + 15) / 16 * (16 * R + 4 * Q); }
