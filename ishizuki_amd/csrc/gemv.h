@@ -105,18 +105,18 @@ __host__ __device__ int gemv_align(const typename F::Args &a, int rpw) {
 
 // Threads per workgroup: F::WG where the format sets it (the workgroup shares one staged copy of
 // x, so a larger one stages fewer copies, each with more waves), else 256; rows of more than 384
-// units (64 lanes per row, K above 24576 for 64-weight units) take 1024, one workgroup per CU: x
-// is then 50 KB and more, and staging it once per CU instead of two to four times measured 10-14 %
-// faster at K = 25600 (Q4_K, Q6_K, IQ2_XS, N = 5120) on MI355X.
-template <class F, int LPR = 16>
+// units (BIG: K above 24576 for 64-weight units) take 1024, one workgroup per CU: x is then 50 KB
+// and more, and staging it once per CU instead of two to four times measured 10-14 % faster at
+// K = 25600 (Q4_K, Q6_K, IQ2_XS, N = 5120) on MI355X. 64 lanes per row also takes 1024.
+template <class F, int LPR = 16, bool BIG = false>
 __host__ __device__ constexpr int gemv_threads() {
-  if constexpr (LPR >= 64) return 1024;
+  if constexpr (LPR >= 64 || BIG) return 1024;
   else if constexpr (requires { F::WG; }) return F::WG;
   else return 256;
 }
 
-template <class F, int LPR, int D, bool RAGGED>
-__global__ __launch_bounds__((gemv_threads<F, LPR>())) void gemv_kernel(typename F::Args args, const uint16_t *__restrict__ x,
+template <class F, int LPR, int D, bool RAGGED, bool BIG = false>
+__global__ __launch_bounds__((gemv_threads<F, LPR, BIG>())) void gemv_kernel(typename F::Args args, const uint16_t *__restrict__ x,
                                                    Out out, int nwg, int part_off) {
   static_assert(LPR % 16 == 0, "lanes per row must be a multiple of 16");
   extern __shared__ __align__(16) uint32_t smem[];
@@ -129,7 +129,7 @@ __global__ __launch_bounds__((gemv_threads<F, LPR>())) void gemv_kernel(typename
   u4 *extra = (u4 *)(xsum + nx * ugroups * 16 * F::Q);  // format tables / scratch
   float *part = (float *)((char *)smem + part_off);      // [wave][row of the workgroup] partial dots
 
-  constexpr int RPW = 64 / LPR, WPG = gemv_threads<F, LPR>() / 64;
+  constexpr int RPW = 64 / LPR, WPG = gemv_threads<F, LPR, BIG>() / 64;
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int sub = lane % LPR, rg = lane / LPR;
   const int upl = (units + LPR - 1) / LPR;  // units per lane per row
@@ -289,16 +289,16 @@ int gemv_num_cu();
 // Grid: one resident round of workgroups (at most what the compiled kernel's registers and this
 // launch's LDS allow), each an equal share of row groups. LDS: the staged x images and sums, the
 // format's tables, then the waves' partial dots for the workgroup's rows.
-template <class F, int LPR, bool RAGGED>
+template <class F, int LPR, bool RAGGED, bool BIG = false>
 static int launch_gemv_k(const typename F::Args &a, const void *x, const Out &o, hipStream_t st) {
   constexpr int RPW = 64 / LPR;
-  constexpr int NT = gemv_threads<F, LPR>(), WPG = NT / 64;
+  constexpr int NT = gemv_threads<F, LPR, BIG>(), WPG = NT / 64;
   const int units = F::units(a.K);
   const size_t ug = (size_t)(units + 15) / 16;
   const size_t xlds = gemv_nx<F>(a) * (ug * 16 * F::R * 16 + ug * 16 * F::Q * 4) + F::extra_lds_bytes(a);
   const size_t part_off = (xlds + 15) / 16 * 16;
   if (part_off > 160 * 1024) return decline("K too large for the GEMV's LDS copy of x");
-  auto kern = gemv_kernel<F, LPR, F::RING, RAGGED>;
+  auto kern = gemv_kernel<F, LPR, F::RING, RAGGED, BIG>;
   const int GA = gemv_align<F>(a, RPW), groups = (a.N + RPW - 1) / RPW, units_g = (groups + GA - 1) / GA;
   const int wg_cap = std::max(F::occ(a) * 4 / WPG, 1);  // workgroups per CU the grid is sized for
   int nwg = 0;
@@ -325,8 +325,10 @@ static int launch_gemv_k(const typename F::Args &a, const void *x, const Out &o,
   return ISHZ_OK;
 }
 
-// Lanes per row: 16 for rows of up to 160 units, 32 up to 384, else 64. RAGGED: the row's units
-// are not a whole number of every lane's slots. x is fp16 (or an activation image, with its row
+// Lanes per row: 16 for rows of up to 160 units, 32 up to 384; longer rows take 16 again, in
+// 1024-thread workgroups (at K = 25600, N = 5120 on MI355X: Q4_K 20.7 -> 19.8 us, Q6_K 28.0 ->
+// 27.5, IQ2_XS 20.4 -> 18.8 against 64 lanes per row, whose last slot was 12 % padding). RAGGED:
+// the row's units are not a whole number of every lane's slots. x is fp16 (or an activation image, with its row
 // factor in rs); y in dtype odt.
 template <class F>
 static int launch_gemv(const typename F::Args &a, const void *x, void *y, hipStream_t st, int odt = ISHZ_DT_F16,
@@ -335,7 +337,7 @@ static int launch_gemv(const typename F::Args &a, const void *x, void *y, hipStr
   const Out o{y, odt, rs};
   if (units <= 160) return units % 16 ? launch_gemv_k<F, 16, true>(a, x, o, st) : launch_gemv_k<F, 16, false>(a, x, o, st);
   if (units <= 384) return units % 32 ? launch_gemv_k<F, 32, true>(a, x, o, st) : launch_gemv_k<F, 32, false>(a, x, o, st);
-  return units % 64 ? launch_gemv_k<F, 64, true>(a, x, o, st) : launch_gemv_k<F, 64, false>(a, x, o, st);
+  return units % 16 ? launch_gemv_k<F, 16, true, true>(a, x, o, st) : launch_gemv_k<F, 16, false, true>(a, x, o, st);
 }
 
 }  // namespace ishz
