@@ -131,29 +131,51 @@ __global__ __launch_bounds__(64 * NW) void vgemm_kernel(P p, int K, int Kc, int 
       const int items = ntl * steps;
       const int cnt = whole ? (ntl > wave ? (ntl - wave + NW - 1) / NW : 0) * steps
                             : (items > wave ? (items - wave + NW - 1) / NW : 0);
-      auto where = [&](int k, int &tl, int &j) {
-        if (whole) {
-          tl = wave + NW * (k / steps);
-          j = k % steps;
-        } else {
-          const int it = wave + NW * k;
-          tl = it / steps;
-          j = it % steps;
-        }
-      };
-      auto load = [&](int k, Raw &r) {
+      // Item cursors (tile tl, step j): item k is tile wave + NW (k / steps), step k % steps
+      // (whole tiles), or item wave + NW k of the workgroup's (tile, step) sequence (dealt steps).
+      // They advance without dividing: a division by the runtime step count for every load,
+      // consume and park test was most of the loop's scalar instructions.
+      struct Cur {
         int tl, j;
-        where(min(k, cnt - 1), tl, j);
-        const int row = min((tb + tl) * 16 + n, N - 1);
-        if constexpr (requires { F::vload_p(p, gp, row, kc0, j, G); })
-          r = F::vload_p(p, gp, row, kc0, j, G);  // formats whose rows are not one byte run
+      };
+      auto next = [&](Cur c) {
+        if (whole) {
+          if (++c.j == steps) {
+            c.j = 0;
+            c.tl += NW;
+          }
+        } else {
+          c.j += NW;
+          while (c.j >= steps) {
+            c.j -= steps;
+            c.tl++;
+          }
+        }
+        return c;
+      };
+      const Cur c0 = whole ? Cur{wave, 0} : Cur{wave / steps, wave % steps};
+      auto load = [&](const Cur &c, Raw &r) {
+        const int row = min((tb + c.tl) * 16 + n, N - 1);
+        if constexpr (requires { F::vload_p(p, gp, row, kc0, c.j, G); })
+          r = F::vload_p(p, gp, row, kc0, c.j, G);  // formats whose rows are not one byte run
         else
-          r = F::vload(p.wrow(gp, row) + (size_t)(kc0 / 256) * F::VSTEP_BYTES, j, G);
+          r = F::vload(p.wrow(gp, row) + (size_t)(kc0 / 256) * F::VSTEP_BYTES, c.j, G);
+      };
+      // the load cursor runs D - 1 items ahead and stops at the wave's last item (loads past the
+      // end re-read it and are dropped)
+      Cur lc = c0, cc = c0;
+      int lk = 0;
+      auto load_next = [&](Raw &r) {
+        load(lc, r);
+        if (lk < cnt - 1) {
+          lc = next(lc);
+          lk++;
+        }
       };
       Raw ring[D];
       if (cnt > 0) {
 #pragma unroll
-        for (int d = 0; d < D - 1; d++) load(d, ring[d]);
+        for (int d = 0; d < D - 1; d++) load_next(ring[d]);
       }
       f4 acc[NQ];
 #pragma unroll
@@ -163,9 +185,8 @@ __global__ __launch_bounds__(64 * NW) void vgemm_kernel(P p, int K, int Kc, int 
         for (int d = 0; d < D; d++) {
           const int k = k0 + d;
           if (k >= cnt) break;
-          load(k + D - 1, ring[(d + D - 1) % D]);
-          int tl, j;
-          where(k, tl, j);
+          load_next(ring[(d + D - 1) % D]);
+          const int tl = cc.tl, j = cc.j;
           const Raw &r = ring[d];
           u4 B[8];
           F::vdecode(r, B, mg, tabs, tabs + 512);
@@ -202,9 +223,8 @@ __global__ __launch_bounds__(64 * NW) void vgemm_kernel(P p, int K, int Kc, int 
             }
           }
           // park at the wave's last item of a tile: sum the row's four lane-group quarters
-          int tl2 = -1, j2;
-          if (k + 1 < cnt) where(k + 1, tl2, j2);
-          if (tl2 != tl) {
+          cc = next(cc);
+          if (k + 1 == cnt || cc.tl != tl) {
 #pragma unroll
             for (int q = 0; q < NQ; q++) {
               if (4 * q >= M) break;
