@@ -80,14 +80,11 @@ DEV uint32_t unmagic(uint32_t halves, _Float16 off) {
   return as_u32(as_h2(halves | 0x64006400u) - h2{off, off});
 }
 
-// (a & mask) | orv in one v_and_or_b32. gfx9 VOP3 encodings take no literal and read one SGPR,
-// so with two constants the compiler splits this into v_and + v_or; keeping orv in a VGPR
-// (see vconst) and the mask in an SGPR makes it one instruction.
-DEV uint32_t and_or(uint32_t a, uint32_t mask, uint32_t orv) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(orv));
-  return r;
-}
+// (a & mask) | orv: one v_and_or_b32 (gfx9 VOP3 encodings take no literal and read one SGPR, so
+// orv is kept in a VGPR, see vconst, and the mask goes to an SGPR). Written in C, not inline
+// assembly: the hazard recognizer cannot see into an asm statement and padded every one that fed
+// a VALU with an s_nop (79 per five units in the headline GEMV's loop, 23 without; 10.9 -> 10.6 us).
+DEV uint32_t and_or(uint32_t a, uint32_t mask, uint32_t orv) { return (a & mask) | orv; }
 // A constant materialised once into a VGPR the compiler cannot rematerialise per use.
 DEV uint32_t vconst(uint32_t c) {
   uint32_t r;
