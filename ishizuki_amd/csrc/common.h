@@ -39,13 +39,13 @@ DEV uint32_t ld4(const uint8_t *p) {
   return v;
 }
 DEV uint32_t ld2(const uint8_t *p) { return *(const uint16_t *)__builtin_assume_aligned(p, 2); }
-// Low 32 bits of a 24-bit by 24-bit product: one full-rate v_mul_u32_u24 (v_mul_lo_u32 is quarter
-// rate). Written as the instruction itself: given the plain product, the compiler picks
-// v_mul_lo_u32 once it can no longer prove both operands fit 24 bits. b is a constant (an SGPR).
+// Low 32 bits of a 24-bit by 24-bit product (both operands below 2^24). Plain C: the compiler
+// emits v_mul_lo_u32, which on gfx950 issues at the rate of v_mul_u32_u24 (a dependent-chain
+// microbenchmark gives both the same time); the inline-assembly v_mul_u32_u24 this replaced
+// measured the same or slower (IQ2_XS GEMV, 25600x5120: 20.3-20.5 us against 19.2-19.3).
 DEV uint32_t mul24(uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_mul_u32_u24 %0, %1, %2" : "=v"(r) : "s"(b), "v"(a));
-  return r;
+  __builtin_assume(a < (1u << 24) && b < (1u << 24));
+  return a * b;
 }
 
 // 16 bytes at a 2-byte-aligned address. A global load that is not dword aligned costs about a
