@@ -343,13 +343,26 @@ DEV void wht128_pair(float &v0, float &v1, int lane) {
   float a = v0 + v1, b = v0 - v1;
   v0 = a;
   v1 = b;
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    const float p0 = __shfl_xor(v0, m, 64), p1 = __shfl_xor(v1, m, 64);
-    const bool hi = (lane & m) != 0;
-    v0 = hi ? p0 - v0 : v0 + p0;
-    v1 = hi ? p1 - v1 : v1 + p1;
-  }
+  // partner lane ^ m: m = 1, 2, 4, 8 by DPP inside 16-lane rows, 16 and 32 by the row swaps
+  // (v_permlane16_swap / v_permlane32_swap) instead of LDS-pipe shuffles; the lower lane keeps
+  // v + p, the upper p - v, as fma(v, +-1, p) (exact, the same rounding)
+  auto stage = [&](float p0, float p1, int m) {
+    const float s = (lane & m) ? -1.0f : 1.0f;
+    v0 = __builtin_fmaf(v0, s, p0);
+    v1 = __builtin_fmaf(v1, s, p1);
+  };
+  stage(ISHZ_DPP(v0, 0xB1), ISHZ_DPP(v1, 0xB1), 1);                                    // quad_perm [1,0,3,2]
+  stage(ISHZ_DPP(v0, 0x4E), ISHZ_DPP(v1, 0x4E), 2);                                    // quad_perm [2,3,0,1]
+  stage(ISHZ_DPP(ISHZ_DPP(v0, 0x141), 0x1B), ISHZ_DPP(ISHZ_DPP(v1, 0x141), 0x1B), 4);    // half mirror, quad reverse
+  stage(ISHZ_DPP(ISHZ_DPP(v0, 0x141), 0x140), ISHZ_DPP(ISHZ_DPP(v1, 0x141), 0x140), 8);  // half mirror, mirror
+  auto swap = [&](float v, int m) {  // the value of lane ^ m, m = 16 or 32
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto r = m == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                           : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __builtin_bit_cast(float, (lane & m) ? r[0] : r[1]);
+  };
+  stage(swap(v0, 16), swap(v1, 16), 16);
+  stage(swap(v0, 32), swap(v1, 32), 32);
   const float r = 0.08838834764831845f;  // 1 / sqrt(128)
   v0 *= r;
   v1 *= r;
@@ -573,18 +586,19 @@ __global__ __launch_bounds__(256) void exl3_rotate_kernel(const void *__restrict
   const int lane = threadIdx.x & 63;
   const size_t base = blk * 128 + 2 * lane;
   const int col = (int)((blk * 128) % width) + 2 * lane;
+  const float s0 = h2f(scales[col]), s1 = h2f(scales[col + 1]);  // issued first: independent
   float v0, v1;
   if (in_dt == ISHZ_DT_F32) {  // fp32 input: the sum of nsum slices (K-split partials), in order
     const size_t slice = blocks * 128;
     const float *xf = (const float *)x + base;
     v0 = 0.0f;
     v1 = 0.0f;
-    for (int s0 = 0; s0 < nsum; s0 += 8) {  // eight slices' loads in flight, summed in order
-      float2 p[8];
+    for (int q0 = 0; q0 < nsum; q0 += 16) {  // sixteen slices' loads in flight, summed in order
+      float2 p[16];
 #pragma unroll
-      for (int i = 0; i < 8; i++) p[i] = s0 + i < nsum ? *(const float2 *)(xf + (s0 + i) * slice) : float2{0.0f, 0.0f};
+      for (int i = 0; i < 16; i++) p[i] = q0 + i < nsum ? *(const float2 *)(xf + (q0 + i) * slice) : float2{0.0f, 0.0f};
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
+      for (int i = 0; i < 16; i++) {
         v0 += p[i].x;
         v1 += p[i].y;
       }
@@ -594,13 +608,13 @@ __global__ __launch_bounds__(256) void exl3_rotate_kernel(const void *__restrict
     v1 = load_act(x, base + 1, in_dt);
   }
   if (before) {
-    v0 *= h2f(scales[col]);
-    v1 *= h2f(scales[col + 1]);
+    v0 *= s0;
+    v1 *= s1;
   }
   wht128_pair(v0, v1, lane);
   if (!before) {
-    v0 *= h2f(scales[col]);
-    v1 *= h2f(scales[col + 1]);
+    v0 *= s0;
+    v1 *= s1;
   }
   if (rs) {  // outputs of a rescaled activation image: its row's factor back
     const float f = rs[(blk * 128) / width];
