@@ -105,6 +105,19 @@ DEV float dot2(uint32_t a, uint32_t b, float c) {
 #define ISHZ_DPP(v, ctrl)                                                                  \
   __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, \
                                                         0xf, 0xf, true))
+// The value of lane ^ 16 / lane ^ 32: the row swaps v_permlane16_swap / v_permlane32_swap of a
+// register with itself (one VALU op, no LDS-pipe shuffle); the wave must be whole.
+DEV float lane_xor16(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 16) ? r[0] : r[1]);
+}
+DEV float lane_xor32(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+}
+
 // Sum over aligned groups of W lanes (W = 8, 16, 32, 64); every lane of a group gets the sum.
 template <int W>
 DEV float group_sum(float v) {
@@ -112,8 +125,8 @@ DEV float group_sum(float v) {
   v += ISHZ_DPP(v, 0x4E);   // quad_perm [2,3,0,1]
   v += ISHZ_DPP(v, 0x141);  // row_half_mirror: lane j <- 7-j within 8
   if (W >= 16) v += ISHZ_DPP(v, 0x140);  // row_mirror: lane j <- 15-j within 16
-  if (W >= 32) v += __shfl_xor(v, 16, 64);
-  if (W >= 64) v += __shfl_xor(v, 32, 64);
+  if (W >= 32) v += lane_xor16(v);
+  if (W >= 64) v += lane_xor32(v);
   return v;
 }
 

@@ -117,8 +117,8 @@ __global__ __launch_bounds__(1024) void exl3_mm(const uint16_t *__restrict__ xh,
       acc = dot2(B.x, *(const uint32_t *)(xr + 16 * tk), acc);
       acc = dot2(B.y, *(const uint32_t *)(xr + 16 * tk + 8), acc);
     }
-    acc += __shfl_xor(acc, 16, 64);
-    acc += __shfl_xor(acc, 32, 64);
+    acc += lane_xor16(acc);
+    acc += lane_xor32(acc);
     if (g == 0) red[wave * 16 + j] = acc;
     __syncthreads();
     if (threadIdx.x < 16) {
@@ -168,8 +168,8 @@ __global__ __launch_bounds__(256) void exl3_mm_f32(const float *__restrict__ x, 
   for (int m = 0; m < 16; m++) {
     if (m >= M) continue;
     float v = acc[m];
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
+    v += lane_xor16(v);
+    v += lane_xor32(v);
     if (g == 0) red[wave][m][j] = v;
   }
   __syncthreads();
@@ -322,8 +322,8 @@ __global__ __launch_bounds__(1024) void exl3_mm2(const uint16_t *__restrict__ xh
 #pragma unroll
     for (int t = 0; t < TN; t++) {
       float a = acc[t];
-      a += __shfl_xor(a, 16, 64);
-      a += __shfl_xor(a, 32, 64);
+      a += lane_xor16(a);
+      a += lane_xor32(a);
       if (g == 0) red2[(wave * TN + t) * 16 + j] = a;
     }
     __syncthreads();
@@ -532,8 +532,8 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
 #pragma unroll
       for (int t = 0; t < NACC; t++) {
         float a = acc[t];
-        a += __shfl_xor(a, 16, 64);
-        a += __shfl_xor(a, 32, 64);
+        a += lane_xor16(a);
+        a += lane_xor32(a);
         if (g == 0) red[(wave * TN + t) * 16 + j] = a;
       }
     }

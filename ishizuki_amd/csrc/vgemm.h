@@ -231,8 +231,8 @@ __global__ __launch_bounds__(64 * NW) void vgemm_kernel(P p, int K, int Kc, int 
 #pragma unroll
               for (int e = 0; e < 4; e++) {
                 float a = acc[q][e];
-                a += __shfl_xor(a, 16, 64);
-                a += __shfl_xor(a, 32, 64);
+                a += lane_xor16(a);
+                a += lane_xor32(a);
                 if (G == 0) {
                   if (whole) outb[tl * 256 + (4 * q + e) * 16 + n] += a;
                   else accb[(((wave * tiles_per_wg + tl) * NQ + q) * 4 + e) * 16 + n] += a;
