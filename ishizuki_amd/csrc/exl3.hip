@@ -378,7 +378,7 @@ DEV void wht128_pair(float &v0, float &v1, int lane) {
 // ROT: xh is the unrotated x and suh its input scales; each workgroup rotates the 128-point blocks
 // that cover its K tiles, for every row, into LDS (after its first weight loads are issued) and
 // reads x there, in place of a separate rotation launch.
-template <int KA, int CB, bool MF, int D, bool ROT = false>
+template <int KA, int CB, bool MF, int D, bool ROT = false, int NTG = 1>
 __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh, int M, int K,
                                                const uint32_t *__restrict__ trellis, int N,
                                                float *__restrict__ yh, int tk_per_wg,
@@ -392,9 +392,18 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
   const int tn0 = blockIdx.x * TN, tiles_n = N / 16, tiles_k = K / 16;
   const int tk0 = blockIdx.y * tk_per_wg, tk1 = min(tk0 + tk_per_wg, tiles_k);
   const typename T32::Win wn = T32::window(8 * (4 * (j & 7) + g) + 4 * (j >> 3));
-  const int tok = MF ? (j < M ? j : 0) : 0;
+  // HM (3INST / MCG, M <= 8): the dots on MFMA 16x16x32 with the weights' fp16 halves as k
+  // entries. In MFMA i of tile quad q, lane group g decodes tile 4q + (g + i) % 4; A row 4 m + e
+  // holds token m's x (each value twice, against a weight's two halves) when e = (g + i) % 4 and
+  // is zero otherwise, so C row 4 m + e collects token m's dot with tile 4q + e alone: lane group
+  // m ends with token m's sums for the quad's four tiles in its four C registers. Four tokens per
+  // MFMA set, NTG sets for up to 4 NTG tokens, every set on the same decoded weights.
+  constexpr bool HM = !MF && CB != 2;
+  constexpr int NX = HM ? NTG : 1;  // x words per lane and step: one per token group
+  int tok[NX];
+#pragma unroll
+  for (int t = 0; t < NX; t++) tok[t] = HM ? min((j >> 2) + 4 * t, M - 1) : MF ? (j < M ? j : 0) : 0;
   const bool live = MF ? j < M : true;
-  const uint16_t *xr = xh + (size_t)tok * K + 2 * g;
   const size_t tstride = (size_t)tiles_n * W;  // words between K tiles
   const uint32_t *base = trellis + (size_t)tn0 * W + 4 * lane;
   uint32_t *stage = (uint32_t *)sm3 + wave * 256;  // this wave's step
@@ -402,24 +411,22 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
 
   struct Raw {
     u4 w;
-    uint32_t xa, xb;
+    uint32_t xa[NX], xb[NX];
   };
   const int nsteps = tk1 - tk0 > wave ? (tk1 - tk0 - wave + KS - 1) / KS : 0;
   auto load = [&](int i, Raw &r) {
     const int tk = tk0 + wave + KS * min(i, nsteps - 1);
     r.w = *(const u4 *)(base + tk * tstride);
-    if constexpr (!ROT) {
-      r.xa = *(const uint32_t *)(xr + 16 * tk);
-      r.xb = *(const uint32_t *)(xr + 16 * tk + 8);
-    }
+    if constexpr (!ROT)
+#pragma unroll
+      for (int t = 0; t < NX; t++) {
+        const uint16_t *xr = xh + (size_t)tok[t] * K + 2 * g + 16 * tk;
+        r.xa[t] = *(const uint32_t *)xr;
+        r.xb[t] = *(const uint32_t *)(xr + 8);
+      }
   };
-  // HM (M = 1, 3INST / MCG): the dots on MFMA 16x16x32. In MFMA i of tile quad q, lane group g
-  // decodes tile 4q + (g + i) % 4 and A holds x (each value twice, against the two halves of a
-  // weight) only in row (g + i) % 4, so C row e collects tile 4q + e alone: lanes 0..15 end with
-  // the quad's four tiles' column sums in their four C registers.
-  constexpr bool HM = !MF && CB != 2;
   using Acc = typename std::conditional<MF || HM, f4, float>::type;
-  constexpr int NACC = HM ? TN / 4 : TN;
+  constexpr int NACC = HM ? NTG * TN / 4 : TN;  // HM: [token group][tile quad]
   Acc acc[NACC];
 #pragma unroll
   for (int t = 0; t < NACC; t++) acc[t] = Acc{};
@@ -433,9 +440,9 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
   // (row m at xl[m * XS + k - kb0], XS = tk_per_wg * 16 + 256 halves: the K range rounded out to
   // whole blocks); every wave takes whole (row, block) pairs
   const int kb0 = (tk0 * 16) & ~127, XS = tk_per_wg * 16 + 256;
-  const uint16_t *xl = (const uint16_t *)(red + (MF ? TN * 256 : KS * TN * 16));
+  const uint16_t *xl = (const uint16_t *)(red + (MF ? TN * 256 : KS * TN * 16 * M));
   if constexpr (ROT) {
-    uint16_t *xw = (uint16_t *)(red + (MF ? TN * 256 : KS * TN * 16));
+    uint16_t *xw = (uint16_t *)(red + (MF ? TN * 256 : KS * TN * 16 * M));
     const int nblk = (min((tk1 * 16 + 127) & ~127, K) - kb0) / 128;
     for (int q = wave; q < M * nblk; q += KS) {
       const int m = q / nblk, b = kb0 + 128 * (q % nblk);
@@ -455,18 +462,25 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
       if (i >= nsteps) break;
       load(i + D - 1, ring[(d + D - 1) % D]);
       Raw &r = ring[d];
-      if constexpr (ROT) {
-        const int xo = tok * XS + 16 * (tk0 + wave + KS * i) - kb0 + 2 * g;
-        r.xa = *(const uint32_t *)(xl + xo);
-        r.xb = *(const uint32_t *)(xl + xo + 8);
-      }
+      if constexpr (ROT)
+#pragma unroll
+        for (int t = 0; t < NX; t++) {
+          const int xo = tok[t] * XS + 16 * (tk0 + wave + KS * i) - kb0 + 2 * g;
+          r.xa[t] = *(const uint32_t *)(xl + xo);
+          r.xb[t] = *(const uint32_t *)(xl + xo + 8);
+        }
       *(u4 *)(stage + 4 * lane) = r.w;  // the wave's own buffer: its LDS operations stay in order
       if constexpr (HM) {
-        // A of MFMA i: x of this lane group's rows, each value twice, on the lanes of row (g + i) % 4
-        const u4 X = {dup_lo(r.xa), dup_hi(r.xa), dup_lo(r.xb), dup_hi(r.xb)};
-        u4 A[4];
+        // A of MFMA i, token group tg: the lane's token's x (rows of lane group g), each value
+        // twice, on the lanes of rows 4 m + (g + i) % 4 of the group's live tokens m
+        u4 A[NTG][4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) A[i] = j < 4 && ((j - g) & 3) == i ? X : u4{0, 0, 0, 0};
+        for (int tg = 0; tg < NTG; tg++) {
+          const u4 X = {dup_lo(r.xa[tg]), dup_hi(r.xa[tg]), dup_lo(r.xb[tg]), dup_hi(r.xb[tg])};
+          const bool on_tok = (j >> 2) + 4 * tg < M;
+#pragma unroll
+          for (int i = 0; i < 4; i++) A[tg][i] = on_tok && (((j & 3) - g) & 3) == i ? X : u4{0, 0, 0, 0};
+        }
 #pragma unroll
         for (int q = 0; q < TN / 4; q++)
 #pragma unroll
@@ -477,7 +491,9 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
                           exl3_halves<CB>(__builtin_amdgcn_ubfe(win, T32::field(1), 16)),
                           exl3_halves<CB>(__builtin_amdgcn_ubfe(win, T32::field(2), 16)),
                           exl3_halves<CB>(__builtin_amdgcn_ubfe(win, T32::field(3), 16))};
-            acc[q] = mfma32(as_h8(A[i]), as_h8(B), acc[q]);
+#pragma unroll
+            for (int tg = 0; tg < NTG; tg++)
+              acc[tg * (TN / 4) + q] = mfma32(as_h8(A[tg][i]), as_h8(B), acc[tg * (TN / 4) + q]);
           }
       } else {
 #pragma unroll
@@ -489,10 +505,10 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
           const uint32_t s3 = __builtin_amdgcn_ubfe(win, T32::field(3), 16);
           const uint32_t b01 = exl3_decode2<CB>(s0, s1), b23 = exl3_decode2<CB>(s2, s3);
           if constexpr (MF) {
-            const u2 A = live ? u2{r.xa, r.xb} : u2{0, 0};
+            const u2 A = live ? u2{r.xa[0], r.xb[0]} : u2{0, 0};
             acc[t] = mfma16(as_h4(A), as_h4(u2{b01, b23}), acc[t]);
           } else {
-            acc[t] = dot2(b23, r.xb, dot2(b01, r.xa, acc[t]));
+            acc[t] = dot2(b23, r.xb[0], dot2(b01, r.xa[0], acc[t]));
           }
         }
       }
@@ -522,13 +538,17 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
       }
     }
   } else {
+    // red[wave][token][tile][column]
     if constexpr (HM) {
-      if (g == 0)
 #pragma unroll
-        for (int q = 0; q < TN / 4; q++)
+      for (int tg = 0; tg < NTG; tg++)
+        if (g + 4 * tg < M)
 #pragma unroll
-          for (int e = 0; e < 4; e++) red[(wave * TN + 4 * q + e) * 16 + j] = acc[q][e];
-    } else {
+          for (int q = 0; q < TN / 4; q++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+              red[((wave * M + g + 4 * tg) * TN + 4 * q + e) * 16 + j] = acc[tg * (TN / 4) + q][e];
+    } else {  // M = 1
 #pragma unroll
       for (int t = 0; t < NACC; t++) {
         float a = acc[t];
@@ -538,10 +558,11 @@ __global__ __launch_bounds__(256) void exl3_mm3(const uint16_t *__restrict__ xh,
       }
     }
     __syncthreads();
-    for (int o = threadIdx.x; o < TN * 16; o += blockDim.x) {
+    for (int o = threadIdx.x; o < M * TN * 16; o += blockDim.x) {
+      const int m = o / (TN * 16), t = (o >> 4) % TN;
       float sum = 0.0f;
-      for (int v = 0; v < KS; v++) sum += red[(v * TN + (o >> 4)) * 16 + (o & 15)];
-      yh[(size_t)blockIdx.y * N + (tn0 + (o >> 4)) * 16 + (o & 15)] = sum;
+      for (int v = 0; v < KS; v++) sum += red[((v * M + m) * TN + t) * 16 + (o & 15)];
+      yh[(size_t)blockIdx.y * M * N + (size_t)m * N + (tn0 + t) * 16 + (o & 15)] = sum;
     }
   }
 }
@@ -708,8 +729,9 @@ extern "C" int ishz_exl3_rotate(const void *x, int in_dtype, int rows, int width
   return ISHZ_OK;
 }
 
-// K splits of the wide-step kernel: about four workgroups per CU for one row, two with MFMA rows
-// (tn_blocks workgroups per split), at most 64.
+// K splits of the wide-step kernel: about four workgroups per CU up to eight rows (the
+// halves-on-MFMA kernel; at 17408 x 5120, 2 bpw, M = 2: 25.1 -> 23.9 us against two), two for the
+// decoded-weight MFMA kernel (tn_blocks workgroups per split), at most 64.
 static int exl3_splits(int M, int K, int tn_blocks);
 // Floats the matvec's K-split parts take at most: the split count of the fewest column blocks (32
 // tiles per step at 1 bit) times M N.
@@ -718,7 +740,7 @@ static size_t exl3_part_floats(int M, int K, int N) {
 }
 static int exl3_splits(int M, int K, int tn_blocks) {
   const int tiles_k = K / 16;
-  return std::max(1, std::min({tiles_k / 4, (M == 1 ? 4 : 2) * num_cu_e() / tn_blocks, 64}));
+  return std::max(1, std::min({tiles_k / 4, (M <= 8 ? 4 : 2) * num_cu_e() / tn_blocks, 64}));
 }
 
 // The matvec into `part` (exl3_part_floats(M, K, N) floats): the wide-step kernel writes each K
@@ -742,13 +764,22 @@ static int exl3_matvec_core(const void *xh, int M, int K, const int16_t *trellis
         const int nsplit = (tiles_k + per - 1) / per;
         float *out = part;
         *nparts = nsplit;
-        const size_t lds = (size_t)KS3 * 256 * 4 + (M == 1 ? (size_t)KS3 * TN * 16 * 4 : (size_t)TN * 256 * 4) +
-                           (suh ? (size_t)M * (per * 16 + 256) * 2 : 0);  // ROT: the rotated K range of x
         auto go = [&]<int CB>() -> int {
-          if (M == 1 && suh)
+          // the halves-on-MFMA kernel for the 3INST / MCG codebooks up to 8 rows, the dot2 kernel
+          // for MUL1 at M = 1, the decoded-weight MFMA kernel otherwise
+          const bool hm = (CB != 2 && M <= 8) || M == 1;
+          const size_t lds = (size_t)KS3 * 256 * 4 + (hm ? (size_t)KS3 * TN * 16 * 4 * M : (size_t)TN * 256 * 4) +
+                             (suh ? (size_t)M * (per * 16 + 256) * 2 : 0);  // ROT: the rotated K range of x
+          if (hm && M > 4 && suh)
+            hipLaunchKernelGGL((exl3_mm3<KA, CB, false, D1, true, 2>), dim3(tn_blocks, nsplit), dim3(64 * KS3), lds, st,
+                               (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per, suh);
+          else if (hm && M > 4)
+            hipLaunchKernelGGL((exl3_mm3<KA, CB, false, D1, false, 2>), dim3(tn_blocks, nsplit), dim3(64 * KS3), lds, st,
+                               (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per);
+          else if (hm && suh)
             hipLaunchKernelGGL((exl3_mm3<KA, CB, false, D1, true>), dim3(tn_blocks, nsplit), dim3(64 * KS3), lds, st,
                                (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per, suh);
-          else if (M == 1)
+          else if (hm)
             hipLaunchKernelGGL((exl3_mm3<KA, CB, false, D1>), dim3(tn_blocks, nsplit), dim3(64 * KS3), lds, st,
                                (const uint16_t *)xh, M, K, (const uint32_t *)trellis, N, out, per);
           else if (suh)
@@ -866,11 +897,12 @@ static bool exl3_fused_rotation(int M, int K, int N, int bits2) {
   const int KA = bits2 / 2;
   // up to two rows: every workgroup rotates its K range of every row, which measured faster than
   // the separate rotation launch at M = 1 and 2 (17408x5120: 32.7 vs 33.7 us at M = 2), even at 4
-  // and slower at 8 (38.0 vs 35.3)
+  // and slower at 8 (38.0 vs 35.3); with the halves-on-MFMA kernel, even at 4 (27.5-27.7 vs
+  // 27.8) and slower at 8 (34.6-34.8 vs 33.5-33.7)
   if (M > 2 || !(bits2 == 2 || bits2 == 4 || bits2 == 8) || (N / 16) % (32 / KA)) return false;
   const int TN = 32 / KA, tiles_k = K / 16, splits = exl3_splits(M, K, N / 16 / TN);
   const size_t per = (tiles_k + splits - 1) / splits;
-  const size_t own = 4 * 256 * 4 + (M == 1 ? (size_t)4 * TN * 16 * 4 : (size_t)TN * 256 * 4);
+  const size_t own = 4 * 256 * 4 + std::max((size_t)4 * TN * 16 * 4 * M, (size_t)TN * 256 * 4);
   return own + (size_t)M * (per * 16 + 256) * 2 <= 120 * 1024;
 }
 
