@@ -22,7 +22,7 @@
 
 namespace ishz {
 // hadamardRotate as a kernel. Blocks up to 128: one wave per 128 contiguous values, two per
-// lane, butterflies across lanes by shuffles (stages above the block size skipped). Larger
+// lane, butterflies across lanes by DPP and row swaps (stages above the block size skipped). Larger
 // blocks: one workgroup per block, in LDS. fp32 math, output in `out_dt`.
 __global__ __launch_bounds__(256) void hadamard_wave_kernel(const void *__restrict__ x, int in_dt,
                                                             size_t chunks, int width, int block,
@@ -44,12 +44,19 @@ __global__ __launch_bounds__(256) void hadamard_wave_kernel(const void *__restri
     v0 = a;
     v1 = b;
   }
-  for (int m = 1; 2 * m < block; m <<= 1) {
-    const float p0 = __shfl_xor(v0, m, 64), p1 = __shfl_xor(v1, m, 64);
-    const bool hi = (lane & m) != 0;
-    v0 = hi ? p0 - v0 : v0 + p0;
-    v1 = hi ? p1 - v1 : v1 + p1;
-  }
+  // partner lane ^ m by DPP inside 16-lane rows, by the row swaps across them; the lower lane keeps
+  // v + p, the upper p - v, as fma(v, +-1, p) (exact, the same rounding)
+  auto stage = [&](float p0, float p1, int m) {
+    const float s = (lane & m) ? -1.0f : 1.0f;
+    v0 = __builtin_fmaf(v0, s, p0);
+    v1 = __builtin_fmaf(v1, s, p1);
+  };
+  if (block > 2) stage(ISHZ_DPP(v0, 0xB1), ISHZ_DPP(v1, 0xB1), 1);
+  if (block > 4) stage(ISHZ_DPP(v0, 0x4E), ISHZ_DPP(v1, 0x4E), 2);
+  if (block > 8) stage(ISHZ_DPP(ISHZ_DPP(v0, 0x141), 0x1B), ISHZ_DPP(ISHZ_DPP(v1, 0x141), 0x1B), 4);
+  if (block > 16) stage(ISHZ_DPP(ISHZ_DPP(v0, 0x141), 0x140), ISHZ_DPP(ISHZ_DPP(v1, 0x141), 0x140), 8);
+  if (block > 32) stage(lane_xor16(v0), lane_xor16(v1), 16);
+  if (block > 64) stage(lane_xor32(v0), lane_xor32(v1), 32);
   const float scale = 1.0f / __builtin_sqrtf((float)block);
   v0 *= scale;
   v1 *= scale;

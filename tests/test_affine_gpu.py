@@ -24,7 +24,7 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
 
-@pytest.mark.parametrize("block", [2, 32, 128, 512, 4096])
+@pytest.mark.parametrize("block", [2, 8, 32, 64, 128, 512, 4096])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_hadamard_fp32(block, inverse):
     x = np.random.default_rng(block).standard_normal((3, 8192)).astype(np.float32)
