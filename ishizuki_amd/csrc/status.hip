@@ -29,9 +29,25 @@ __global__ __launch_bounds__(256) void act_half_kernel(const void *__restrict__ 
                                                        uint16_t *__restrict__ xh, float *__restrict__ rs) {
   __shared__ float wmax[4];
   const size_t row = (size_t)blockIdx.x * K;
+  // eight loads in flight per thread and pass (one at a time waited out a memory latency each)
+  constexpr int U = 8;
   float m = 0.0f;
-  for (int k = threadIdx.x; k < K; k += blockDim.x) m = fmaxf(m, fabsf(load_act(x, row + k, dt)));
-  for (int o = 32; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  for (int k0 = threadIdx.x; k0 < K; k0 += U * blockDim.x) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int k = k0 + u * (int)blockDim.x;
+      v[u] = k < K ? fabsf(load_act(x, row + k, dt)) : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) m = fmaxf(m, v[u]);
+  }
+  m = fmaxf(m, ISHZ_DPP(m, 0xB1));   // the wave's max: quad, half-row and row by DPP,
+  m = fmaxf(m, ISHZ_DPP(m, 0x4E));
+  m = fmaxf(m, ISHZ_DPP(m, 0x141));
+  m = fmaxf(m, ISHZ_DPP(m, 0x140));
+  m = fmaxf(m, lane_xor16(m));       // across rows by the row swaps
+  m = fmaxf(m, lane_xor32(m));
   if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
   __syncthreads();
   m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
@@ -43,7 +59,19 @@ __global__ __launch_bounds__(256) void act_half_kernel(const void *__restrict__ 
     e = e > 127 ? 127 : e;
   }
   const float down = ldexpf(1.0f, -e);
-  for (int k = threadIdx.x; k < K; k += blockDim.x) xh[row + k] = f2h(load_act(x, row + k, dt) * down);
+  for (int k0 = threadIdx.x; k0 < K; k0 += U * blockDim.x) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int k = k0 + u * (int)blockDim.x;
+      v[u] = k < K ? load_act(x, row + k, dt) : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int k = k0 + u * (int)blockDim.x;
+      if (k < K) xh[row + k] = f2h(v[u] * down);
+    }
+  }
   if (threadIdx.x == 0) rs[blockIdx.x] = ldexpf(1.0f, e);
 }
 
