@@ -273,13 +273,6 @@ struct FAffine {
     stage_group(a, xs, xsum, wave, nw, pre);  // first group: loads issued by stage_load
     for (int c0 = wave + PF * nw; c0 < npass; c0 += PF * nw)
       stage_group(a, xs, xsum, c0, nw, load_group(a, x, c0, nw));
-#ifdef ISHZ_TIMING_ISSUE
-    {
-      uint64_t t;
-      asm volatile("s_memrealtime %0\n s_waitcnt lgkmcnt(0)" : "=s"(t)::"memory");
-      if (lane == 0) ishz_timing2[blockIdx.x * nw + wave] = t;
-    }
-#endif
     __syncthreads();
   }
 

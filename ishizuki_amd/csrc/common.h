@@ -171,9 +171,6 @@ struct Out {
 // (100 MHz) at a kernel's phase boundaries, for a timeline of its phases; read back from the host
 // with hipMemcpyFromSymbol.
 __device__ uint64_t ishz_timing[4096 * 5];
-#ifdef ISHZ_TIMING_ISSUE
-__device__ uint64_t ishz_timing2[4096];
-#endif
 #endif
 
 // ---------------------------------------------------------------- MFMA

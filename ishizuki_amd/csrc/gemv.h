@@ -190,9 +190,6 @@ __global__ __launch_bounds__((gemv_threads<F, LPR, BIG>())) void gemv_kernel(typ
     advance(gl, kl);
   }
 
-#ifdef ISHZ_TIMING_ISSUE
-  asm volatile("s_memrealtime %0\n s_waitcnt lgkmcnt(0)" : "=s"(ts[1])::"memory");
-#endif
   // after the first loads are out (visible after staging's barrier)
   for (int i = threadIdx.x; i < WPG * nrows; i += WPG * 64) part[i] = 0.0f;
   int im0 = 0;  // first x image of this workgroup's rows
@@ -205,12 +202,7 @@ __global__ __launch_bounds__((gemv_threads<F, LPR, BIG>())) void gemv_kernel(typ
     F::stage(args, x, xs, xsum, extra, units, pre);  // ends with a barrier
   }
 #ifdef ISHZ_TIMING
-#ifdef ISHZ_TIMING_ISSUE
-  asm volatile("s_memrealtime %0\n s_waitcnt lgkmcnt(0)" : "=s"(ts[3])::"memory");
-  ts[2] = ishz_timing2[blockIdx.x * WPG + wave];
-#else
   ts[1] = ts[2] = ts[3] = __builtin_amdgcn_s_memrealtime();
-#endif
 #endif
   const uint32_t mg = vconst(0x64006400u);
   const u4 *grid = extra, *sgn = extra + F::GRID_ENTRIES;
