@@ -66,7 +66,7 @@ def test_dequant_random_rates(bits2, cb):
     assert bits_equal(w, oracle.exl3_dequant(t, bits2, cb))
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 8, 16])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 7, 8, 16])
 @pytest.mark.parametrize("bits2,cb", [(4, 0), (4, 2), (3, 2), (6, 1), (2, 0), (2, 2), (8, 1), (10, 0)])
 def test_matvec(M, bits2, cb):
     K, N = 1024, 512
