@@ -166,7 +166,11 @@ int ishz_exl3_rotate(const void *x, int in_dtype, int rows, int width, const uin
    launches). The K-split partial products are summed in split order: the same bits on every
    call. ishz_exl3_matvec_ws takes them (and bf16 x's fp16 image) in a caller workspace of
    ishz_exl3_matvec_workspace_size(M, K, N) bytes and allocates nothing; ishz_exl3_matvec is the
-   same call with stream-ordered temporaries (hipMallocAsync) instead. fp32 x needs neither. */
+   same call with stream-ordered temporaries (hipMallocAsync) instead. fp32 x needs neither.
+   fp16 / bf16 x with the 3INST and MCG codebooks, up to 8 rows: each weight's two fp16 halves
+   (its codebook image before their final add) meet x in fp32, so the weight's own fp16 rounding
+   is skipped (at most half an fp16 ulp per weight); MUL1 and more rows multiply the decoded fp16
+   weight. fp32 x multiplies the exactly decoded weight. */
 size_t ishz_exl3_matvec_workspace_size(int M, int K, int N);
 int ishz_exl3_matvec_ws(const void *xh, int x_dtype, int M, int K, const int16_t *trellis, int N,
                         int bits2, int codebook, float *yh, void *workspace, size_t workspace_bytes,
