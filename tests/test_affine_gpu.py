@@ -256,6 +256,23 @@ def test_affine_rotated_verify(M, block, K, prestage):
     assert_close(y.float().cpu().numpy(), ref, bound=bd, what=f"verify M={M} block={block} K={K} prestage={prestage}")
 
 
+@pytest.mark.parametrize("N,K,M,group", [(4352, 5120, 8, 64), (4352, 1024, 4, 64), (8320, 2304, 3, 128),
+                                         (8320, 5120, 16, 64), (4100, 5120, 8, 64)])
+def test_affine_verify_leftover_tiles(N, K, M, group):
+    """More 16-row tiles than CUs but not a whole number per CU (4352 rows: 272 tiles on 256 CUs;
+    4100 rows: a last tile of 4 rows), with x prestaged: several tiles per workgroup, uneven
+    counts, group 128, and (M = 16 at K = 5120) x staged in K chunks. Two calls in a row give the
+    same bits."""
+    print(f"affine leftover N={N} K={K} M={M} g={group}", flush=True)
+    (x, w, s, b), signs, (ref, bd) = affine_case(N, K, M, group, seed=N + K + M, block=128, signs_seed=9)
+    sg = torch.from_numpy(signs)
+    y1 = affine.linear(x, w, s, b, signs=sg, block=128, group_size=group)
+    y2 = affine.linear(x, w, s, b, signs=sg, block=128, group_size=group)
+    assert y1 is not None and y2 is not None
+    assert_close(y1.float().cpu().numpy(), ref, bound=bd, what=f"leftover N={N} K={K} M={M}")
+    assert torch.equal(y1, y2)
+
+
 def test_affine_bf16_scales():
     N, K = 300, 1024
     codes, s, b = synth.affine_pack(N, K, group=64, seed=3)
